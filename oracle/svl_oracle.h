@@ -1,0 +1,110 @@
+/*
+ * CPU oracle for the EmbeddingGemma-2 text encoder forward pass.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker that the HIP path is
+ * compared against; it is never linked into, loaded by, or called from the
+ * product library. Only tests, the smoke check and the CPU-baseline leg of
+ * bench.py load it.
+ *
+ * Every function restates one scalar function of the reference crate
+ * (src/tensor/kernels.rs, src/model/text.rs, src/model/config.rs) with the
+ * same loop order, the same f32 evaluation order and no FMA contraction
+ * (compiled with -ffp-contract=off), using the platform libm for
+ * expf/tanhf/sinf/cosf/powf/sqrtf as the reference does on Linux.
+ *
+ * Status codes mirror src/error.rs:24-37.
+ */
+#ifndef SVL_ORACLE_H
+#define SVL_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    SVLO_OK = 0,
+    SVLO_USAGE = 2,
+    SVLO_IO = 3,
+    SVLO_CORRUPT = 4,
+    SVLO_LIMIT = 5,
+    SVLO_UNSUPPORTED = 6,
+    SVLO_INTERNAL = 7
+};
+
+/* kernels.rs scalar functions (device-free, caller-owned buffers). */
+float svlo_dot(const float *a, const float *b, size_t n);
+int svlo_add(const float *a, const float *b, size_t n, float *out);
+int svlo_linear(const float *input, const float *weight, size_t rows, size_t in_features,
+                size_t out_features, float *out);
+int svlo_matmul(const float *left, const float *right, size_t m, size_t k, size_t n, float *out);
+int svlo_rms_norm_rows(const float *input, const float *weight, size_t rows, size_t width,
+                       float eps, float *out);
+int svlo_rms_norm_rows_unscaled(const float *input, size_t rows, size_t width, float eps,
+                                float *out);
+int svlo_softmax(const float *values, size_t n, float *out);
+float svlo_gelu_tanh_value(float v);
+void svlo_gelu_tanh(const float *values, size_t n, float *out);
+int svlo_geglu(const float *gate, const float *up, size_t n, float *out);
+int svlo_l2_normalize(const float *input, size_t n, float *out);
+int svlo_mean_pool(const float *values, size_t rows, size_t width, float *out);
+int svlo_truncate_and_normalize(const float *values, size_t n, size_t dim, float *out);
+int svlo_rope_inv_freq(size_t head_dim, float base, float *out);
+int svlo_rope_with_inv_freq(float *values, size_t seq_len, size_t num_heads, size_t head_dim,
+                            const float *inv_freq, size_t n_inv_freq, size_t position_offset);
+/* sliding_window < 0 means full attention. */
+int svlo_bidirectional_attention(const float *q, const float *k, const float *v, size_t seq_len,
+                                 size_t num_heads, size_t num_kv_heads, size_t head_dim,
+                                 int64_t sliding_window, float scale, float *out);
+
+/* Validated text configuration (src/model/config.rs:76-95). */
+typedef struct {
+    int64_t vocab_size;
+    int64_t hidden_size;
+    int64_t intermediate_size;
+    int64_t num_hidden_layers;
+    int64_t num_attention_heads;
+    int64_t hidden_size_per_layer_input;
+    int64_t embedding_dim;
+    int64_t max_position_embeddings;
+    int64_t sliding_window;
+    int64_t pad_token_id; /* -1 when absent */
+    float rms_norm_eps;
+    float full_rope_theta;
+    float sliding_rope_theta;
+    const int32_t *layer_type; /* [layers], 0 = sliding, 1 = full */
+    const int64_t *head_dim;   /* [layers] */
+    const int64_t *num_kv_heads; /* [layers] */
+} svlo_text_config;
+
+/*
+ * Weights in the order of TextConfig::tensor_shapes (config.rs:394-484):
+ * [0] embed_tokens, [1] embedding_projection, [2] norm,
+ * [3] ple.per_layer_model_projection, [4] ple.per_layer_projection_norm,
+ * then 17 per layer: input_layernorm, post_attention_layernorm,
+ * pre_feedforward_layernorm, post_feedforward_layernorm, layer_scalar,
+ * gate_proj, up_proj, down_proj, per_layer_input_gate, per_layer_projection,
+ * post_per_layer_input_norm, q_proj, k_proj, v_proj, o_proj, q_norm, k_norm.
+ */
+#define SVLO_GLOBAL_TENSORS 5
+#define SVLO_LAYER_TENSORS 17
+
+/*
+ * TextModel::forward_impl (text.rs:182-538). features may be NULL.
+ * out_projected [seq, embedding_dim], out_pooled and out_normalized
+ * [embedding_dim] are required; out_hidden [(layers+1), seq, hidden] is
+ * optional. msg (optional, msg_len bytes) receives the error text.
+ */
+int svlo_text_forward(const svlo_text_config *cfg, const float *const *weights,
+                      const uint32_t *ids, size_t seq, const float *features,
+                      size_t feature_start, size_t feature_count, size_t features_len,
+                      float *out_projected, float *out_pooled, float *out_normalized,
+                      float *out_hidden, char *msg, size_t msg_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
