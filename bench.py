@@ -1,0 +1,201 @@
+"""Throughput benchmark of the MI355X text encoder.
+
+Workload (one "step" = one forward pass of one batch): the EmbeddingGemma-
+shaped FP32 text encoder (hidden 768, 24 layers, 3 query heads sharing one
+KV head of dim 256, GeGLU FFN 1152, PLE 256, vocab 262144) with random-init
+weights (seed 0), batch 64 rows, row lengths uniform in [64, 512] (seed 1),
+token ids uniform over the vocabulary (seed 1), padding masked by packing
+the rows back to back, outputs at Matryoshka dims 768 / 512 / 256 / 128.
+Token ids are resident in HBM before the timed region; every step runs the
+whole encoder and writes the normalised embeddings to HBM.
+
+Prints one JSON line: embeddings/s (value), the roofline of the dominant
+kernel (the gate/up GEMM, measured with HIP events on the stream it runs
+on), and the CPU oracle timed on this host's cores on a bounded sample.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "seldon-vault-lite-rust_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "text embeddings/sec at batch 64×seq 512 FP32; % FP32-MFMA peak; p50 latency"
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X published dense FP32 matrix peak
+PEAK_HBM_GBS = 8000.0
+BATCH, LEN_LO, LEN_HI = 64, 64, 512
+DIMS = [768, 512, 256, 128]
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-sample-rows", type=int, default=-1,
+                    help="rows of the workload timed on the CPU oracle (default: one per core, "
+                         "at most 16; 0 skips the CPU baseline)")
+    ap.add_argument("--t1-runs", type=int, default=20)
+    return ap.parse_args()
+
+
+def gemm_traffic():
+    """HBM bytes per launch of the gate/up GEMM from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor),
+    or None when no such measurement is committed."""
+    path = os.path.join(ROOT, "profiles", "gemm_gate_up_T2_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(cfg, weights, rows_all, n_rows):
+    from oracle import oracle as O
+    import numpy as np
+
+    if n_rows == 0:
+        return None
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    n = n_rows if n_rows > 0 else max(1, min(cores, 16))
+    rows = rows_all[:n]
+    model = O.OracleTextModel(cfg, weights)
+    t0 = time.perf_counter()
+    outs = model.forward_rows(rows, threads=n)
+    wall = time.perf_counter() - t0
+    assert all(np.isfinite(o["normalized"]).all() for o in outs)
+    toks = sum(len(r) for r in rows)
+    return {"value": n / wall, "unit": "embeddings/s", "cores": n, "kind": "port",
+            "sample": f"first {n} rows of the same batch ({toks} tokens, lengths "
+                      f"{min(len(r) for r in rows)}-{max(len(r) for r in rows)}), one row per "
+                      f"thread, scalar C oracle (-O2, no FMA contraction), {wall:.1f} s wall"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(rows are independent and would shard by data parallelism, see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import svl_amd
+    import svl_synth
+
+    torch.cuda.set_device(0)
+    dev = svl_amd.Device.get(0)
+    cfg = svl_synth.config_a()
+    weights = svl_synth.weights(cfg, seed=0)
+    lengths = svl_synth.row_lengths(BATCH, LEN_LO, LEN_HI, seed=1)
+    rows = svl_synth.token_rows(cfg["vocab_size"], lengths, seed=1)
+    model = svl_amd.TextModel(svl_amd.TextConfig.from_json_value(cfg), weights, dev)
+
+    offsets = np.zeros(BATCH + 1, np.int64)
+    offsets[1:] = np.cumsum(lengths)
+    T = int(offsets[-1])
+    ids = torch.from_numpy(np.concatenate(rows).astype(np.int32)).to("cuda:0")
+    out = torch.zeros((BATCH, sum(DIMS)), dtype=torch.float32, device="cuda:0")
+    stream = torch.cuda.current_stream()
+
+    def step():
+        model.forward_device(ids.data_ptr(), offsets, DIMS, out.data_ptr(), stream.cuda_stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: K steps, per-kernel HIP events recorded on the same stream.
+    model.set_kernel_timing(True)
+    step_ms = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        a = time.perf_counter()
+        step()
+        step_ms.append((time.perf_counter() - a) * 1e3)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    stats = model.kernel_stats()
+    model.set_kernel_timing(False)
+
+    value = BATCH * args.steps / elapsed
+    ms_per_step = elapsed * 1e3 / args.steps
+    p50 = float(np.median(step_ms))
+
+    # Dominant kernel: the fused gate/up GEMM with GeGLU epilogue.
+    gu = stats["gemm_gate_up"]
+    gu_ms = gu["ms"] / max(gu["launches"], 1)
+    gu_flops = gu["work"] / max(gu["launches"], 1)
+    gu_tflops = gu_flops / (gu_ms * 1e-3) / 1e12
+    gemm_keys = [k for k in stats if k.startswith("gemm_")]
+    gemm_ms = sum(stats[k]["ms"] for k in gemm_keys)
+    gemm_flops = sum(stats[k]["work"] for k in gemm_keys)
+    gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else 0.0
+    attn = stats["attention"]
+    attn_tflops = attn["work"] / (attn["ms"] * 1e-3) / 1e12 if attn["ms"] else 0.0
+    fwd_flops = (gemm_flops + attn["work"]) / args.steps
+    total_kernel_ms = sum(v["ms"] for v in stats.values()) / args.steps
+
+    # T1 latency: batch 1 x 128 tokens.
+    t1_ids = torch.from_numpy(svl_synth.token_rows(cfg["vocab_size"], [128], seed=1)[0]
+                              .astype(np.int32)).to("cuda:0")
+    t1_off = np.array([0, 128], np.int64)
+    t1_out = torch.zeros((1, 768), dtype=torch.float32, device="cuda:0")
+    lat = []
+    for i in range(args.t1_runs + 2):
+        a = time.perf_counter()
+        model.forward_device(t1_ids.data_ptr(), t1_off, [768], t1_out.data_ptr(), stream.cuda_stream)
+        if i >= 2:
+            lat.append((time.perf_counter() - a) * 1e3)
+
+    traffic = gemm_traffic()
+    roofline = {"kernel": "gemm_nt_mfma<128,128,EPI_GEGLU> (gate/up projection + GeGLU)",
+                "bound": "mfma", "achieved": round(gu_tflops, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(gu_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+                "traffic": traffic,
+                "flops_per_launch": gu_flops, "avg_launch_ms": round(gu_ms, 4),
+                "launches": gu["launches"]}
+
+    cpu = cpu_baseline(cfg, weights, rows, args.cpu_sample_rows)
+
+    breakdown = {k: {"ms_per_step": round(v["ms"] / args.steps, 3),
+                     "launches_per_step": v["launches"] // max(args.steps, 1)}
+                 for k, v in stats.items() if v["launches"]}
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "embeddings/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (random-init weights seed 0, token ids and row lengths seed 1)",
+        "config": {"workload": "EmbeddingGemma-shaped FP32 text encoder forward (hidden 768, 24 "
+                               "layers, 3 q heads / 1 KV head, head_dim 256, GeGLU 1152, PLE 256, "
+                               "vocab 262144): batch 64 rows, lengths U[64,512], padding masked, "
+                               "Matryoshka outputs 768/512/256/128",
+                   "batch": BATCH, "tokens": T, "max_seq_len": LEN_HI, "parallelism": "single GPU"},
+        "p50_ms": round(p50, 3),
+        "t1_p50_ms": round(float(np.median(lat)), 3),
+        "gemm_tflops": round(gemm_tflops, 3),
+        "gemm_frac_of_fp32_mfma_peak": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+        "attention_tflops": round(attn_tflops, 3),
+        "forward_tflops": round(fwd_flops / (ms_per_step * 1e-3) / 1e12, 3),
+        "forward_frac_of_fp32_mfma_peak": round(fwd_flops / (ms_per_step * 1e-3) / 1e12
+                                                / PEAK_FP32_MFMA_TFLOPS, 4),
+        "kernel_ms_per_step": round(total_kernel_ms, 3),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": breakdown,
+    }
+    if cpu:
+        line["speedup_vs_cpu_baseline"] = round(value / cpu["value"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

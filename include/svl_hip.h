@@ -1,0 +1,213 @@
+/*
+ * svl_hip.h — C ABI of the MI355X (gfx950) encoder backend.
+ *
+ * The boundary sits at the whole text forward pass: weights stay resident in
+ * HBM, token ids and row offsets go in, pooled / normalised embeddings come
+ * out. It replaces the body of TextModel::forward_impl
+ * (src/model/text.rs:182-538) behind the unchanged TextModel / TextEmbedder
+ * API, the way src/tensor/neon.rs sits behind src/tensor/kernels.rs.
+ *
+ * A second group of entry points mirrors the kernel seam of
+ * src/tensor/kernels.rs on device pointers, so each kernel can be checked on
+ * its own against the reference's known answers.
+ *
+ * Conventions:
+ *  - Status codes mirror src/error.rs:24-37 (Usage, Io, Corrupt,
+ *    LimitExceeded, Unsupported, Internal) plus SVL_DEVICE for HIP failures.
+ *  - The caller owns every buffer it passes; the library never retains a
+ *    caller pointer past the call. The library owns device weights and
+ *    workspaces.
+ *  - svl_last_error() returns the calling thread's last message.
+ *  - A model may be called from several threads; calls are serialised per
+ *    model, and repeated calls are bit-identical (fixed reduction orders,
+ *    no floating-point atomics).
+ *  - Streams are passed as void* (a hipStream_t); NULL selects the model's
+ *    own stream (model entry points) or the null stream (kernel seam).
+ */
+#ifndef SVL_HIP_H
+#define SVL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* src/error.rs:24-37 */
+typedef enum {
+    SVL_OK = 0,
+    SVL_USAGE = 2,
+    SVL_IO = 3,
+    SVL_CORRUPT = 4,
+    SVL_LIMIT = 5,
+    SVL_UNSUPPORTED = 6,
+    SVL_INTERNAL = 7,
+    SVL_DEVICE = 8
+} svl_status;
+
+/* src/tensor/dtype.rs:11-57 (FP16 is rejected as in the reference). */
+typedef enum { SVL_F32 = 0, SVL_BF16 = 1 } svl_dtype;
+
+typedef struct svl_ctx svl_ctx;
+typedef struct svl_text_model svl_text_model;
+
+/* One named weight tensor, borrowed for the duration of the call
+ * (src/binary/safetensors.rs:69-110 TensorEntry). */
+typedef struct {
+    const char *name;
+    int32_t dtype; /* svl_dtype */
+    int32_t ndim;
+    int64_t shape[8];
+    const void *data; /* host memory, little-endian */
+} svl_tensor_view;
+
+/* Validated text configuration (src/model/config.rs:76-95 TextConfig and
+ * :64-72 LayerConfig). Arrays have num_hidden_layers entries. */
+typedef struct {
+    int64_t vocab_size;
+    int64_t hidden_size;
+    int64_t intermediate_size;
+    int64_t num_hidden_layers;
+    int64_t num_attention_heads;
+    int64_t hidden_size_per_layer_input;
+    int64_t embedding_dim;
+    int64_t max_position_embeddings;
+    int64_t sliding_window;
+    int64_t pad_token_id; /* -1 when the config declares none */
+    double rms_norm_eps;
+    double full_rope_theta;
+    double sliding_rope_theta;
+    const int32_t *layer_type; /* 0 = sliding_attention, 1 = full_attention */
+    const int64_t *head_dim;
+    const int64_t *num_kv_heads;
+} svl_text_config;
+
+/* Multimodal soft tokens for one row (text.rs:167-180, 226-275):
+ * rows [start, start + count) of that row's hidden state are replaced by
+ * data[count, hidden_size]. data == NULL means no replacement. */
+typedef struct {
+    const float *data;
+    int64_t start;
+    int64_t count;
+    int64_t len; /* number of floats in data */
+} svl_feature_span;
+
+/* ---- context and model lifetime ------------------------------------------ */
+
+/* Selects one HIP device; gfx950 only. */
+svl_status svl_init(int device_ordinal, svl_ctx **out);
+svl_status svl_shutdown(svl_ctx *ctx);
+/* Thread-local message of the last failing call on this thread. */
+const char *svl_last_error(void);
+
+/* Validates the inventory like src/model/weights.rs:125-189 (missing,
+ * unexpected or mis-shaped tensors -> CORRUPT, non-finite -> CORRUPT, BF16
+ * widened exactly), copies the weights to HBM in the backend's packed
+ * layouts, and returns a model. Replaces TextModel::new / from_files
+ * (text.rs:104-126). */
+svl_status svl_text_model_create(svl_ctx *ctx, const svl_text_config *cfg,
+                                 const svl_tensor_view *tensors, size_t n_tensors,
+                                 svl_text_model **out);
+svl_status svl_text_model_destroy(svl_text_model *model);
+
+/* ---- whole forward pass -------------------------------------------------- */
+
+/* Runs `batch` independent forward passes (text.rs:150-180, 182-538), one
+ * per row; row r is ids[offsets[r] .. offsets[r+1]). Row r of every output
+ * equals TextModel::forward(row r). Host buffers.
+ *  features        NULL or [batch] spans (forward_with_features)
+ *  out_normalized  [batch, embedding_dim]   (ForwardOutput::normalized)
+ *  out_pooled      NULL or [batch, embedding_dim]   (::pooled)
+ *  out_projected   NULL or [total_tokens, embedding_dim] (::projected)
+ *  out_hidden      NULL or [num_hidden_layers + 1, total_tokens, hidden]
+ *                  (::hidden_states, capture_hidden = true)
+ * Validation order per row follows text.rs:188-218: empty -> CORRUPT,
+ * > 8192 or > max_position_embeddings -> LIMIT, id >= vocab -> CORRUPT; a
+ * non-finite intermediate -> INTERNAL. */
+svl_status svl_text_forward_batch(svl_text_model *model, const uint32_t *ids,
+                                  const int64_t *offsets, int32_t batch,
+                                  const svl_feature_span *features, float *out_normalized,
+                                  float *out_pooled, float *out_projected, float *out_hidden);
+
+/* Device-resident variant for serving loops: d_ids already in HBM, row
+ * offsets on the host, Matryoshka outputs written to HBM as
+ * d_out[batch, sum(dims)] (each block = truncate_and_normalize(normalized,
+ * dims[i]), kernels.rs:916-927; dims[i] == embedding_dim gives normalized).
+ * Enqueued on `stream` (NULL = the model's stream); the call returns after
+ * the stream has drained and the device error flags have been read. */
+svl_status svl_text_forward_device(svl_text_model *model, const uint32_t *d_ids,
+                                   const int64_t *offsets, int32_t batch, const int32_t *dims,
+                                   int32_t n_dims, float *d_out, void *stream);
+
+/* TextModel::embed_ids (text.rs:546-554): one row, Matryoshka dimension. */
+svl_status svl_text_embed_ids(svl_text_model *model, const uint32_t *ids, int64_t n,
+                              int64_t dimension, float *out);
+
+/* ForwardOutput::embedding / kernels::truncate_and_normalize
+ * (text.rs:72-74, kernels.rs:916-927); host buffers. */
+svl_status svl_truncate_and_normalize(const float *values, size_t n, size_t dimension,
+                                      float *out);
+
+/* Per-kernel GPU time of the last forward call, when enabled: one entry per
+ * kernel class (see svl_kernel_class_name). Used by the benchmark to relate
+ * a kernel's algorithmic work to its measured duration. */
+svl_status svl_text_model_set_kernel_timing(svl_text_model *model, int enable);
+int32_t svl_kernel_class_count(void);
+const char *svl_kernel_class_name(int32_t cls);
+/* ms[cls] = summed milliseconds, launches[cls] = number of launches and
+ * flops[cls] = algorithmic FLOPs (GEMMs, attention) or bytes (bandwidth
+ * kernels) accumulated since timing was enabled. */
+svl_status svl_text_model_kernel_stats(svl_text_model *model, double *ms, int64_t *launches,
+                                       double *work);
+
+/* ---- kernel seam: src/tensor/kernels.rs on device pointers --------------- */
+/* Each call validates like its reference function, runs on `stream`, waits
+ * for it, and returns INTERNAL if the output holds a non-finite value where
+ * the reference checks for one. */
+
+/* kernels.rs:577-685 linear: out[r, c] = sum_k in[r, k] * w[c, k]. */
+svl_status svl_linear(const float *d_in, const float *d_w, int64_t rows, int64_t in_features,
+                      int64_t out_features, float *d_out, void *stream);
+/* kernels.rs:727-776 rms_norm_rows; d_weight == NULL gives
+ * rms_norm_rows_unscaled (kernels.rs:810-857). */
+svl_status svl_rms_norm_rows(const float *d_in, const float *d_weight, int64_t rows,
+                             int64_t width, float eps, float *d_out, void *stream);
+/* kernels.rs:936-988 rope_with_inv_freq on [seq, heads, head_dim], in place;
+ * inv_freq is a host array of head_dim / 2 values. */
+svl_status svl_rope_with_inv_freq(float *d_values, int64_t seq_len, int64_t num_heads,
+                                  int64_t head_dim, const float *inv_freq, int64_t n_inv_freq,
+                                  int64_t position_offset, void *stream);
+/* kernels.rs:991-1010 rope_inv_freq (host). */
+svl_status svl_rope_inv_freq(int64_t head_dim, float base, float *out);
+/* kernels.rs:1037-1135 bidirectional_attention; sliding_window < 0 = full. */
+svl_status svl_bidirectional_attention(const float *d_q, const float *d_k, const float *d_v,
+                                       int64_t seq_len, int64_t num_heads,
+                                       int64_t num_kv_heads, int64_t head_dim,
+                                       int64_t sliding_window, float scale, float *d_out,
+                                       void *stream);
+/* kernels.rs:386-400 gelu_tanh / geglu, kernels.rs:44-52 add. */
+svl_status svl_gelu_tanh(const float *d_in, int64_t n, float *d_out, void *stream);
+svl_status svl_geglu(const float *d_gate, const float *d_up, int64_t n, float *d_out,
+                     void *stream);
+svl_status svl_add(const float *d_a, const float *d_b, int64_t n, float *d_out, void *stream);
+/* kernels.rs:882-909 mean_pool and kernels.rs:414-444 l2_normalize. */
+svl_status svl_mean_pool(const float *d_values, int64_t rows, int64_t width, float *d_out,
+                         void *stream);
+svl_status svl_l2_normalize(const float *d_in, int64_t n, float *d_out, void *stream);
+
+/* ---- deterministic synthetic data (benchmark and tests) ------------------ */
+/* Counter-based SplitMix64: element i of stream s under seed k is
+ * u = (splitmix64(k ^ (s * 0x9E3779B97F4A7C15) + i) >> 40) / 2^24 in [0, 1),
+ * scaled to [lo, hi). Host buffers; multithreaded. */
+void svl_synth_uniform(uint64_t seed, uint64_t stream, float lo, float hi, size_t n, float *out);
+/* floor(u * vocab) token ids and lo + floor(u * (hi - lo + 1)) lengths. */
+void svl_synth_ids(uint64_t seed, uint64_t stream, uint32_t vocab, size_t n, uint32_t *out);
+void svl_synth_lengths(uint64_t seed, uint64_t stream, int64_t lo, int64_t hi, size_t n,
+                       int64_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SVL_HIP_H */

@@ -1,0 +1,119 @@
+// Internal declarations shared by the host runtime (text_model.cpp, api.cpp)
+// and the device translation unit (svl_device.hip). Kernel launchers take
+// device pointers and a stream and return the launch status.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+namespace svl {
+
+// Device error flag bits (one int per model, read after every forward).
+enum : int {
+    FLAG_NONFINITE = 1,   // a non-finite activation (reference: Error::Internal)
+    FLAG_BAD_TOKEN = 2,   // id >= vocab in the device-resident path (Error::Corrupt)
+};
+
+// GEMM epilogues: C = epilogue(A[M,K] . W[N,K]^T).
+enum GemmEpi : int {
+    EPI_STORE = 0,     // C[m,n] = acc
+    EPI_SCALE = 1,     // C[m,n] = acc * alpha
+    EPI_GEGLU = 2,     // W rows interleaved in 32-blocks (gate, up); C[m,j] = gelu(g) * u
+    EPI_GELU_MUL = 3,  // C[m,n] = gelu(acc) * aux[m * ldaux + n]
+};
+
+struct GemmArgs {
+    const float *A;
+    int64_t lda;
+    const float *W;
+    int64_t ldw;
+    float *C;
+    int64_t ldc;
+    int M, N, K;
+    int epi;
+    float alpha;
+    const float *aux;
+    int64_t ldaux;
+    int n_out;  // EPI_GEGLU: number of real output columns (intermediate size)
+};
+
+hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
+// Plain scalar-FMA fallback for shapes the MFMA kernel does not take
+// (K % 4 != 0); same epilogues.
+hipError_t launch_gemm_simple(const GemmArgs &a, hipStream_t s);
+
+// out = rms_norm_rows(x, w) (w == nullptr: unscaled).
+hipError_t launch_rms_rows(const float *x, const float *w, float *out, int64_t rows, int width,
+                           float eps, int *flag, hipStream_t s);
+
+// h_out = (res + rms(x, w1)) * scale ; if w2: n_out = rms(h_out, w2).
+hipError_t launch_resnorm(const float *x, const float *w1, const float *res, float *h_out,
+                          const float *w2, float *n_out, float scale, int64_t rows, int width,
+                          float eps, int *flag, hipStream_t s);
+
+// h[t] = table[ids[t]] * scale, or feats[featmap[t]] when featmap[t] >= 0;
+// n[t] = rms(h[t], w_in).
+hipError_t launch_gather(const uint32_t *ids, const float *table, int64_t vocab,
+                         const int32_t *featmap, const float *feats, float scale,
+                         const float *w_in, float *h, float *n, int64_t tokens, int width,
+                         float eps, int *flag, hipStream_t s);
+
+// In place on qkv[T, ld]: per-head q RMSNorm(q_norm) + RoPE, k RMSNorm(k_norm)
+// + RoPE, v unscaled RMSNorm. cos/sin tables are [positions, hd/2].
+hipError_t launch_qkv_post(float *qkv, int64_t ld, int64_t tokens, int nh, int nkv, int hd,
+                           const float *qn, const float *kn, const float *cos_t,
+                           const float *sin_t, const int32_t *pos, float eps, int *flag,
+                           hipStream_t s);
+
+// RoPE only (kernel seam): values [T, heads, hd], position = pos0 + t.
+hipError_t launch_rope(float *x, int64_t tokens, int heads, int hd, const float *cos_t,
+                       const float *sin_t, int *flag, hipStream_t s);
+
+// Work item of the attention kernel: one kv head of one row, a block of
+// query vectors [qv0, qv0 + block) where vector v = (pos v / G, head kvh*G + v % G).
+struct AttnTile {
+    int32_t tok0;  // first token of the row in the packed layout
+    int32_t len;   // row length
+    int32_t kvh;   // key/value head
+    int32_t qv0;   // first query vector of the block
+};
+
+struct AttnArgs {
+    const float *q;  // token t, head h at q + t * ldq + h * hd
+    const float *k;  // token t, kv head g at k + t * ldk + g * hd
+    const float *v;
+    float *out;      // token t, head h at out + t * ldo + h * hd
+    int64_t ldq, ldk, ldv, ldo;
+    int nh, nkv, hd;
+    int window;      // < 0: full attention
+    float scale;
+    const AttnTile *tiles;  // MFMA kernel work items
+    int n_tiles;
+    const int32_t *pos;     // per token: position in its row (simple kernel)
+    const int32_t *rowlen;  // per token: length of its row (simple kernel)
+    int64_t tokens;
+    int *flag;
+};
+// Query vectors per work item of the MFMA kernel (0 if hd has no MFMA kernel).
+int attn_block_vectors(int hd);
+hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
+
+// Per row r of [offsets[r], offsets[r+1]): pos[t] = t - offsets[r] and
+// rowlen[t] = offsets[r+1] - offsets[r] (rowlen may be null).
+hipError_t launch_positions(const int64_t *offsets, int batch, int32_t *pos, int32_t *rowlen,
+                            hipStream_t s);
+
+// Mean pool + L2 + Matryoshka per row (masked segmented reduction).
+// pooled / normalized may be null; trunc_out [batch, sum(dims)] may be null.
+hipError_t launch_pool(const float *proj, int width, const int64_t *offsets, int batch,
+                       const int32_t *dims, int n_dims, int dims_total, float *pooled,
+                       float *normalized, float *trunc_out, int *flag, hipStream_t s);
+
+// Elementwise seam kernels.
+hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s);
+hipError_t launch_geglu(const float *g, const float *u, float *y, int64_t n, hipStream_t s);
+hipError_t launch_add(const float *a, const float *b, float *y, int64_t n, hipStream_t s);
+hipError_t launch_finite_check(const float *x, int64_t n, int *flag, hipStream_t s);
+
+}  // namespace svl

@@ -1,0 +1,155 @@
+"""GPU parity of each kernel of the seam (src/tensor/kernels.rs on device
+pointers) against the reference's known answers and the CPU oracle.
+Tolerances follow the reference's own SIMD-vs-scalar differential tests
+(docs/adr/0012: 2e-4 relative for linear, 2e-5 for RMSNorm, 1e-6 for L2 and
+pooling); attention is checked at 1e-4 absolute."""
+import numpy as np
+import pytest
+import torch
+
+import svl_amd as S
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(DEV)
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def empty(n):
+    return torch.empty(n, dtype=torch.float32, device=DEV)
+
+
+def test_linear_kat():  # kernels.rs:1401-1410
+    out = empty(4)
+    S.linear(dev([1, 2, 3, 4, 5, 6]), dev([1, 0, -1, 0, 1, 1]), 2, 3, 2, out)
+    assert host(out).tolist() == [-2.0, 5.0, -2.0, 11.0]
+
+
+@pytest.mark.parametrize("rows,inf,outf", [(1, 768, 768), (37, 768, 1280), (130, 1152, 768),
+                                           (257, 256, 768), (5, 12, 20), (3, 10, 7), (64, 16, 8)])
+def test_linear_matches_oracle(rows, inf, outf):
+    rng = np.random.default_rng(rows * 7 + inf)
+    x = rng.standard_normal((rows, inf)).astype(np.float32)
+    w = (rng.standard_normal((outf, inf)) / np.sqrt(inf)).astype(np.float32)
+    out = empty(rows * outf)
+    S.linear(dev(x), dev(w), rows, inf, outf, out)
+    got = host(out).reshape(rows, outf)
+    ref = O.linear(x, w, rows, inf, outf).reshape(rows, outf)
+    exact = x.astype(np.float64) @ w.astype(np.float64).T
+    np.testing.assert_allclose(got, exact, atol=2e-4 * np.abs(exact).max(), rtol=0)
+    np.testing.assert_allclose(got, ref, atol=2e-4 * np.abs(exact).max(), rtol=0)
+
+
+def test_linear_rejects_nonfinite_output():
+    out = empty(1)
+    with pytest.raises(S.SvlError) as e:
+        S.linear(dev([float("inf")]), dev([1.0]), 1, 1, 1, out)
+    assert e.value.kind == "Internal"
+
+
+def test_rms_norm_kats():  # kernels.rs:1431-1443
+    out = empty(4)
+    S.rms_norm_rows(dev([3, 4, 0, 2]), dev([1, 1]), 2, 2, 0.0, out)
+    np.testing.assert_allclose(host(out), [0.848528, 1.131371, 0, np.sqrt(2)], atol=1e-5)
+    out2 = empty(2)
+    S.rms_norm_rows(dev([3, 4]), None, 1, 2, 0.0, out2)
+    np.testing.assert_allclose(host(out2), [0.848528, 1.131371], atol=1e-5)
+    with pytest.raises(S.SvlError):
+        S.rms_norm_rows(dev([float("nan")]), dev([1.0]), 1, 1, 0.0, empty(1))
+
+
+@pytest.mark.parametrize("rows,width", [(1000, 768), (77, 256), (9, 16), (5, 7), (3, 2304)])
+def test_rms_norm_matches_oracle(rows, width):
+    rng = np.random.default_rng(width)
+    x = rng.standard_normal((rows, width)).astype(np.float32) * 3
+    w = rng.uniform(0.5, 1.5, width).astype(np.float32)
+    out = empty(rows * width)
+    S.rms_norm_rows(dev(x), dev(w), rows, width, 1e-6, out)
+    np.testing.assert_allclose(host(out), O.rms_norm_rows(x, w, rows, width, 1e-6), atol=2e-5, rtol=2e-5)
+    S.rms_norm_rows(dev(x), None, rows, width, 1e-6, out)
+    np.testing.assert_allclose(host(out), O.rms_norm_rows_unscaled(x, rows, width, 1e-6), atol=2e-5, rtol=2e-5)
+
+
+def test_rope_kat_and_oracle():  # kernels.rs:1494-1509
+    v = dev([1.0, 0.0])
+    S.rope_with_inv_freq(v, 1, 1, 2, S.rope_inv_freq(2, 10000.0), 1)
+    np.testing.assert_allclose(host(v), [0.540302, 0.841471], atol=1e-5)
+    rng = np.random.default_rng(3)
+    seq, heads, hd = 300, 3, 256
+    x = rng.standard_normal(seq * heads * hd).astype(np.float32)
+    inv = O.rope_inv_freq(hd, 10000.0)
+    np.testing.assert_array_equal(S.rope_inv_freq(hd, 10000.0), inv)
+    t = dev(x)
+    S.rope_with_inv_freq(t, seq, heads, hd, inv, 5)
+    np.testing.assert_allclose(host(t), O.rope_with_inv_freq(x, seq, heads, hd, inv, 5), atol=1e-5)
+
+
+def test_attention_kats():  # kernels.rs:1529-1566
+    out = empty(2)
+    S.bidirectional_attention(dev([1, 1]), dev([1, 0]), dev([10, 20]), 2, 1, 1, 1, None, 1.0, out)
+    np.testing.assert_allclose(host(out), [12.6894, 12.6894], atol=1e-4)
+    q, k, v = dev([1, 1, 1]), dev([1, 0, 0]), dev([10, 20, 30])
+    out = empty(3)
+    S.bidirectional_attention(q, k, v, 3, 1, 1, 1, 0, 1.0, out)
+    assert host(out).tolist() == [10.0, 20.0, 30.0]
+    S.bidirectional_attention(q, k, v, 3, 1, 1, 1, 1, 1.0, out)
+    np.testing.assert_allclose(host(out), [12.6894, 16.3582, 25.0], atol=1e-4)
+    out = empty(4)
+    S.bidirectional_attention(dev([1, 1, 0, 0]), dev([1, 0]), dev([5, 7]), 1, 4, 2, 1, None, 1.0, out)
+    np.testing.assert_allclose(host(out), [5, 5, 7, 7], atol=1e-6)
+
+
+@pytest.mark.parametrize("seq,nh,nkv,hd,window", [
+    (1, 3, 1, 256, None), (37, 3, 1, 256, None), (130, 3, 1, 256, 16), (700, 3, 1, 256, 512),
+    (97, 4, 2, 256, 8), (64, 12, 12, 64, None), (50, 8, 8, 128, 7), (33, 4, 1, 512, None),
+    (21, 2, 1, 8, 2), (9, 2, 1, 16, None)])
+def test_attention_matches_oracle(seq, nh, nkv, hd, window):
+    rng = np.random.default_rng(seq + hd)
+    # unit-RMS rows scaled like q/k after their norms (weights ~0.25)
+    q = (rng.standard_normal((seq, nh, hd)) * 0.25).astype(np.float32)
+    k = (rng.standard_normal((seq, nkv, hd)) * 0.25).astype(np.float32)
+    v = rng.standard_normal((seq, nkv, hd)).astype(np.float32)
+    out = empty(seq * nh * hd)
+    S.bidirectional_attention(dev(q), dev(k), dev(v), seq, nh, nkv, hd, window, 1.0, out)
+    ref = O.bidirectional_attention(q, k, v, seq, nh, nkv, hd, window, 1.0)
+    np.testing.assert_allclose(host(out), ref, atol=1e-4, rtol=1e-4)
+
+
+def test_elementwise_kats():  # kernels.rs:1151-1160, 1301-1316
+    out = empty(2)
+    S.add(dev([1, 2]), dev([3, 4]), 2, out)
+    assert host(out).tolist() == [4.0, 6.0]
+    S.geglu(dev([1, 0]), dev([2, 3]), 2, out)
+    np.testing.assert_allclose(host(out), [1.682384, 0.0], atol=1e-5)
+    out4 = empty(4)
+    S.gelu_tanh(dev([0, 1, -1, 10]), 4, out4)
+    np.testing.assert_allclose(host(out4), [0, 0.841192, -0.158808, 10], atol=1e-4)
+    x = np.linspace(-6, 6, 10001, dtype=np.float32)
+    o = empty(x.size)
+    S.gelu_tanh(dev(x), x.size, o)
+    ref = np.array([O.gelu_tanh_value(float(t)) for t in x], np.float32)
+    np.testing.assert_allclose(host(o), ref, atol=2e-6, rtol=2e-6)
+
+
+def test_pool_and_l2_kats():  # kernels.rs:1319-1324, 1466-1477
+    out = empty(2)
+    S.mean_pool(dev([1, 2, 3, 4]), 2, 2, out)
+    assert host(out).tolist() == [2.0, 3.0]
+    S.l2_normalize(dev([3, 4]), 2, out)
+    np.testing.assert_allclose(host(out), [0.6, 0.8], atol=1e-7)
+    with pytest.raises(S.SvlError) as e:
+        S.l2_normalize(dev([0, 0]), 2, out)
+    assert e.value.kind == "Internal"
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((513, 768)).astype(np.float32)
+    o = empty(768)
+    S.mean_pool(dev(x), 513, 768, o)
+    # same order of f32 operations as mean_pool_scalar: bit-identical
+    np.testing.assert_array_equal(host(o), O.mean_pool(x, 513, 768))
