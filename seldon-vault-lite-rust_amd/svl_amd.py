@@ -104,6 +104,23 @@ _lib = None
 _lib_lock = threading.Lock()
 
 
+def _share_torch_hip_runtime():
+    """PyTorch-ROCm ships its own libamdhip64.so (SONAME libamdhip64.so.7,
+    the same as /opt/rocm's). Loading torch's HIP library first makes this
+    library bind to that already-loaded runtime, so a process that also uses
+    torch for device buffers and streams has exactly one HIP runtime; two
+    runtimes in one process cannot share streams and torch cannot initialise
+    after another runtime has claimed the device. Without torch the library
+    uses the system ROCm runtime."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        return
+    tlib = os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so")
+    if os.path.exists(tlib):
+        ctypes.CDLL(tlib, mode=ctypes.RTLD_GLOBAL)
+
+
 def lib():
     """Loads libsvl_hip.so; raises if it has not been built."""
     global _lib
@@ -113,6 +130,7 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"HIP extension missing: {LIB_PATH} (build with make -C "
                                f"seldon-vault-lite-rust_amd or __graft_entry__.build())")
+        _share_torch_hip_runtime()
         L = ctypes.CDLL(LIB_PATH)
         vp, i64, i32, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
         fptr = ctypes.POINTER(ctypes.c_float)
