@@ -41,7 +41,23 @@ def parse():
                     help="rows of the workload timed on the CPU oracle (default: one per core, "
                          "at most 16; 0 skips the CPU baseline)")
     ap.add_argument("--t1-runs", type=int, default=20)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (3 times), the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     return ap.parse_args()
+
+
+def copy_calibration():
+    import torch
+
+    n = (1 << 30) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4,
+                      "launches": 3}), flush=True)
 
 
 def gemm_traffic():
@@ -83,6 +99,10 @@ def main():
               f"(rows are independent and would shard by data parallelism, see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     import numpy as np
     import torch
@@ -150,7 +170,7 @@ def main():
     t1_off = np.array([0, 128], np.int64)
     t1_out = torch.zeros((1, 768), dtype=torch.float32, device="cuda:0")
     lat = []
-    for i in range(args.t1_runs + 2):
+    for i in range(args.t1_runs + 2 if args.t1_runs > 0 else 0):
         a = time.perf_counter()
         model.forward_device(t1_ids.data_ptr(), t1_off, [768], t1_out.data_ptr(), stream.cuda_stream)
         if i >= 2:
@@ -180,7 +200,7 @@ def main():
                                "Matryoshka outputs 768/512/256/128",
                    "batch": BATCH, "tokens": T, "max_seq_len": LEN_HI, "parallelism": "single GPU"},
         "p50_ms": round(p50, 3),
-        "t1_p50_ms": round(float(np.median(lat)), 3),
+        "t1_p50_ms": round(float(np.median(lat)), 3) if lat else None,
         "gemm_tflops": round(gemm_tflops, 3),
         "gemm_frac_of_fp32_mfma_peak": round(gemm_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
         "attention_tflops": round(attn_tflops, 3),
