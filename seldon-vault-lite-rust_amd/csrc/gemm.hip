@@ -10,19 +10,30 @@
 //  * 256 threads = 4 wave64s in a 2x2 grid; each wave owns a (BM/2)x(BN/2)
 //    block built from v_mfma_f32_32x32x2_f32 tiles (32 FMA/clk/SIMD, the FP32
 //    matrix peak).
-//  * K advances in BK = 32 slices staged through LDS, double buffered: the
-//    next slice is fetched from HBM/L2 into registers while the MFMAs run
-//    on the current one. Rows are padded to 36 floats so the 16 lanes of a
-//    ds_read_b128 phase hit 64 distinct banks.
+//  * K advances in BK-wide slices that go straight from HBM/L2 into LDS with
+//    buffer_load_dwordx4 ... lds (no register staging), double buffered: the
+//    DMA of slice k+1 is in flight while the MFMAs consume slice k, with one
+//    barrier per slice. Buffer resources bound each operand to its valid
+//    rows, so the ragged M tail (and N tail) reads zeros without branches.
+//  * LDS rows are unpadded; 16-byte chunks are XOR-swizzled by row
+//    (chunk ^ (row / rows_per_bank_line) % chunks_per_row) on the way in, so
+//    the row-parallel ds_read_b128 fragment loads hit distinct banks.
 //  * Each lane reads float4 = 4 consecutive k of its row and feeds them to 4
 //    MFMAs; lanes 0-31 carry k..k+3 and lanes 32-63 k+4..k+7 of the same 8-k
 //    step, a k-permutation applied identically to A and W, so the sum over
-//    k is unchanged.
+//    k is unchanged. Every output element sees the same MFMA sequence over k
+//    whatever the tile shape, so results do not depend on the tile chosen
+//    or on a row's position in the batch.
+//  * The tile shape is chosen per launch: 128x128 (3 workgroups per CU) for
+//    wide outputs, 128x64 for mid-size grids, 64x64 x BK 32 (4 per CU) when
+//    N <= 256, where 128x128 tiles would leave most CUs idle.
 //  * Tiles are numbered M-major with N fastest and remapped so consecutive
 //    tiles land on the same XCD: the N tiles that share an A block hit that
 //    XCD's L2 instead of HBM.
 //  * Epilogues fuse the elementwise op that follows each projection in
 //    text.rs (PLE scale, GeGLU, GELU-gate x per-layer input).
+#include <algorithm>
+
 #include "dev_common.hpp"
 #include "svl_internal.hpp"
 
@@ -30,6 +41,7 @@ namespace svl {
 
 template <int BM, int BN>
 struct GemmShape {
+    static_assert(BM % 64 == 0 && BN % 64 == 0, "2x2 waves of 32x32 MFMA tiles");
     static constexpr int BK = 32;
     static constexpr int LDS = BK + 4;
     static constexpr int WM = BM / 2;
@@ -40,8 +52,42 @@ struct GemmShape {
     static constexpr int W_F4 = BN * BK / 4 / 256;
 };
 
-template <int BM, int BN, int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_nt_mfma(GemmArgs p, int tiles_m, int tiles_n) {
+// Epilogue shared by the GEMM kernels. Accumulator register r of a 32x32
+// tile holds row 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.
+template <int TM, int TN, int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x16 (&acc)[TM][TN],
+                                              int mw, int nw, int l32, int hh) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = mw + i * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+            if (m >= p.M) continue;
+            float *crow = p.C + (int64_t)m * p.ldc;
+            if constexpr (EPI == EPI_GEGLU) {
+#pragma unroll
+                for (int j = 0; j < TN; j += 2) {
+                    const int oc = nw / 2 + (j / 2) * 32 + l32;
+                    if (oc < p.n_out) crow[oc] = gelu_tanh(acc[i][j][r]) * acc[i][j + 1][r];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int n = nw + j * 32 + l32;
+                    if (n >= p.N) continue;
+                    float v = acc[i][j][r];
+                    if constexpr (EPI == EPI_SCALE) v = v * p.alpha;
+                    if constexpr (EPI == EPI_GELU_MUL)
+                        v = gelu_tanh(v) * p.aux[(int64_t)m * p.ldaux + n];
+                    crow[n] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int EPI, int MINB = 2>
+__global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_m, int tiles_n) {
     using S = GemmShape<BM, BN>;
     __shared__ float As[2][BM * S::LDS];
     __shared__ float Ws[2][BN * S::LDS];
@@ -129,36 +175,115 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_mfma(GemmArgs p, int tiles_m, 
         __syncthreads();
     }
 
-    // Epilogue. Accumulator register r of a 32x32 tile holds row
-    // 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.
-    const int mw = m0 + wm * S::WM, nw = n0 + wn * S::WN;
+    gemm_epilogue<S::TM, S::TN, EPI>(p, acc, m0 + wm * S::WM, n0 + wn * S::WN, l32, hh);
+}
+
+// s_waitcnt vmcnt(N): at most N vector-memory operations of this wave in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Direct-to-LDS variant; requires K % BK == 0 and 16-byte aligned rows.
+template <int BM, int BN, int BK, int EPI, int MINB>
+__global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m, int tiles_n) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int TM = BM / 64, TN = BN / 64;   // 32x32 tiles per wave
+    constexpr int CPR = BK / 4;                 // 16-byte chunks per row
+    constexpr int RPK = 64 / CPR;               // rows per 1 KB DMA instruction
+    constexpr int RPL = 64 / BK;                // rows per 64-bank LDS line
+    constexpr int A_CH = BM / RPK / 4;          // DMA instructions per wave per slice
+    constexpr int W_CH = BN / RPK / 4;
+    static_assert(BM % 64 == 0 && BN % 64 == 0 && A_CH >= 1 && W_CH >= 1, "tile shape");
+    static_assert(EPI != EPI_GEGLU || TN % 2 == 0, "GeGLU pairs 32-column tiles");
+    __shared__ float As[2][BM * BK];
+    __shared__ float Ws[2][BN * BK];
+
+    const int ntiles = tiles_m * tiles_n;
+    const int bid = blockIdx.x;
+    const int xcd = bid & 7, local = bid >> 3;
+    const int q8 = ntiles >> 3, r8 = ntiles & 7;
+    const int tile = xcd * q8 + min(xcd, r8) + local;
+    const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int M = p.M, N = p.N;
+
+    // Operand windows: [valid rows of this tile] x lda floats; reads past
+    // the last valid row return zero.
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.A + (int64_t)m0 * p.lda), (short)0, (int)(min(BM, M - m0) * p.lda * 4),
+        0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.W + (int64_t)n0 * p.ldw), (short)0, (int)(min(BN, N - n0) * p.ldw * 4),
+        0x00020000);
+    int a_off[A_CH], w_off[W_CH];
 #pragma unroll
-    for (int i = 0; i < S::TM; ++i) {
+    for (int q = 0; q < A_CH; ++q) {
+        const int row = (wave * A_CH + q) * RPK + lane / CPR;
+        const int c = (lane % CPR) ^ ((row / RPL) % CPR);
+        a_off[q] = (row * (int)p.lda + 4 * c) * 4;
+    }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = mw + i * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-            if (m >= M) continue;
-            float *crow = p.C + (int64_t)m * p.ldc;
-            if constexpr (EPI == EPI_GEGLU) {
+    for (int q = 0; q < W_CH; ++q) {
+        const int row = (wave * W_CH + q) * RPK + lane / CPR;
+        const int c = (lane % CPR) ^ ((row / RPL) % CPR);
+        w_off[q] = (row * (int)p.ldw + 4 * c) * 4;
+    }
+    auto issue = [&](int buf, int k0) {
 #pragma unroll
-                for (int j = 0; j < S::TN; j += 2) {
-                    const int oc = nw / 2 + (j / 2) * 32 + l32;
-                    if (oc < p.n_out) crow[oc] = gelu_tanh(acc[i][j][r]) * acc[i][j + 1][r];
-                }
-            } else {
+        for (int q = 0; q < A_CH; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void *)&As[buf][(wave * A_CH + q) * 256], 16,
+                a_off[q], k0 * 4, 0, 0);
 #pragma unroll
-                for (int j = 0; j < S::TN; ++j) {
-                    const int n = nw + j * 32 + l32;
-                    if (n >= N) continue;
-                    float v = acc[i][j][r];
-                    if constexpr (EPI == EPI_SCALE) v = v * p.alpha;
-                    if constexpr (EPI == EPI_GELU_MUL)
-                        v = gelu_tanh(v) * p.aux[(int64_t)m * p.ldaux + n];
-                    crow[n] = v;
-                }
-            }
+        for (int q = 0; q < W_CH; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rw, (__attribute__((address_space(3))) void *)&Ws[buf][(wave * W_CH + q) * 256], 16,
+                w_off[q], k0 * 4, 0, 0);
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int sw = (l32 / RPL) % CPR;
+    const int nk = p.K / BK;
+    issue(0, 0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        wait_vmcnt<0>();   // this wave's DMA of slice kt has landed
+        __syncthreads();   // ... and every wave's; slice kt-1 is no longer read
+        if (kt + 1 < nk) issue(cur ^ 1, (kt + 1) * BK);
+        const float *as = &As[cur][(wm * (BM / 2) + l32) * BK];
+        const float *ws = &Ws[cur][(wn * (BN / 2) + l32) * BK];
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 8) {
+            const int pos = ((kk >> 2) + hh) ^ sw;
+            f32x4 a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) a[i] = *(const f32x4 *)(as + i * 32 * BK + 4 * pos);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) b[j] = *(const f32x4 *)(ws + j * 32 * BK + 4 * pos);
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
+                                                                         acc[i][j], 0, 0, 0);
         }
     }
+    gemm_epilogue<TM, TN, EPI>(p, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2), l32, hh);
+#endif
 }
 
 // One thread per output element; any K. Kept for shapes the MFMA kernel's
@@ -191,6 +316,27 @@ __global__ __launch_bounds__(256) void gemm_nt_simple(GemmArgs p) {
     }
 }
 
+template <int BM, int BN, int BK, int EPI, int MINB>
+static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
+    const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
+    hipLaunchKernelGGL((gemm_nt_dma<BM, BN, BK, EPI, MINB>), dim3(tm * tn), dim3(256), 0, s, a, tm,
+                       tn);
+    return hipGetLastError();
+}
+
+// Tile choice: N <= 256 -> 64x64 (x BK 32, 4 workgroups per CU); fewer than
+// four 128x128 tiles per CU -> 128x64; otherwise 128x128 (3 per CU). GeGLU
+// needs 32-column tile pairs, so it always takes 128x128.
+template <int EPI>
+static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
+    const int64_t tiles128 = (int64_t)((a.M + 127) / 128) * ((a.N + 127) / 128);
+    if constexpr (EPI != EPI_GEGLU) {
+        if (a.N <= 256 && a.K % 32 == 0) return launch_dma<64, 64, 32, EPI, 4>(a, s);
+        if (tiles128 < 4 * 256) return launch_dma<128, 64, 16, EPI, 4>(a, s);
+    }
+    return launch_dma<128, 128, 16, EPI, 3>(a, s);
+}
+
 template <int BM, int BN, int EPI>
 static hipError_t launch_mfma(const GemmArgs &a, hipStream_t s) {
     const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
@@ -213,6 +359,17 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
     const bool vec_ok = (a.K % 4 == 0) && (a.lda % 4 == 0) && (a.ldw % 4 == 0) &&
                         ((uintptr_t)a.A % 16 == 0) && ((uintptr_t)a.W % 16 == 0);
     if (!vec_ok) return launch_gemm_simple(a, s);
+    // Buffer offsets are 32-bit: an operand window must stay below 2 GiB.
+    const bool dma_ok = a.K % 16 == 0 && (int64_t)128 * std::max(a.lda, a.ldw) * 4 < INT32_MAX;
+    if (dma_ok) {
+        switch (a.epi) {
+            case EPI_STORE: return launch_dma_auto<EPI_STORE>(a, s);
+            case EPI_SCALE: return launch_dma_auto<EPI_SCALE>(a, s);
+            case EPI_GEGLU: return launch_dma_auto<EPI_GEGLU>(a, s);
+            case EPI_GELU_MUL: return launch_dma_auto<EPI_GELU_MUL>(a, s);
+        }
+        return hipErrorInvalidValue;
+    }
     switch (a.epi) {
         case EPI_STORE: return launch_mfma<128, 128, EPI_STORE>(a, s);
         case EPI_SCALE: return launch_mfma<128, 128, EPI_SCALE>(a, s);
