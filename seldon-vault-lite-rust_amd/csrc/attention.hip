@@ -26,12 +26,15 @@
 // Generic kernel (any head_dim): one wave per (token, head), the reference's
 // own order of operations (score row, max-subtracted exp, divide by the sum,
 // p-weighted value rows in key order).
+#include <algorithm>
+
 #include "dev_common.hpp"
 #include "svl_internal.hpp"
 
 namespace svl {
 
 constexpr int ATTN_WAVES = 4;
+constexpr float RESCALE_LOG2 = 8.0f;
 
 template <int N>
 __device__ __forceinline__ void load_n(const float *src, float (&dst)[N]) {
@@ -176,6 +179,205 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_mfma_kernel(AttnArgs p) {
     }
 }
 
+// head_dim 256 variant with the K/V tiles streamed by DMA.
+//  * K and V tiles (32 keys x 1 KB) go from HBM/L2 straight into LDS with
+//    buffer_load_dwordx4 ... lds, double buffered (2 x 64 KB): tile t+1 is in
+//    flight while tile t is consumed; one barrier per tile. Keys past the row
+//    end fall outside the buffer window and read as zero.
+//  * K rows are stored with their 16-byte chunks XOR-swizzled by (key % 16):
+//    S^T reads 32 key rows at the same chunk, which then hit 16 distinct
+//    bank groups per phase. V rows are read row-contiguously by each half
+//    wave and stay unswizzled.
+//  * Output row i of O^T tile t holds head dims (t / 4) * 128 + 4 i + t % 4:
+//    lane l reads chunks l and 32 + l of a V row, contiguous across lanes.
+//  * Online softmax in log2 units (v_exp_f32) with a lazily moved reference
+//    max, so the 128 output accumulators are rescaled only when a query's
+//    running max grows by more than 2^8.
+//  * The per-tile advance of the DMA source goes in the scalar offset, and
+//    the swizzled K-read offsets are 8 per-lane values, which keeps the
+//    kernel within 512 registers without spills.
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    constexpr int HD = 256;
+    constexpr int KT = 32;
+    constexpr int NQ = HD / 8;   // float4 query fragments per lane
+    constexpr int NT = HD / 32;  // output tiles
+    constexpr int ROWS_PER_WAVE = KT / WAVES;
+    __shared__ float Ks[2][KT * HD];
+    __shared__ float Vs[2][KT * HD];
+
+    const AttnTile tile = p.tiles[blockIdx.x];
+    const int G = p.nh / p.nkv;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int nvec = tile.len * G;
+    const int v = tile.qv0 + wave * 32 + l32;
+    const bool vvalid = v < nvec;
+    const int vq = vvalid ? v : nvec - 1;
+    const int qpos = vq / G;
+    const int qhead = tile.kvh * G + (vq - qpos * G);
+    const float *qrow = p.q + (int64_t)(tile.tok0 + qpos) * p.ldq + qhead * HD;
+
+    // Query fragments pre-scaled by scale * log2(e): S^T comes out in log2 units.
+    const float scale2 = p.scale * 1.4426950408889634f;
+    f32x4 qf[NQ];
+#pragma unroll
+    for (int c = 0; c < NQ; ++c) qf[c] = *(const f32x4 *)(qrow + 8 * c + 4 * hh) * scale2;
+
+    f32x16 o[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+    float m_ref = -INFINITY, l_run = 0.f;
+
+    const int v_last = min(tile.qv0 + 32 * WAVES, nvec) - 1;
+    const int p_lo = tile.qv0 / G, p_hi = v_last / G;
+    int k_lo = 0, k_hi = tile.len - 1;
+    if (p.window >= 0) {
+        k_lo = max(0, p_lo - p.window);
+        k_hi = min(tile.len - 1, p_hi + p.window);
+    }
+    const int k_first = (k_lo / KT) * KT;
+    const int n_tiles = (k_hi - k_first) / KT + 1;
+
+    // Buffer windows over this row's keys of this KV head.
+    const int ldk = (int)p.ldk, ldv = (int)p.ldv;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.k + (int64_t)tile.tok0 * p.ldk + tile.kvh * HD), (short)0,
+        ((tile.len - 1) * ldk + HD) * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.v + (int64_t)tile.tok0 * p.ldv + tile.kvh * HD), (short)0,
+        ((tile.len - 1) * ldv + HD) * 4, 0x00020000);
+    // One DMA instruction moves one 1 KB key row of the tile; lane l fills
+    // chunk slot l (K: with global chunk l ^ (row % 16)).
+    int koff[ROWS_PER_WAVE], voff[ROWS_PER_WAVE];
+#pragma unroll
+    for (int q = 0; q < ROWS_PER_WAVE; ++q) {
+        const int r = wave * ROWS_PER_WAVE + q;
+        koff[q] = (r * ldk + 4 * (lane ^ (r & 15))) * 4;
+        voff[q] = (r * ldv + 4 * lane) * 4;
+    }
+    auto issue = [&](int buf, int k0) {
+#pragma unroll
+        for (int q = 0; q < ROWS_PER_WAVE; ++q) {
+            const int r = wave * ROWS_PER_WAVE + q;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rk, (__attribute__((address_space(3))) void *)&Ks[buf][r * HD], 16, koff[q],
+                k0 * ldk * 4, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rv, (__attribute__((address_space(3))) void *)&Vs[buf][r * HD], 16, voff[q],
+                k0 * ldv * 4, 0, 0);
+        }
+    };
+    // K fragment c (chunk 2c + hh of key row l32) sits at chunk
+    // (2c + hh) ^ (l32 % 16) = 16 (c / 8) + 2 ((c % 8) ^ (sw / 2)) + (hh ^ (sw % 2)).
+    const int sw = l32 & 15;
+    int kcol[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) kcol[b] = l32 * HD + 4 * (2 * (b ^ (sw >> 1)) + (hh ^ (sw & 1)));
+
+    issue(0, k_first);
+    for (int it = 0; it < n_tiles; ++it) {
+        const int k0 = k_first + it * KT;
+        const int cur = it & 1;
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+        __syncthreads();
+        if (it + 1 < n_tiles) issue(cur ^ 1, k0 + KT);
+
+        f32x16 s0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s0[r] = 0.f;
+        const float *kb = Ks[cur];
+#pragma unroll
+        for (int c = 0; c < NQ; ++c) {
+            const f32x4 a0 = *(const f32x4 *)(kb + kcol[c & 7] + 64 * (c >> 3));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], qf[c][j], s0, 0, 0, 0);
+        }
+
+        // Scores in log2 units; masks only on the row-tail tile and on tiles
+        // that cross a sliding-window edge of some query of the block.
+        // Lanes of invalid query vectors are never stored and need no mask.
+        float pr[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pr[r] = s0[r];
+        const bool tail = k0 + KT > tile.len;
+        const bool edge = p.window >= 0 && (k0 < p_hi - p.window || k0 + KT - 1 > p_lo + p.window);
+        if (tail || edge) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                const int dist = qpos > key ? qpos - key : key - qpos;
+                const bool ok = (key < tile.len) & ((p.window < 0) | (dist <= p.window));
+                pr[r] = ok ? pr[r] : -INFINITY;
+            }
+        }
+        float tmax = pr[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, pr[r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        // Lazy rescale: the reference max m_ref only moves when a query's
+        // max grows by more than RESCALE_LOG2 (probabilities then stay below
+        // 2^RESCALE_LOG2). O and l are divided out at the end, so the result
+        // is the same softmax; the 128 accumulator registers are rescaled
+        // only on the (rare, wave-uniform) tiles where some max jumped.
+        const bool grow = tmax > m_ref + RESCALE_LOG2;
+        if (__ballot(grow)) {
+            const float m_new = grow ? tmax : m_ref;
+            const float alpha = m_ref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) o[t] = o[t] * alpha;
+            m_ref = m_new;
+        }
+        float psum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            pr[r] = pr[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pr[r] - m_ref);
+            psum += pr[r];
+        }
+        psum += __shfl_xor(psum, 32, 64);
+        l_run += psum;
+
+        const float *vb = Vs[cur] + 4 * hh * HD + 4 * l32;
+#pragma unroll
+        for (int si = 0; si < 16; ++si) {
+            const float *vp = vb + (8 * (si >> 2) + (si & 3)) * HD;
+            const f32x4 va = *(const f32x4 *)(vp);
+            const f32x4 vc = *(const f32x4 *)(vp + 128);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[t], pr[si], o[t], 0, 0, 0);
+                o[4 + t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vc[t], pr[si], o[4 + t], 0, 0, 0);
+            }
+        }
+    }
+
+    if (vvalid) {
+        const float inv = 1.0f / l_run;
+        float *orow = p.out + (int64_t)(tile.tok0 + qpos) * p.ldo + qhead * HD;
+        bool ok = isfinite(inv);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = 8 * (r >> 2) + 4 * hh + (r & 3);
+            f32x4 lo, hi;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                lo[t] = o[t][r] * inv;
+                hi[t] = o[4 + t][r] * inv;
+            }
+            ok = ok && finite4(lo) && finite4(hi);
+            *(f32x4 *)(orow + 4 * i) = lo;
+            *(f32x4 *)(orow + 128 + 4 * i) = hi;
+        }
+        if (!ok) raise_flag(p.flag, FLAG_NONFINITE);
+    }
+#endif
+}
+
 constexpr int ATTN_SIMPLE_MAX_KEYS = 8192;
 
 __global__ __launch_bounds__(64) void attn_simple_kernel(AttnArgs p) {
@@ -246,8 +448,11 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
                                a);
             return hipGetLastError();
         case 256:
-            hipLaunchKernelGGL((attn_mfma_kernel<256, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
-                               a);
+            if (a.tokens * std::max(std::max(a.ldk, a.ldv), (int64_t)256) * 4 < INT32_MAX)
+                hipLaunchKernelGGL((attn_dma256_kernel<ATTN_WAVES>), dim3(a.n_tiles), block, 0, s, a);
+            else
+                hipLaunchKernelGGL((attn_mfma_kernel<256, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
+                                   a);
             return hipGetLastError();
         default:
             if (!a.pos || !a.rowlen) return hipErrorInvalidValue;
