@@ -296,6 +296,64 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(
     if (!ok) raise_flag(flag, FLAG_NONFINITE);
 }
 
+// head_dim 256 fast path: one wave per token. Lane l holds elements
+// [4l, 4l+4) of every head row of the token (one float4 per head row), so
+// each head-row norm is one wave reduction, and the rotate-half partner of
+// element j < 128 (element j + 128) sits in lane l ^ 32.
+template <int ROWS>
+__global__ __launch_bounds__(256) void qkv_post256_kernel(
+    float *__restrict__ qkv, int64_t ld, int64_t tokens, int nh, int nkv,
+    const float *__restrict__ qn, const float *__restrict__ kn, const float *__restrict__ cos_t,
+    const float *__restrict__ sin_t, const int32_t *__restrict__ pos, float eps, int *flag) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= tokens) return;
+    const int per_tok = nh + 2 * nkv;
+    f32x4 *row = (f32x4 *)(qkv + t * ld) + lane;
+    f32x4 x[ROWS];
+    float ss[ROWS];
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k) {
+        if (k < per_tok) {
+            x[k] = row[64 * k];
+            ss[k] = x[k].x * x[k].x + x[k].y * x[k].y + x[k].z * x[k].z + x[k].w * x[k].w;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k)
+        if (k < per_tok) ss[k] = wave_sum(ss[k]);
+    const f32x4 wq = ((const f32x4 *)qn)[lane];
+    const f32x4 wk = ((const f32x4 *)kn)[lane];
+    const int half = lane >> 5;  // 0: elements j < 128, 1: j >= 128
+    const int64_t tab = (int64_t)pos[t] * 128 + 4 * (lane & 31);
+    const f32x4 c = *(const f32x4 *)(cos_t + tab);
+    const f32x4 sn = *(const f32x4 *)(sin_t + tab);
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k) {
+        if (k >= per_tok) continue;
+        ok = ok && isfinite(ss[k]);
+        const float inv = rms_inverse(ss[k], 256, eps);
+        if (k >= nh + nkv) {  // value head: unscaled norm, no rotation
+            const f32x4 y = x[k] * inv;
+            ok = ok && finite4(y);
+            row[64 * k] = y;
+            continue;
+        }
+        const f32x4 y = x[k] * inv * (k < nh ? wq : wk);
+        f32x4 other;
+        other.x = __shfl_xor(y.x, 32, 64);
+        other.y = __shfl_xor(y.y, 32, 64);
+        other.z = __shfl_xor(y.z, 32, 64);
+        other.w = __shfl_xor(y.w, 32, 64);
+        // first half: first*c - second*s; second half: first*s + second*c
+        const f32x4 out = half ? other * sn + y * c : y * c - other * sn;
+        ok = ok && finite4(out);
+        row[64 * k] = out;
+    }
+    if (!ok) raise_flag(flag, FLAG_NONFINITE);
+}
+
 hipError_t launch_qkv_post(float *qkv, int64_t ld, int64_t tokens, int nh, int nkv, int hd,
                            const float *qn, const float *kn, const float *cos_t,
                            const float *sin_t, const int32_t *pos, float eps, int *flag,
@@ -303,6 +361,17 @@ hipError_t launch_qkv_post(float *qkv, int64_t ld, int64_t tokens, int nh, int n
     const int64_t head_rows = tokens * (nh + 2 * nkv);
     if (head_rows <= 0) return hipSuccess;
     if (hd > QKV_MAX_HD || hd % 2) return hipErrorInvalidValue;
+    const bool aligned = ld % 4 == 0 && (uintptr_t)qkv % 16 == 0;
+    if (hd == 256 && aligned && nh + 2 * nkv <= 8) {
+        const dim3 grid((unsigned)((tokens + 3) / 4));
+        if (nh + 2 * nkv <= 5)
+            hipLaunchKernelGGL(qkv_post256_kernel<5>, grid, dim3(256), 0, s, qkv, ld, tokens, nh,
+                               nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
+        else
+            hipLaunchKernelGGL(qkv_post256_kernel<8>, grid, dim3(256), 0, s, qkv, ld, tokens, nh,
+                               nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(qkv_post_kernel, dim3((unsigned)((head_rows + 3) / 4)), dim3(256), 0, s,
                        qkv, ld, tokens, nh, nkv, hd, qn, kn, cos_t, sin_t, pos, eps, flag);
     return hipGetLastError();
@@ -361,10 +430,13 @@ hipError_t launch_positions(const int64_t *offsets, int batch, int32_t *pos, int
 }
 
 // ---- masked mean pool + L2 + Matryoshka (kernels.rs:882-927) ---------------
-// One workgroup per row. Each thread owns columns c = tid + 256*j and sums the
-// row's tokens in order, then multiplies by 1/len: the same operations in the
-// same order as mean_pool_scalar, so pooled is bit-identical for identical
-// projected inputs.
+// pool_sum_kernel: one 64-lane workgroup per (row, 64 columns); each lane
+// sums its column over the row's tokens in token order and multiplies by
+// 1/len: the same operations in the same order as mean_pool_scalar, so
+// pooled is bit-identical for identical projected inputs. Loads are issued
+// eight tokens ahead of the additions to keep HBM busy.
+// pool_norm_kernel: one workgroup per row: L2 normalisation and the
+// Matryoshka truncations, each renormalised.
 constexpr int POOL_MAX_WIDTH = 4096;
 
 __device__ float block_sum_256(float v, float *red) {
@@ -376,30 +448,46 @@ __device__ float block_sum_256(float v, float *red) {
     return red[0] + red[1] + red[2] + red[3];
 }
 
-__global__ __launch_bounds__(256) void pool_kernel(const float *__restrict__ proj, int width,
-                                                   const int64_t *__restrict__ offsets,
-                                                   const int32_t *__restrict__ dims, int n_dims,
-                                                   int dims_total, float *__restrict__ pooled,
-                                                   float *__restrict__ normalized,
-                                                   float *__restrict__ trunc_out, int *flag) {
+__global__ __launch_bounds__(64) void pool_sum_kernel(const float *__restrict__ proj, int width,
+                                                      const int64_t *__restrict__ offsets,
+                                                      float *__restrict__ pooled, int *flag) {
+    const int r = blockIdx.x;
+    const int c = blockIdx.y * 64 + threadIdx.x;
+    if (c >= width) return;
+    const int64_t a = offsets[r], b = offsets[r + 1];
+    const float *src = proj + a * width + c;
+    const int64_t n = b - a;
+    float acc = 0.f;
+    int64_t t = 0;
+    for (; t + 8 <= n; t += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[(t + u) * width];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; t < n; ++t) acc += src[t * width];
+    acc *= 1.0f / (float)n;
+    if (!isfinite(acc)) raise_flag(flag, FLAG_NONFINITE);
+    pooled[(int64_t)r * width + c] = acc;
+}
+
+__global__ __launch_bounds__(256) void pool_norm_kernel(const float *__restrict__ pooled, int width,
+                                                        const int32_t *__restrict__ dims,
+                                                        int n_dims, int dims_total,
+                                                        float *__restrict__ normalized,
+                                                        float *__restrict__ trunc_out, int *flag) {
     __shared__ float nv[POOL_MAX_WIDTH];
     __shared__ float red[4];
     const int r = blockIdx.x;
-    const int64_t a = offsets[r], b = offsets[r + 1];
-    const float inv_rows = 1.0f / (float)(b - a);
-    bool ok = true;
     float ss = 0.f;
     for (int c = threadIdx.x; c < width; c += 256) {
-        float acc = 0.f;
-        for (int64_t t = a; t < b; ++t) acc += proj[t * width + c];
-        acc *= inv_rows;
-        ok = ok && isfinite(acc);
-        if (pooled) pooled[(int64_t)r * width + c] = acc;
-        nv[c] = acc;
-        ss += acc * acc;
+        const float v = pooled[(int64_t)r * width + c];
+        nv[c] = v;
+        ss += v * v;
     }
     ss = block_sum_256(ss, red);
-    ok = ok && isfinite(ss) && ss > 0.f;
+    bool ok = isfinite(ss) && ss > 0.f;
     const float inv = 1.0f / sqrtf(ss);
     for (int c = threadIdx.x; c < width; c += 256) {
         const float y = nv[c] * inv;
@@ -427,9 +515,21 @@ hipError_t launch_pool(const float *proj, int width, const int64_t *offsets, int
                        const int32_t *dims, int n_dims, int dims_total, float *pooled,
                        float *normalized, float *trunc_out, int *flag, hipStream_t s) {
     if (batch <= 0) return hipSuccess;
+    if (width > POOL_MAX_WIDTH || !pooled) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pool_sum_kernel, dim3(batch, (width + 63) / 64), dim3(64), 0, s, proj,
+                       width, offsets, pooled, flag);
+    if (!normalized && !trunc_out) return hipGetLastError();
+    return launch_pool_norm(pooled, width, batch, dims, n_dims, dims_total, normalized, trunc_out,
+                            flag, s);
+}
+
+hipError_t launch_pool_norm(const float *pooled, int width, int batch, const int32_t *dims,
+                            int n_dims, int dims_total, float *normalized, float *trunc_out,
+                            int *flag, hipStream_t s) {
+    if (batch <= 0) return hipSuccess;
     if (width > POOL_MAX_WIDTH) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(pool_kernel, dim3(batch), dim3(256), 0, s, proj, width, offsets, dims,
-                       n_dims, dims_total, pooled, normalized, trunc_out, flag);
+    hipLaunchKernelGGL(pool_norm_kernel, dim3(batch), dim3(256), 0, s, pooled, width, dims, n_dims,
+                       dims_total, normalized, trunc_out, flag);
     return hipGetLastError();
 }
 

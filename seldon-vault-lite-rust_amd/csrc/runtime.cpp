@@ -1315,20 +1315,14 @@ svl_status svl_l2_normalize(const float *d_in, int64_t n, float *d_out, void *st
     int *flag;
     ST_TRY(seam_flag(&flag));
     hipStream_t s = (hipStream_t)stream;
-    // one row of n values pooled over a single token is the vector itself;
-    // the pool kernel then applies l2_normalize_scalar's arithmetic.
-    int64_t *doff = nullptr;
-    const int64_t offs[2] = {0, 1};
-    HIP_TRY(hipMalloc((void **)&doff, sizeof offs));
+    // The pool-normalisation kernel on one already pooled row applies
+    // l2_normalize_scalar's arithmetic.
     svl_status st = SVL_OK;
-    if (hipMemcpyAsync(doff, offs, sizeof offs, hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipMemsetAsync(flag, 0, sizeof(int), s) != hipSuccess ||
-        launch_pool(d_in, (int)n, doff, 1, nullptr, 0, 0, nullptr, d_out, nullptr, flag, s) !=
-            hipSuccess)
+    if (hipMemsetAsync(flag, 0, sizeof(int), s) != hipSuccess ||
+        launch_pool_norm(d_in, (int)n, 1, nullptr, 0, 0, d_out, nullptr, flag, s) != hipSuccess)
         st = fail(SVL_DEVICE, "l2 launch failed");
     if (st == SVL_OK) st = seam_finish(s, flag, "L2 normalization");
     (void)hipStreamSynchronize(s);
-    (void)hipFree(doff);
     if (st == SVL_INTERNAL) g_err = "cannot normalize a zero or non-finite vector";
     return st;
 }

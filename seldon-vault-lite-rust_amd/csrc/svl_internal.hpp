@@ -105,10 +105,15 @@ hipError_t launch_positions(const int64_t *offsets, int batch, int32_t *pos, int
                             hipStream_t s);
 
 // Mean pool + L2 + Matryoshka per row (masked segmented reduction).
-// pooled / normalized may be null; trunc_out [batch, sum(dims)] may be null.
+// pooled [batch, width] is required; normalized and trunc_out
+// [batch, sum(dims)] may be null.
 hipError_t launch_pool(const float *proj, int width, const int64_t *offsets, int batch,
                        const int32_t *dims, int n_dims, int dims_total, float *pooled,
                        float *normalized, float *trunc_out, int *flag, hipStream_t s);
+// L2 normalisation and Matryoshka truncations of already pooled rows.
+hipError_t launch_pool_norm(const float *pooled, int width, int batch, const int32_t *dims,
+                            int n_dims, int dims_total, float *normalized, float *trunc_out,
+                            int *flag, hipStream_t s);
 
 // Elementwise seam kernels.
 hipError_t launch_gelu(const float *x, float *y, int64_t n, hipStream_t s);
