@@ -147,7 +147,11 @@ struct svl_text_model {
     int64_t rope_positions = 0;
     int type_hd[2] = {0, 0};
 
+    int64_t max_qkv = 0, max_q = 0;  // widest per-layer QKV / query row
     hipStream_t stream = nullptr;
+    hipStream_t stream2 = nullptr;   // second group of rows
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    bool split_streams = true;
     std::mutex mu;
 
     // workspace
@@ -185,6 +189,9 @@ struct svl_text_model {
             (void)hipEventDestroy(t.a);
             (void)hipEventDestroy(t.b);
         }
+        if (ev_fork) (void)hipEventDestroy(ev_fork);
+        if (ev_join) (void)hipEventDestroy(ev_join);
+        if (stream2) (void)hipStreamDestroy(stream2);
         if (stream) (void)hipStreamDestroy(stream);
     }
 };
@@ -388,49 +395,66 @@ void collect_timing(svl_text_model *m) {
 
 // ---------------------------------------------------------------------------
 // Per-call geometry.
+//
+// A batch is cut into at most two groups of consecutive rows with about the
+// same number of tokens. Each group runs the whole encoder on its own stream
+// (both at the default priority), on its own token range of every workspace
+// buffer, so the two streams' kernels fill each other's partial last rounds
+// of workgroups and the bandwidth-bound norm kernels of one group overlap the
+// MFMA-bound GEMMs of the other. Every row's arithmetic is unchanged.
+
+constexpr int64_t SPLIT_MIN_TOKENS = 4096;
+
+struct Group {
+    int32_t r0 = 0, nrows = 0;  // rows [r0, r0 + nrows)
+    int64_t t0 = 0, T = 0;      // tokens [t0, t0 + T)
+    int64_t off_slot = 0;       // first entry of this group's rebased offsets
+    // attention work lists per distinct (nkv, hd): (first tile, count)
+    std::map<std::pair<int, int>, std::pair<int, int>> tile_ranges;
+    double attn_flops[2] = {0, 0};  // algorithmic attention FLOPs per layer type
+};
 
 struct Batch {
     int32_t B = 0;
     int64_t T = 0;
-    std::vector<int64_t> offsets;  // host copy
-    // attention work lists per distinct (nkv, hd) key
-    std::map<std::pair<int, int>, std::pair<int, int>> tile_ranges;  // -> (first, count)
-    std::vector<AttnTile> tiles;
-    // attention algorithmic FLOPs per layer type, for timing
-    double attn_flops[2] = {0, 0};
+    std::vector<int64_t> offsets;      // host copy, global
+    std::vector<int64_t> dev_offsets;  // per group: nrows + 1 offsets rebased to the group
+    std::vector<AttnTile> tiles;       // all groups, tok0 relative to the group
+    std::vector<Group> groups;
 };
 
-void build_tiles(const svl_text_model *m, Batch &b) {
-    b.tiles.clear();
-    b.tile_ranges.clear();
-    std::vector<int> order(b.B);
-    for (int r = 0; r < b.B; ++r) order[r] = r;
+void build_group(const svl_text_model *m, Batch &b, Group &g) {
+    g.off_slot = (int64_t)b.dev_offsets.size();
+    for (int r = 0; r <= g.nrows; ++r) b.dev_offsets.push_back(b.offsets[g.r0 + r] - g.t0);
+    std::vector<int> order(g.nrows);
+    for (int r = 0; r < g.nrows; ++r) order[r] = g.r0 + r;
     // longest rows first: the attention cost of a work item grows with its row
     std::stable_sort(order.begin(), order.end(), [&](int x, int y) {
         return b.offsets[x + 1] - b.offsets[x] > b.offsets[y + 1] - b.offsets[y];
     });
     for (const DevLayer &ly : m->layers) {
         const auto key = std::make_pair(ly.nkv, ly.hd);
-        if (b.tile_ranges.count(key)) continue;
+        if (g.tile_ranges.count(key)) continue;
         const int bv = attn_block_vectors(ly.hd);
         const int first = (int)b.tiles.size();
         if (bv > 0) {
             const int G = (int)(m->NH / ly.nkv);
             for (int r : order) {
                 const int64_t len = b.offsets[r + 1] - b.offsets[r];
-                for (int g = 0; g < ly.nkv; ++g)
+                const int32_t tok0 = (int32_t)(b.offsets[r] - g.t0);
+                for (int kv = 0; kv < ly.nkv; ++kv)
                     for (int64_t v0 = 0; v0 < len * G; v0 += bv)
-                        b.tiles.push_back({(int32_t)b.offsets[r], (int32_t)len, g, (int32_t)v0});
+                        b.tiles.push_back({tok0, (int32_t)len, kv, (int32_t)v0});
             }
         }
-        b.tile_ranges[key] = {first, (int)b.tiles.size() - first};
+        g.tile_ranges[key] = {first, (int)b.tiles.size() - first};
     }
     // algorithmic attention FLOPs: 4 * hd * nh * sum_i keys(i) per layer
     for (int t = 0; t < 2; ++t) {
         double f = 0;
         const int hd = m->type_hd[t];
         if (!hd) continue;
-        for (int r = 0; r < b.B; ++r) {
+        for (int r = g.r0; r < g.r0 + g.nrows; ++r) {
             const int64_t len = b.offsets[r + 1] - b.offsets[r];
             double keys = 0;
             if (t == 1 || m->window >= len) {
@@ -442,23 +466,46 @@ void build_tiles(const svl_text_model *m, Batch &b) {
             }
             f += 4.0 * hd * (double)m->NH * keys;
         }
-        b.attn_flops[t] = f;
+        g.attn_flops[t] = f;
+    }
+}
+
+void build_groups(const svl_text_model *m, Batch &b, bool allow_split) {
+    b.groups.clear();
+    b.tiles.clear();
+    b.dev_offsets.clear();
+    int32_t split = 0;
+    if (allow_split && b.B >= 2 && b.T >= SPLIT_MIN_TOKENS) {
+        // first row boundary at or past half the tokens, kept inside 1..B-1
+        split = 1;
+        while (split < b.B - 1 && 2 * b.offsets[split] < b.T) ++split;
+    }
+    if (split > 0) {
+        b.groups.resize(2);
+        b.groups[0].r0 = 0;
+        b.groups[0].nrows = split;
+        b.groups[1].r0 = split;
+        b.groups[1].nrows = b.B - split;
+    } else {
+        b.groups.resize(1);
+        b.groups[0].r0 = 0;
+        b.groups[0].nrows = b.B;
+    }
+    for (Group &g : b.groups) {
+        g.t0 = b.offsets[g.r0];
+        g.T = b.offsets[g.r0 + g.nrows] - g.t0;
+        build_group(m, b, g);
     }
 }
 
 svl_status ensure_workspace(svl_text_model *m, const Batch &b, int64_t feat_floats,
                             int dims_total) {
     const int64_t T = std::max<int64_t>(b.T, 1);
-    int64_t max_qkv = 0, max_q = 0;
-    for (const DevLayer &ly : m->layers) {
-        max_qkv = std::max<int64_t>(max_qkv, m->NH * ly.hd + 2 * ly.nkv * ly.hd);
-        max_q = std::max<int64_t>(max_q, m->NH * ly.hd);
-    }
     HIP_TRY(m->h.ensure(T * m->H));
     HIP_TRY(m->n.ensure(T * m->H));
     HIP_TRY(m->tmp.ensure(T * m->H));
-    HIP_TRY(m->qkv.ensure(T * max_qkv));
-    HIP_TRY(m->attn.ensure(T * max_q));
+    HIP_TRY(m->qkv.ensure(T * m->max_qkv));
+    HIP_TRY(m->attn.ensure(T * m->max_q));
     HIP_TRY(m->act.ensure(T * m->I));
     HIP_TRY(m->ple.ensure(T * m->L * m->P));
     HIP_TRY(m->pg.ensure(T * m->P));
@@ -466,7 +513,7 @@ svl_status ensure_workspace(svl_text_model *m, const Batch &b, int64_t feat_floa
     HIP_TRY(m->pos.ensure(T));
     HIP_TRY(m->rowlen.ensure(T));
     HIP_TRY(m->ids.ensure(T));
-    HIP_TRY(m->offsets.ensure(b.B + 1));
+    HIP_TRY(m->offsets.ensure(std::max<size_t>(b.dev_offsets.size(), 1)));
     HIP_TRY(m->tiles.ensure(std::max<size_t>(b.tiles.size(), 1)));
     HIP_TRY(m->pooled.ensure((size_t)b.B * m->E));
     HIP_TRY(m->normalized.ensure((size_t)b.B * m->E));
@@ -479,60 +526,70 @@ svl_status ensure_workspace(svl_text_model *m, const Batch &b, int64_t feat_floa
     return SVL_OK;
 }
 
-// The whole encoder for one packed batch, enqueued on `s`
-// (text.rs:209-531). Inputs already in m->ids / m->offsets / m->tiles
-// (and m->featmap / m->feats when has_features).
-svl_status enqueue_forward(svl_text_model *m, const Batch &b, hipStream_t s, const uint32_t *d_ids,
-                           bool has_features, const int32_t *d_dims, int n_dims, int dims_total,
-                           float *d_trunc, float *h_hidden) {
-    const int64_t T = b.T, H = m->H, P = m->P, L = m->L, E = m->E;
+// The whole encoder for one group of rows, enqueued on `s`
+// (text.rs:209-531). Inputs already in m->ids / m->offsets / m->tiles (and
+// m->featmap / m->feats when has_features). Every buffer is addressed at the
+// group's token (or row) range; the per-layer-width QKV and attention
+// buffers are carved at their widest layer so the groups never overlap.
+svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hipStream_t s,
+                         const uint32_t *d_ids, bool has_features, const int32_t *d_dims,
+                         int n_dims, int dims_total, float *d_trunc, float *h_hidden) {
+    const int64_t T = grp.T, H = m->H, P = m->P, L = m->L, E = m->E, t0 = grp.t0;
+    if (T == 0) return SVL_OK;
     int *flag = m->flag.p;
     const double Td = (double)T;
+    float *h = m->h.p + t0 * H, *n = m->n.p + t0 * H, *tmp = m->tmp.p + t0 * H;
+    float *qkv = m->qkv.p + t0 * m->max_qkv, *attn = m->attn.p + t0 * m->max_q;
+    float *act = m->act.p + t0 * m->I, *ple = m->ple.p + t0 * L * P, *pg = m->pg.p + t0 * P;
+    float *proj = m->proj.p + t0 * E;
+    int32_t *pos = m->pos.p + t0, *rowlen = m->rowlen.p + t0;
+    const int64_t *offs = m->offsets.p + grp.off_slot;
+    const int64_t T_all = b.T;
 
-    HIP_TRY(launch_positions(m->offsets.p, b.B, m->pos.p, m->rowlen.p, s));
+    HIP_TRY(launch_positions(offs, grp.nrows, pos, rowlen, s));
     {
         Timer tm(m, s, KC_GATHER, Td * H * 4 * 3);
-        HIP_TRY(launch_gather(d_ids, m->embed, m->V, has_features ? m->featmap.p : nullptr,
+        HIP_TRY(launch_gather(d_ids + t0, m->embed, m->V, has_features ? m->featmap.p + t0 : nullptr,
                               has_features ? m->feats.p : nullptr, m->embedding_scale,
-                              m->layers[0].ln_in, m->h.p, m->n.p, T, (int)H, m->eps, flag, s));
+                              m->layers[0].ln_in, h, n, T, (int)H, m->eps, flag, s));
     }
     if (h_hidden)
-        HIP_TRY(hipMemcpyAsync(h_hidden, m->h.p, (size_t)(T * H) * 4, hipMemcpyDeviceToHost, s));
+        HIP_TRY(hipMemcpyAsync(h_hidden + t0 * H, h, (size_t)(T * H) * 4, hipMemcpyDeviceToHost,
+                               s));
 
     // Projection-only per-layer embeddings (text.rs:285-306).
     {
-        GemmArgs g{m->h.p, H, m->ple_model, H, m->ple.p, L * P, (int)T, (int)(L * P), (int)H,
-                   EPI_SCALE, m->ple_scale, nullptr, 0, 0};
+        GemmArgs g{h, H, m->ple_model, H, ple, L * P, (int)T, (int)(L * P), (int)H, EPI_SCALE,
+                   m->ple_scale, nullptr, 0, 0};
         Timer tm(m, s, KC_GEMM_PLE_MODEL, 2.0 * Td * H * L * P);
         HIP_TRY(launch_gemm(g, s));
     }
     {
         Timer tm(m, s, KC_PLE_NORM, Td * L * P * 8);
-        HIP_TRY(launch_rms_rows(m->ple.p, m->ple_norm, m->ple.p, T * L, (int)P, m->eps, flag, s));
+        HIP_TRY(launch_rms_rows(ple, m->ple_norm, ple, T * L, (int)P, m->eps, flag, s));
     }
 
     for (int64_t l = 0; l < L; ++l) {
         const DevLayer &ly = m->layers[(size_t)l];
         const int64_t qd = m->NH * ly.hd, kd = (int64_t)ly.nkv * ly.hd, ldqkv = qd + 2 * kd;
         {
-            GemmArgs g{m->n.p, H, ly.w_qkv, H, m->qkv.p, ldqkv, (int)T, (int)ldqkv, (int)H,
-                       EPI_STORE, 1.f, nullptr, 0, 0};
+            GemmArgs g{n, H, ly.w_qkv, H, qkv, ldqkv, (int)T, (int)ldqkv, (int)H, EPI_STORE, 1.f,
+                       nullptr, 0, 0};
             Timer tm(m, s, KC_GEMM_QKV, 2.0 * Td * H * ldqkv);
             HIP_TRY(launch_gemm(g, s));
         }
         {
             Timer tm(m, s, KC_QKV_POST, Td * ldqkv * 8);
-            HIP_TRY(launch_qkv_post(m->qkv.p, ldqkv, T, (int)m->NH, ly.nkv, ly.hd, ly.q_norm,
-                                    ly.k_norm, m->cos_t[ly.full], m->sin_t[ly.full], m->pos.p,
-                                    m->eps, flag, s));
+            HIP_TRY(launch_qkv_post(qkv, ldqkv, T, (int)m->NH, ly.nkv, ly.hd, ly.q_norm, ly.k_norm,
+                                    m->cos_t[ly.full], m->sin_t[ly.full], pos, m->eps, flag, s));
         }
         {
-            const auto range = b.tile_ranges.at(std::make_pair(ly.nkv, ly.hd));
+            const auto range = grp.tile_ranges.at(std::make_pair(ly.nkv, ly.hd));
             AttnArgs a{};
-            a.q = m->qkv.p;
-            a.k = m->qkv.p + qd;
-            a.v = m->qkv.p + qd + kd;
-            a.out = m->attn.p;
+            a.q = qkv;
+            a.k = qkv + qd;
+            a.v = qkv + qd + kd;
+            a.out = attn;
             a.ldq = a.ldk = a.ldv = ldqkv;
             a.ldo = qd;
             a.nh = (int)m->NH;
@@ -542,75 +599,97 @@ svl_status enqueue_forward(svl_text_model *m, const Batch &b, hipStream_t s, con
             a.scale = 1.0f;  // text.rs:421
             a.tiles = m->tiles.p + range.first;
             a.n_tiles = range.second;
-            a.pos = m->pos.p;
-            a.rowlen = m->rowlen.p;
+            a.pos = pos;
+            a.rowlen = rowlen;
             a.tokens = T;
             a.flag = flag;
-            Timer tm(m, s, KC_ATTENTION, b.attn_flops[ly.full]);
+            Timer tm(m, s, KC_ATTENTION, grp.attn_flops[ly.full]);
             HIP_TRY(launch_attention(a, s));
         }
         {
-            GemmArgs g{m->attn.p, qd, ly.w_o, qd, m->tmp.p, H, (int)T, (int)H, (int)qd, EPI_STORE,
-                       1.f, nullptr, 0, 0};
+            GemmArgs g{attn, qd, ly.w_o, qd, tmp, H, (int)T, (int)H, (int)qd, EPI_STORE, 1.f,
+                       nullptr, 0, 0};
             Timer tm(m, s, KC_GEMM_O, 2.0 * Td * qd * H);
             HIP_TRY(launch_gemm(g, s));
         }
         {
             Timer tm(m, s, KC_RESNORM, Td * H * 4 * 4);
-            HIP_TRY(launch_resnorm(m->tmp.p, ly.ln_post_attn, m->h.p, m->h.p, ly.ln_pre_ff, m->n.p,
-                                   1.0f, T, (int)H, m->eps, flag, s));
+            HIP_TRY(launch_resnorm(tmp, ly.ln_post_attn, h, h, ly.ln_pre_ff, n, 1.0f, T, (int)H,
+                                   m->eps, flag, s));
         }
         {
-            GemmArgs g{m->n.p, H, ly.w_gu, H, m->act.p, m->I, (int)T, (int)(2 * m->I_pad), (int)H,
-                       EPI_GEGLU, 1.f, nullptr, 0, (int)m->I};
+            GemmArgs g{n, H, ly.w_gu, H, act, m->I, (int)T, (int)(2 * m->I_pad), (int)H, EPI_GEGLU,
+                       1.f, nullptr, 0, (int)m->I};
             Timer tm(m, s, KC_GEMM_GATE_UP, 2.0 * Td * H * 2 * m->I);
             HIP_TRY(launch_gemm(g, s));
         }
         {
-            GemmArgs g{m->act.p, m->I, ly.w_down, m->I, m->tmp.p, H, (int)T, (int)H, (int)m->I,
-                       EPI_STORE, 1.f, nullptr, 0, 0};
+            GemmArgs g{act, m->I, ly.w_down, m->I, tmp, H, (int)T, (int)H, (int)m->I, EPI_STORE,
+                       1.f, nullptr, 0, 0};
             Timer tm(m, s, KC_GEMM_DOWN, 2.0 * Td * m->I * H);
             HIP_TRY(launch_gemm(g, s));
         }
         {
             Timer tm(m, s, KC_RESNORM, Td * H * 4 * 3);
-            HIP_TRY(launch_resnorm(m->tmp.p, ly.ln_post_ff, m->h.p, m->h.p, nullptr, nullptr, 1.0f,
-                                   T, (int)H, m->eps, flag, s));
+            HIP_TRY(launch_resnorm(tmp, ly.ln_post_ff, h, h, nullptr, nullptr, 1.0f, T, (int)H,
+                                   m->eps, flag, s));
         }
         {
-            GemmArgs g{m->h.p, H, ly.w_pg, H, m->pg.p, P, (int)T, (int)P, (int)H, EPI_GELU_MUL,
-                       1.f, m->ple.p + l * P, L * P, 0};
+            GemmArgs g{h, H, ly.w_pg, H, pg, P, (int)T, (int)P, (int)H, EPI_GELU_MUL, 1.f,
+                       ple + l * P, L * P, 0};
             Timer tm(m, s, KC_GEMM_PLE_GATE, 2.0 * Td * H * P);
             HIP_TRY(launch_gemm(g, s));
         }
         {
-            GemmArgs g{m->pg.p, P, ly.w_pp, P, m->tmp.p, H, (int)T, (int)H, (int)P, EPI_STORE,
-                       1.f, nullptr, 0, 0};
+            GemmArgs g{pg, P, ly.w_pp, P, tmp, H, (int)T, (int)H, (int)P, EPI_STORE, 1.f, nullptr,
+                       0, 0};
             Timer tm(m, s, KC_GEMM_PLE_PROJ, 2.0 * Td * P * H);
             HIP_TRY(launch_gemm(g, s));
         }
         {
             const float *next = l + 1 < L ? m->layers[(size_t)l + 1].ln_in : m->final_norm;
             Timer tm(m, s, KC_RESNORM, Td * H * 4 * 4);
-            HIP_TRY(launch_resnorm(m->tmp.p, ly.ln_post_ple, m->h.p, m->h.p, next, m->n.p,
-                                   ly.scalar, T, (int)H, m->eps, flag, s));
+            HIP_TRY(launch_resnorm(tmp, ly.ln_post_ple, h, h, next, n, ly.scalar, T, (int)H,
+                                   m->eps, flag, s));
         }
         if (h_hidden)
-            HIP_TRY(hipMemcpyAsync(h_hidden + (size_t)((l + 1) * T * H), m->h.p,
+            HIP_TRY(hipMemcpyAsync(h_hidden + (size_t)((l + 1) * T_all * H + t0 * H), h,
                                    (size_t)(T * H) * 4, hipMemcpyDeviceToHost, s));
     }
 
     // Final norm (fused above), projection, pooling (text.rs:520-531).
     {
-        GemmArgs g{m->n.p, H, m->out_proj, H, m->proj.p, E, (int)T, (int)E, (int)H, EPI_STORE,
-                   1.f, nullptr, 0, 0};
+        GemmArgs g{n, H, m->out_proj, H, proj, E, (int)T, (int)E, (int)H, EPI_STORE, 1.f, nullptr,
+                   0, 0};
         Timer tm(m, s, KC_GEMM_OUT, 2.0 * Td * H * E);
         HIP_TRY(launch_gemm(g, s));
     }
     {
         Timer tm(m, s, KC_POOL, Td * E * 4);
-        HIP_TRY(launch_pool(m->proj.p, (int)E, m->offsets.p, b.B, d_dims, n_dims, dims_total,
-                            m->pooled.p, m->normalized.p, d_trunc, flag, s));
+        HIP_TRY(launch_pool(proj, (int)E, offs, grp.nrows, d_dims, n_dims, dims_total,
+                            m->pooled.p + (int64_t)grp.r0 * E,
+                            m->normalized.p + (int64_t)grp.r0 * E,
+                            d_trunc ? d_trunc + (int64_t)grp.r0 * dims_total : nullptr, flag, s));
+    }
+    return SVL_OK;
+}
+
+// Enqueues every group: group 0 on s0, group 1 (if any) on the model's
+// second stream, which waits for everything s0 has enqueued so far and is
+// joined back into s0 at the end.
+svl_status enqueue_forward(svl_text_model *m, const Batch &b, hipStream_t s0,
+                           const uint32_t *d_ids, bool has_features, const int32_t *d_dims,
+                           int n_dims, int dims_total, float *d_trunc, float *h_hidden) {
+    if (b.groups.size() > 1) {
+        HIP_TRY(hipEventRecord(m->ev_fork, s0));
+        HIP_TRY(hipStreamWaitEvent(m->stream2, m->ev_fork, 0));
+    }
+    for (size_t gi = 0; gi < b.groups.size(); ++gi)
+        ST_TRY(enqueue_group(m, b, b.groups[gi], gi == 0 ? s0 : m->stream2, d_ids, has_features,
+                             d_dims, n_dims, dims_total, d_trunc, h_hidden));
+    if (b.groups.size() > 1) {
+        HIP_TRY(hipEventRecord(m->ev_join, m->stream2));
+        HIP_TRY(hipStreamWaitEvent(s0, m->ev_join, 0));
     }
     return SVL_OK;
 }
@@ -670,13 +749,13 @@ svl_status prepare_batch(svl_text_model *m, const int64_t *offsets, int32_t batc
         if (offsets[r + 1] < offsets[r]) return fail(SVL_USAGE, "offsets must not decrease");
     b.T = offsets[batch];
     if (b.T > (int64_t)INT32_MAX / 8) return fail(SVL_LIMIT, "batch holds too many tokens");
-    build_tiles(m, b);
+    build_groups(m, b, m->split_streams);
     return SVL_OK;
 }
 
 svl_status upload_batch_meta(svl_text_model *m, const Batch &b, hipStream_t s) {
-    HIP_TRY(hipMemcpyAsync(m->offsets.p, b.offsets.data(), (b.B + 1) * sizeof(int64_t),
-                           hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(m->offsets.p, b.dev_offsets.data(),
+                           b.dev_offsets.size() * sizeof(int64_t), hipMemcpyHostToDevice, s));
     if (!b.tiles.empty())
         HIP_TRY(hipMemcpyAsync(m->tiles.p, b.tiles.data(), b.tiles.size() * sizeof(AttnTile),
                                hipMemcpyHostToDevice, s));
@@ -923,7 +1002,14 @@ svl_status svl_text_model_create(svl_ctx *ctx, const svl_text_config *cfg,
         HIP_TRY(hipMemcpy(m->cos_t[t], cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
         HIP_TRY(hipMemcpy(m->sin_t[t], sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
     }
+    for (const DevLayer &ly : m->layers) {
+        m->max_qkv = std::max<int64_t>(m->max_qkv, m->NH * ly.hd + 2 * (int64_t)ly.nkv * ly.hd);
+        m->max_q = std::max<int64_t>(m->max_q, m->NH * ly.hd);
+    }
     HIP_TRY(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+    HIP_TRY(hipStreamCreateWithFlags(&m->stream2, hipStreamNonBlocking));
+    HIP_TRY(hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming));
+    HIP_TRY(hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming));
     HIP_TRY(hipHostMalloc((void **)&m->h_flag, sizeof(int), hipHostMallocDefault));
     *out = guard.release();
     return SVL_OK;
@@ -1064,6 +1150,13 @@ svl_status svl_text_embed_ids(svl_text_model *m, const uint32_t *ids, int64_t n,
     ST_TRY(svl_text_forward_batch(m, ids ? ids : empty_ids, offs, 1, nullptr, normalized.data(),
                                   nullptr, nullptr, nullptr));
     return svl_truncate_and_normalize(normalized.data(), (size_t)m->E, (size_t)dimension, out);
+}
+
+svl_status svl_text_model_set_stream_split(svl_text_model *m, int enable) {
+    if (!m) return fail(SVL_USAGE, "model is null");
+    std::lock_guard<std::mutex> lock(m->mu);
+    m->split_streams = enable != 0;
+    return SVL_OK;
 }
 
 svl_status svl_text_model_set_kernel_timing(svl_text_model *m, int enable) {

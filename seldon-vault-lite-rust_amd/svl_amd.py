@@ -93,7 +93,8 @@ class _FeatureSpan(ctypes.Structure):
 EXPORTED = [
     "svl_init", "svl_shutdown", "svl_last_error", "svl_text_model_create",
     "svl_text_model_destroy", "svl_text_forward_batch", "svl_text_forward_device",
-    "svl_text_embed_ids", "svl_truncate_and_normalize", "svl_text_model_set_kernel_timing",
+    "svl_text_embed_ids", "svl_truncate_and_normalize", "svl_text_model_set_stream_split",
+    "svl_text_model_set_kernel_timing",
     "svl_kernel_class_count", "svl_kernel_class_name", "svl_text_model_kernel_stats",
     "svl_linear", "svl_rms_norm_rows", "svl_rope_with_inv_freq", "svl_rope_inv_freq",
     "svl_bidirectional_attention", "svl_gelu_tanh", "svl_geglu", "svl_add", "svl_mean_pool",
@@ -148,6 +149,7 @@ def lib():
         L.svl_text_embed_ids.argtypes = [vp, vp, i64, i64, vp]
         L.svl_truncate_and_normalize.argtypes = [vp, ctypes.c_size_t, ctypes.c_size_t, vp]
         L.svl_text_model_set_kernel_timing.argtypes = [vp, ctypes.c_int]
+        L.svl_text_model_set_stream_split.argtypes = [vp, ctypes.c_int]
         L.svl_text_model_kernel_stats.argtypes = [vp, vp, vp, vp]
         L.svl_linear.argtypes = [vp, vp, i64, i64, i64, vp, vp]
         L.svl_rms_norm_rows.argtypes = [vp, vp, i64, i64, f32, vp, vp]
@@ -606,6 +608,10 @@ class TextModel:
         _check(lib().svl_text_embed_ids(self.handle, _ptr(ids) if ids.size else None, ids.size,
                                         int(dimension), _ptr(out)))
         return out[:dimension]
+
+    def set_stream_split(self, enable: bool):
+        """Large batches as two row groups on two streams (default) or one."""
+        _check(lib().svl_text_model_set_stream_split(self.handle, 1 if enable else 0))
 
     def set_kernel_timing(self, enable: bool):
         _check(lib().svl_text_model_set_kernel_timing(self.handle, 1 if enable else 0))

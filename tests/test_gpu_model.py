@@ -147,6 +147,24 @@ def test_packed_batch_equals_independent_calls_bit_for_bit():
         assert a.normalized().tobytes() == b.normalized().tobytes()
 
 
+def test_two_stream_row_groups_are_bit_identical():
+    # Batches above 4096 tokens run as two row groups on two streams.
+    cfg = svl_synth.config_a(layers=2, vocab=4096)
+    w = svl_synth.weights(cfg)
+    m = model(cfg, w)
+    rows = svl_synth.token_rows(4096, [512, 300, 700, 1024, 100, 900, 800, 513, 64])
+    assert sum(len(r) for r in rows) >= 4096
+    split = m.forward_batch(rows, capture_hidden=True)
+    m.set_stream_split(False)
+    single = m.forward_batch(rows, capture_hidden=True)
+    m.set_stream_split(True)
+    for a, b in zip(split, single):
+        assert a.normalized().tobytes() == b.normalized().tobytes()
+        assert a.hidden_states().tobytes() == b.hidden_states().tobytes()
+    for r, a in zip(rows[:3], split[:3]):
+        assert m.forward(r).normalized().tobytes() == a.normalized().tobytes()
+
+
 def test_features_replace_rows_like_the_reference():  # text.rs:226-275
     cfg = svl_synth.config_a(layers=3, vocab=4096)
     w = svl_synth.weights(cfg)
