@@ -44,6 +44,8 @@ def parse():
                     help="rows of the workload timed on the CPU oracle (default: one per core, "
                          "at most 16; 0 skips the CPU baseline)")
     ap.add_argument("--t1-runs", type=int, default=20)
+    ap.add_argument("--row-groups", type=int, default=3,
+                    help="row groups (streams) the batch is split into")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (3 times), the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -128,6 +130,8 @@ def main():
     out = torch.zeros((BATCH, sum(DIMS)), dtype=torch.float32, device="cuda:0")
     stream = torch.cuda.current_stream()
 
+    model.set_stream_split(args.row_groups)
+
     def step():
         model.forward_device(ids.data_ptr(), offsets, DIMS, out.data_ptr(), stream.cuda_stream)
 
@@ -160,7 +164,7 @@ def main():
     single_stream_ms = (time.perf_counter() - k0) * 1e3 / args.steps
     stats = model.kernel_stats()
     model.set_kernel_timing(False)
-    model.set_stream_split(True)
+    model.set_stream_split(args.row_groups)
 
     value = BATCH * args.steps / elapsed
     ms_per_step = elapsed * 1e3 / args.steps
@@ -214,7 +218,8 @@ def main():
                                "layers, 3 q heads / 1 KV head, head_dim 256, GeGLU 1152, PLE 256, "
                                "vocab 262144): batch 64 rows, lengths U[64,512], padding masked, "
                                "Matryoshka outputs 768/512/256/128",
-                   "batch": BATCH, "tokens": T, "max_seq_len": LEN_HI, "parallelism": "single GPU"},
+                   "batch": BATCH, "tokens": T, "max_seq_len": LEN_HI, "parallelism": "single GPU",
+                   "row_groups": args.row_groups},
         "p50_ms": round(p50, 3),
         "t1_p50_ms": round(float(np.median(lat)), 3) if lat else None,
         "gemm_tflops": round(gemm_tflops, 3),

@@ -149,12 +149,12 @@ svl_status svl_text_embed_ids(svl_text_model *model, const uint32_t *ids, int64_
 svl_status svl_truncate_and_normalize(const float *values, size_t n, size_t dimension,
                                       float *out);
 
-/* Large batches run as two groups of rows on two streams of the model (the
- * second waits for the caller's stream and is joined back into it), so one
- * group's kernels fill the GPU while the other's drain. enable = 0 runs
- * every batch as one group on one stream (default: enabled). Results are
- * bit-identical either way. */
-svl_status svl_text_model_set_stream_split(svl_text_model *model, int enable);
+/* Batches of 4096 tokens or more run as `groups` groups of rows (1..4,
+ * default 3), group 0 on the caller's stream and the others on streams of
+ * the model that wait for it and are joined back into it, so one group's
+ * kernels fill the GPU while another's drain. groups <= 1 runs every batch
+ * as one group on one stream. Results are bit-identical for any setting. */
+svl_status svl_text_model_set_stream_split(svl_text_model *model, int groups);
 
 /* Per-kernel GPU time of the last forward call, when enabled: one entry per
  * kernel class (see svl_kernel_class_name). Used by the benchmark to relate

@@ -149,9 +149,10 @@ struct svl_text_model {
 
     int64_t max_qkv = 0, max_q = 0;  // widest per-layer QKV / query row
     hipStream_t stream = nullptr;
-    hipStream_t stream2 = nullptr;   // second group of rows
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
-    bool split_streams = true;
+    static constexpr int MAX_GROUPS = 4;
+    hipStream_t extra[MAX_GROUPS - 1] = {};  // streams of row groups 1..3
+    hipEvent_t ev_fork = nullptr, ev_join[MAX_GROUPS - 1] = {};
+    int row_groups = 3;                      // row groups per large batch
     std::mutex mu;
 
     // workspace
@@ -190,8 +191,10 @@ struct svl_text_model {
             (void)hipEventDestroy(t.b);
         }
         if (ev_fork) (void)hipEventDestroy(ev_fork);
-        if (ev_join) (void)hipEventDestroy(ev_join);
-        if (stream2) (void)hipStreamDestroy(stream2);
+        for (int i = 0; i < MAX_GROUPS - 1; ++i) {
+            if (ev_join[i]) (void)hipEventDestroy(ev_join[i]);
+            if (extra[i]) (void)hipStreamDestroy(extra[i]);
+        }
         if (stream) (void)hipStreamDestroy(stream);
     }
 };
@@ -396,12 +399,12 @@ void collect_timing(svl_text_model *m) {
 // ---------------------------------------------------------------------------
 // Per-call geometry.
 //
-// A batch is cut into at most two groups of consecutive rows with about the
+// A large batch is cut into a few groups of consecutive rows with about the
 // same number of tokens. Each group runs the whole encoder on its own stream
-// (both at the default priority), on its own token range of every workspace
-// buffer, so the two streams' kernels fill each other's partial last rounds
-// of workgroups and the bandwidth-bound norm kernels of one group overlap the
-// MFMA-bound GEMMs of the other. Every row's arithmetic is unchanged.
+// (all at the default priority), on its own token range of every workspace
+// buffer, so the streams' kernels fill each other's partial last rounds of
+// workgroups and the bandwidth-bound norm kernels of one group overlap the
+// MFMA-bound GEMMs of another. Every row's arithmetic is unchanged.
 
 constexpr int64_t SPLIT_MIN_TOKENS = 4096;
 
@@ -470,26 +473,27 @@ void build_group(const svl_text_model *m, Batch &b, Group &g) {
     }
 }
 
-void build_groups(const svl_text_model *m, Batch &b, bool allow_split) {
+void build_groups(const svl_text_model *m, Batch &b, int max_groups) {
     b.groups.clear();
     b.tiles.clear();
     b.dev_offsets.clear();
-    int32_t split = 0;
-    if (allow_split && b.B >= 2 && b.T >= SPLIT_MIN_TOKENS) {
-        // first row boundary at or past half the tokens, kept inside 1..B-1
-        split = 1;
-        while (split < b.B - 1 && 2 * b.offsets[split] < b.T) ++split;
-    }
-    if (split > 0) {
-        b.groups.resize(2);
-        b.groups[0].r0 = 0;
-        b.groups[0].nrows = split;
-        b.groups[1].r0 = split;
-        b.groups[1].nrows = b.B - split;
-    } else {
-        b.groups.resize(1);
-        b.groups[0].r0 = 0;
-        b.groups[0].nrows = b.B;
+    int ng = 1;
+    if (b.T >= SPLIT_MIN_TOKENS) ng = std::max(1, std::min<int>(max_groups, b.B));
+    // group k starts at the first row boundary at or past k/ng of the tokens,
+    // every group keeping at least one row
+    int32_t r = 0;
+    for (int k = 0; k < ng; ++k) {
+        int32_t end = b.B;
+        if (k + 1 < ng) {
+            end = std::max(r + 1, 1);
+            while (end < b.B - (ng - 1 - k) && (int64_t)ng * b.offsets[end] < (int64_t)(k + 1) * b.T)
+                ++end;
+        }
+        Group g;
+        g.r0 = r;
+        g.nrows = end - r;
+        b.groups.push_back(g);
+        r = end;
     }
     for (Group &g : b.groups) {
         g.t0 = b.offsets[g.r0];
@@ -674,22 +678,24 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
     return SVL_OK;
 }
 
-// Enqueues every group: group 0 on s0, group 1 (if any) on the model's
-// second stream, which waits for everything s0 has enqueued so far and is
-// joined back into s0 at the end.
+// Enqueues every group: group 0 on s0, group k > 0 on the model's stream k,
+// which waits for everything s0 has enqueued so far and is joined back into
+// s0 at the end.
 svl_status enqueue_forward(svl_text_model *m, const Batch &b, hipStream_t s0,
                            const uint32_t *d_ids, bool has_features, const int32_t *d_dims,
                            int n_dims, int dims_total, float *d_trunc, float *h_hidden) {
-    if (b.groups.size() > 1) {
+    const size_t ng = b.groups.size();
+    if (ng > 1) {
         HIP_TRY(hipEventRecord(m->ev_fork, s0));
-        HIP_TRY(hipStreamWaitEvent(m->stream2, m->ev_fork, 0));
+        for (size_t gi = 1; gi < ng; ++gi)
+            HIP_TRY(hipStreamWaitEvent(m->extra[gi - 1], m->ev_fork, 0));
     }
-    for (size_t gi = 0; gi < b.groups.size(); ++gi)
-        ST_TRY(enqueue_group(m, b, b.groups[gi], gi == 0 ? s0 : m->stream2, d_ids, has_features,
-                             d_dims, n_dims, dims_total, d_trunc, h_hidden));
-    if (b.groups.size() > 1) {
-        HIP_TRY(hipEventRecord(m->ev_join, m->stream2));
-        HIP_TRY(hipStreamWaitEvent(s0, m->ev_join, 0));
+    for (size_t gi = 0; gi < ng; ++gi)
+        ST_TRY(enqueue_group(m, b, b.groups[gi], gi == 0 ? s0 : m->extra[gi - 1], d_ids,
+                             has_features, d_dims, n_dims, dims_total, d_trunc, h_hidden));
+    for (size_t gi = 1; gi < ng; ++gi) {
+        HIP_TRY(hipEventRecord(m->ev_join[gi - 1], m->extra[gi - 1]));
+        HIP_TRY(hipStreamWaitEvent(s0, m->ev_join[gi - 1], 0));
     }
     return SVL_OK;
 }
@@ -749,7 +755,7 @@ svl_status prepare_batch(svl_text_model *m, const int64_t *offsets, int32_t batc
         if (offsets[r + 1] < offsets[r]) return fail(SVL_USAGE, "offsets must not decrease");
     b.T = offsets[batch];
     if (b.T > (int64_t)INT32_MAX / 8) return fail(SVL_LIMIT, "batch holds too many tokens");
-    build_groups(m, b, m->split_streams);
+    build_groups(m, b, m->row_groups);
     return SVL_OK;
 }
 
@@ -1007,9 +1013,11 @@ svl_status svl_text_model_create(svl_ctx *ctx, const svl_text_config *cfg,
         m->max_q = std::max<int64_t>(m->max_q, m->NH * ly.hd);
     }
     HIP_TRY(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
-    HIP_TRY(hipStreamCreateWithFlags(&m->stream2, hipStreamNonBlocking));
     HIP_TRY(hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming));
-    HIP_TRY(hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming));
+    for (int i = 0; i < svl_text_model::MAX_GROUPS - 1; ++i) {
+        HIP_TRY(hipStreamCreateWithFlags(&m->extra[i], hipStreamNonBlocking));
+        HIP_TRY(hipEventCreateWithFlags(&m->ev_join[i], hipEventDisableTiming));
+    }
     HIP_TRY(hipHostMalloc((void **)&m->h_flag, sizeof(int), hipHostMallocDefault));
     *out = guard.release();
     return SVL_OK;
@@ -1155,7 +1163,7 @@ svl_status svl_text_embed_ids(svl_text_model *m, const uint32_t *ids, int64_t n,
 svl_status svl_text_model_set_stream_split(svl_text_model *m, int enable) {
     if (!m) return fail(SVL_USAGE, "model is null");
     std::lock_guard<std::mutex> lock(m->mu);
-    m->split_streams = enable != 0;
+    m->row_groups = std::max(1, std::min(enable, svl_text_model::MAX_GROUPS));
     return SVL_OK;
 }
 

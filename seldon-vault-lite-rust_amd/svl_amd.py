@@ -609,9 +609,11 @@ class TextModel:
                                         int(dimension), _ptr(out)))
         return out[:dimension]
 
-    def set_stream_split(self, enable: bool):
-        """Large batches as two row groups on two streams (default) or one."""
-        _check(lib().svl_text_model_set_stream_split(self.handle, 1 if enable else 0))
+    def set_stream_split(self, groups):
+        """Row groups (1..4, each on its own stream) for batches of 4096+
+        tokens; True = 3 (the default), False = 1."""
+        g = 3 if groups is True else (1 if groups is False else int(groups))
+        _check(lib().svl_text_model_set_stream_split(self.handle, g))
 
     def set_kernel_timing(self, enable: bool):
         _check(lib().svl_text_model_set_kernel_timing(self.handle, 1 if enable else 0))
