@@ -203,6 +203,85 @@ svl_status svl_mean_pool(const float *d_values, int64_t rows, int64_t width, flo
                          void *stream);
 svl_status svl_l2_normalize(const float *d_in, int64_t n, float *d_out, void *stream);
 
+/* ---- vision tower and image prompts --------------------------------------- */
+
+typedef struct svl_vision_model svl_vision_model;
+
+/* Validated vision configuration (src/model/vision.rs:58-70 VisionConfig;
+ * patch_size 16 and pooling_kernel_size 3 are fixed, vision.rs:174-183). */
+typedef struct {
+    int64_t hidden_size;
+    int64_t intermediate_size;
+    int64_t num_hidden_layers;
+    int64_t num_attention_heads;
+    int64_t num_key_value_heads;
+    int64_t head_dim;
+    int64_t position_embedding_size;
+    double rms_norm_eps;
+    double rope_theta;
+} svl_vision_config;
+
+/* One preprocessed image (src/media/preprocess.rs:87-147 ImagePatches).
+ * Only the first valid_patches rows are read, as VisionModel::forward does
+ * (vision.rs:742-809): pixel_values [valid_patches, 768] (16x16x3 values per
+ * patch), positions [valid_patches, 2] patch-grid (x, y). */
+typedef struct {
+    const float *pixel_values;
+    const int32_t *positions;
+    int64_t valid_patches;
+    int64_t max_patches;
+    int64_t grid_width;
+    int64_t grid_height;
+    int64_t soft_tokens;
+} svl_image_patches;
+
+/* src/model/image.rs:30-44 ImageSpecialTokens. */
+typedef struct {
+    uint32_t bos, eos, pad, boi, image, eoi;
+} svl_image_special_tokens;
+
+/* Validates the inventory like VisionWeights::decode (vision.rs:556-610):
+ * unexpected vision_tower. / embed_vision. tensors, missing or mis-shaped
+ * ones -> CORRUPT; packs the weights into HBM. Replaces VisionModel::new
+ * (vision.rs:701-723) with its weights; text_hidden is the width of the
+ * embedding projection's output. */
+svl_status svl_vision_model_create(svl_ctx *ctx, const svl_vision_config *cfg,
+                                   int64_t text_hidden, const svl_tensor_view *tensors,
+                                   size_t n_tensors, svl_vision_model **out);
+svl_status svl_vision_model_destroy(svl_vision_model *model);
+
+/* VisionModel::forward (vision.rs:742-959) for `batch` images at once; image
+ * i's result equals the reference's forward(image i).
+ *  out_soft    [sum soft_tokens, text_hidden]  (VisionOutput::pooled of each
+ *              image, images back to back)
+ *  out_hidden  NULL or [num_hidden_layers + 1, sum valid_patches, hidden]
+ *              (VisionOutput::hidden_states, images back to back per layer)
+ * Validation follows the reference's order: zero patches -> CORRUPT, a
+ * position outside the table -> CORRUPT, negative positions and an
+ * inconsistent pooling geometry -> INTERNAL, a non-finite value -> INTERNAL. */
+svl_status svl_vision_forward_batch(svl_vision_model *model, const svl_image_patches *images,
+                                    int32_t batch, float *out_soft, float *out_hidden);
+
+/* Device-resident variant: d_pixels holds the images' patches back to back
+ * in HBM ([sum valid_patches, 768]; the library rescales them in place);
+ * images[i].pixel_values is ignored, positions stay on the host. Soft tokens
+ * go to d_out [sum soft_tokens, text_hidden] on `stream` (NULL = the model's
+ * stream); the call returns after the stream has drained. */
+svl_status svl_vision_forward_device(svl_vision_model *model, float *d_pixels,
+                                     const svl_image_patches *images, int32_t batch,
+                                     float *d_out, void *stream);
+
+/* ImageEmbedder::embed_impl (image.rs:209-253) for `batch` images: the
+ * vision tower, then the prompt <bos> <boi> <image> x soft_tokens <eoi>
+ * <eos> through the text model with the soft tokens replacing positions
+ * [2, 2 + soft_tokens) (text.rs forward_with_features), then
+ * ForwardOutput::embedding(dimension). out [batch, dimension]. The soft
+ * tokens stay in HBM between the two models. */
+svl_status svl_image_embed_batch(svl_vision_model *vision, svl_text_model *text,
+                                 const svl_image_special_tokens *tokens,
+                                 const svl_image_patches *images, int32_t batch,
+                                 int64_t dimension, float *out);
+
 /* ---- deterministic synthetic data (benchmark and tests) ------------------ */
 /* Counter-based SplitMix64: element i of stream s under seed k is
  * u = (splitmix64(k ^ (s * 0x9E3779B97F4A7C15) + i) >> 40) / 2^24 in [0, 1),

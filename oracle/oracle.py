@@ -299,3 +299,147 @@ class OracleTextModel:
         threads = threads or min(len(rows), os.cpu_count() or 1)
         with ThreadPoolExecutor(max_workers=threads) as ex:
             return list(ex.map(lambda r: self.forward(r), rows))
+
+
+# ---- vision tower (src/model/vision.rs) -------------------------------------------
+
+VISION_GLOBAL_TENSORS = 2
+VISION_LAYER_TENSORS = 13
+VISION_LAYER_NAMES = [
+    "input_layernorm.weight",
+    "post_attention_layernorm.weight",
+    "pre_feedforward_layernorm.weight",
+    "post_feedforward_layernorm.weight",
+    "self_attn.q_proj.linear.weight",
+    "self_attn.k_proj.linear.weight",
+    "self_attn.v_proj.linear.weight",
+    "self_attn.o_proj.linear.weight",
+    "self_attn.q_norm.weight",
+    "self_attn.k_norm.weight",
+    "mlp.gate_proj.linear.weight",
+    "mlp.up_proj.linear.weight",
+    "mlp.down_proj.linear.weight",
+]
+
+
+def vision_tensor_names(num_layers: int) -> list[str]:
+    """Names in VisionConfig::tensor_shapes order (vision.rs:345-414)."""
+    names = ["vision_tower.patch_embedder.input_proj.weight",
+             "vision_tower.patch_embedder.position_embedding_table"]
+    for i in range(num_layers):
+        names += [f"vision_tower.encoder.layers.{i}.{n}" for n in VISION_LAYER_NAMES]
+    names.append("embed_vision.embedding_projection.weight")
+    return names
+
+
+class _VisCfg(ctypes.Structure):
+    _fields_ = [
+        ("hidden_size", ctypes.c_int64),
+        ("intermediate_size", ctypes.c_int64),
+        ("num_hidden_layers", ctypes.c_int64),
+        ("num_attention_heads", ctypes.c_int64),
+        ("num_key_value_heads", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("position_embedding_size", ctypes.c_int64),
+        ("rms_norm_eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float),
+    ]
+
+
+def _vision_lib():
+    L = lib()
+    if not getattr(L, "_vision_ready", False):
+        f = ctypes.POINTER(ctypes.c_float)
+        i32 = ctypes.POINTER(ctypes.c_int32)
+        sz = ctypes.c_size_t
+        L.svlo_axial_inv_freq.argtypes = [sz, ctypes.c_float, f]
+        L.svlo_axial_rope.argtypes = [f, sz, sz, sz, i32, sz, f, sz]
+        L.svlo_pool_patches.argtypes = [f, i32, sz, sz, sz, sz, sz, f]
+        L.svlo_vision_forward.argtypes = [ctypes.POINTER(_VisCfg), ctypes.POINTER(f), sz, f, i32,
+                                          sz, sz, sz, sz, sz, f, f, ctypes.c_char_p, sz]
+        L._vision_ready = True
+    return L
+
+
+def _ip(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+
+def axial_inv_freq(head_dim, theta):
+    out = np.empty(max(head_dim // 4, 1), np.float32)
+    _check(_vision_lib().svlo_axial_inv_freq(head_dim, theta, _fp(out)), "axial_inv_freq")
+    return out[: head_dim // 4]
+
+
+def axial_rope(values, seq, heads, head_dim, positions, inv_freq):
+    values = _f32(values).copy()
+    pos = np.ascontiguousarray(positions, np.int32).reshape(-1)
+    inv = _f32(inv_freq)
+    _check(_vision_lib().svlo_axial_rope(_fp(values), seq, heads, head_dim, _ip(pos),
+                                         pos.size // 2, _fp(inv), inv.size), "axial_rope")
+    return values
+
+
+def pool_patches(hidden, positions, valid, grid_w, grid_h, soft, width):
+    hidden = _f32(hidden)
+    pos = np.ascontiguousarray(positions, np.int32).reshape(-1)
+    out = np.empty(max(soft * width, 1), np.float32)
+    _check(_vision_lib().svlo_pool_patches(_fp(hidden), _ip(pos), valid, grid_w, grid_h, soft,
+                                           width, _fp(out)), "pool_patches")
+    return out[: soft * width]
+
+
+def resolve_vision_config(config: dict) -> dict:
+    """The fields of VisionConfig (vision.rs:84-273) that the forward pass uses."""
+    v = config["vision_config"]
+    return dict(
+        hidden_size=int(v["hidden_size"]), intermediate_size=int(v["intermediate_size"]),
+        num_hidden_layers=int(v["num_hidden_layers"]),
+        num_attention_heads=int(v["num_attention_heads"]),
+        num_key_value_heads=int(v["num_key_value_heads"]), head_dim=int(v["head_dim"]),
+        position_embedding_size=int(v["position_embedding_size"]),
+        rms_norm_eps=float(np.float32(float(v["rms_norm_eps"]))),
+        rope_theta=float(np.float32(float(v["rope_parameters"]["rope_theta"]))))
+
+
+class OracleVisionModel:
+    """The reference VisionModel restated on the CPU (vision.rs:686-959).
+
+    `patches` is any object with the ImagePatches accessors of
+    media/preprocess.rs:87-147: pixel_values [>= valid, 768],
+    positions [>= valid, 2], valid_patches, max_patches, patch_grid, soft_tokens.
+    """
+
+    def __init__(self, config: dict, weights: dict, text_hidden: int):
+        self.cfg = c = resolve_vision_config(config)
+        self.text_hidden = int(text_hidden)
+        self._c = _VisCfg(c["hidden_size"], c["intermediate_size"], c["num_hidden_layers"],
+                          c["num_attention_heads"], c["num_key_value_heads"], c["head_dim"],
+                          c["position_embedding_size"], c["rms_norm_eps"], c["rope_theta"])
+        names = vision_tensor_names(c["num_hidden_layers"])
+        self._arrays = [_f32(weights[n]).reshape(-1) for n in names]
+        self._ptrs = (ctypes.POINTER(ctypes.c_float) * len(names))(*[_fp(a) for a in self._arrays])
+
+    def forward(self, patches, capture_hidden=False):
+        """Returns dict(pooled [soft, text_hidden], hidden_states, soft_tokens)."""
+        c = self.cfg
+        valid = int(patches.valid_patches)
+        pix = _f32(np.asarray(patches.pixel_values, np.float32).reshape(-1)[: valid * 768])
+        pos = np.ascontiguousarray(np.asarray(patches.positions, np.int32).reshape(-1, 2)[:valid])
+        gw, gh = patches.patch_grid
+        soft = int(patches.soft_tokens)
+        H, L = c["hidden_size"], c["num_hidden_layers"]
+        pooled = np.empty(max(soft, 1) * self.text_hidden, np.float32)
+        hidden = np.empty((L + 1) * max(valid, 1) * H, np.float32) if capture_hidden else None
+        msg = ctypes.create_string_buffer(256)
+        st = _vision_lib().svlo_vision_forward(
+            ctypes.byref(self._c), self._ptrs, self.text_hidden, _fp(pix), _ip(pos), valid,
+            int(patches.max_patches), int(gw), int(gh), soft, _fp(pooled),
+            None if hidden is None else _fp(hidden), msg, 256)
+        if st != 0:
+            raise OracleError(st, msg.value.decode())
+        out = dict(pooled=pooled[: soft * self.text_hidden].reshape(soft, self.text_hidden),
+                   soft_tokens=soft)
+        if capture_hidden:
+            out["hidden_states"] = hidden.reshape(L + 1, valid, H)
+        return out

@@ -103,6 +103,55 @@ int svlo_text_forward(const svlo_text_config *cfg, const float *const *weights,
                       float *out_projected, float *out_pooled, float *out_normalized,
                       float *out_hidden, char *msg, size_t msg_len);
 
+/* ---- vision tower (src/model/vision.rs) --------------------------------- */
+
+/* Validated vision configuration (vision.rs:58-70). */
+typedef struct {
+    int64_t hidden_size;
+    int64_t intermediate_size;
+    int64_t num_hidden_layers;
+    int64_t num_attention_heads;
+    int64_t num_key_value_heads;
+    int64_t head_dim;
+    int64_t position_embedding_size;
+    float rms_norm_eps;
+    float rope_theta;
+} svlo_vision_config;
+
+/*
+ * Weights in the order of VisionConfig::tensor_shapes (vision.rs:345-414):
+ * [0] patch_embedder.input_proj [hidden, 768],
+ * [1] patch_embedder.position_embedding_table [2, pos, hidden],
+ * then 13 per layer: input_layernorm, post_attention_layernorm,
+ * pre_feedforward_layernorm, post_feedforward_layernorm, q_proj, k_proj,
+ * v_proj, o_proj, q_norm, k_norm, gate_proj, up_proj, down_proj,
+ * and last embed_vision.embedding_projection [text_hidden, hidden].
+ */
+#define SVLO_VISION_GLOBAL_TENSORS 2
+#define SVLO_VISION_LAYER_TENSORS 13
+
+/* vision.rs:1047-1065; out has head_dim / 4 entries. */
+int svlo_axial_inv_freq(size_t head_dim, float theta, float *out);
+/* vision.rs:1073-1148 on [sequence, heads, head_dim]; positions [n, 2] (x, y). */
+int svlo_axial_rope(float *values, size_t sequence, size_t heads, size_t head_dim,
+                    const int32_t *positions, size_t n_positions, const float *inv_freq,
+                    size_t n_inv_freq);
+/* vision.rs:980-1040; out [soft_tokens, hidden_size]. */
+int svlo_pool_patches(const float *hidden, const int32_t *positions, size_t valid,
+                      size_t grid_width, size_t grid_height, size_t soft_tokens,
+                      size_t hidden_size, float *out);
+/*
+ * VisionModel::forward (vision.rs:742-959) over the first `valid` patches:
+ * pixel_values [valid, 768], positions [valid, 2]. out_pooled
+ * [soft_tokens, text_hidden] (VisionOutput::pooled); out_hidden
+ * [(layers + 1), valid, hidden] optional.
+ */
+int svlo_vision_forward(const svlo_vision_config *cfg, const float *const *weights,
+                        size_t text_hidden, const float *pixel_values, const int32_t *positions,
+                        size_t valid, size_t max_patches, size_t grid_width, size_t grid_height,
+                        size_t soft_tokens, float *out_pooled, float *out_hidden, char *msg,
+                        size_t msg_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,39 +21,12 @@
 #include <vector>
 
 #include "../../include/svl_hip.h"
+#include "host_common.hpp"
 #include "svl_internal.hpp"
-
-struct svl_ctx {
-    int device;
-};
 
 namespace {
 
 using namespace svl;
-
-thread_local std::string g_err;
-
-svl_status fail(svl_status st, const char *fmt, ...) {
-    char buf[512];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
-    va_end(ap);
-    g_err = buf;
-    return st;
-}
-
-#define HIP_TRY(expr)                                                                       \
-    do {                                                                                    \
-        hipError_t e_ = (expr);                                                             \
-        if (e_ != hipSuccess) return fail(SVL_DEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
-    } while (0)
-
-#define ST_TRY(expr)                    \
-    do {                                \
-        svl_status s_ = (expr);         \
-        if (s_ != SVL_OK) return s_;    \
-    } while (0)
 
 // src/model/config.rs:27-51, text.rs:34, tensor/owned.rs MAX_TENSOR_ELEMENTS,
 // weights.rs MAX_WEIGHT_ELEMENTS.
@@ -66,8 +39,6 @@ constexpr int64_t MAX_INTERMEDIATE_SIZE = 65536;
 constexpr int64_t MAX_VOCAB_SIZE = 1000000;
 constexpr int64_t MAX_EMBEDDING_DIM = 16384;
 constexpr int64_t MAX_POSITIONS = 1048576;
-constexpr int64_t MAX_ACTIVATION_ELEMENTS = int64_t(1) << 28;
-constexpr int64_t MAX_TENSOR_ELEMENTS = int64_t(1) << 30;
 constexpr int64_t MAX_WEIGHT_ELEMENTS = int64_t(1) << 30;
 
 // ---------------------------------------------------------------------------
@@ -93,26 +64,6 @@ const char *kClassNames[KC_COUNT] = {
     "gemm_qkv",      "gemm_o",         "gemm_gate_up", "gemm_down", "gemm_ple_gate",
     "gemm_ple_proj", "gemm_ple_model", "gemm_out",     "attention", "qkv_norm_rope",
     "resnorm",       "gather",         "ple_norm",     "pool"};
-
-template <class T>
-struct DevBuf {
-    T *p = nullptr;
-    size_t n = 0;
-    hipError_t ensure(size_t count) {
-        if (count <= n) return hipSuccess;
-        if (p) (void)hipFree(p);
-        p = nullptr;
-        n = 0;
-        hipError_t e = hipMalloc((void **)&p, std::max<size_t>(count, 1) * sizeof(T));
-        if (e == hipSuccess) n = count;
-        return e;
-    }
-    void release() {
-        if (p) (void)hipFree(p);
-        p = nullptr;
-        n = 0;
-    }
-};
 
 struct DevLayer {
     float *w_qkv = nullptr, *w_o = nullptr, *w_gu = nullptr, *w_down = nullptr;
@@ -296,36 +247,8 @@ std::vector<std::pair<std::string, std::vector<int64_t>>> tensor_shapes(const sv
     return s;
 }
 
-// TensorEntry::to_f32 (safetensors.rs:69-110): F32 little-endian or BF16
-// widened exactly (bf16.rs:13-15, bits << 16). Non-finite values are
-// rejected like Tensor::validate_finite (owned.rs:126-135).
-svl_status decode_f32(const svl_tensor_view &t, int64_t numel, std::vector<float> &out) {
-    out.resize((size_t)numel);
-    if (t.dtype == SVL_F32) {
-        std::memcpy(out.data(), t.data, (size_t)numel * 4);
-    } else if (t.dtype == SVL_BF16) {
-        const uint16_t *b = (const uint16_t *)t.data;
-        for (int64_t i = 0; i < numel; ++i) {
-            const uint32_t bits = (uint32_t)b[i] << 16;
-            std::memcpy(&out[(size_t)i], &bits, 4);
-        }
-    } else {
-        return fail(SVL_UNSUPPORTED, "tensor %s has an unsupported dtype", t.name);
-    }
-    for (int64_t i = 0; i < numel; ++i)
-        if (!std::isfinite(out[(size_t)i]))
-            return fail(SVL_INTERNAL, "non-finite tensor value at index %lld of %s",
-                        (long long)i, t.name);
-    return SVL_OK;
-}
-
 svl_status upload(svl_text_model *m, const float *host, size_t count, float **dst) {
-    float *d = nullptr;
-    HIP_TRY(hipMalloc((void **)&d, std::max<size_t>(count, 1) * sizeof(float)));
-    m->allocations.push_back(d);
-    HIP_TRY(hipMemcpy(d, host, count * sizeof(float), hipMemcpyHostToDevice));
-    *dst = d;
-    return SVL_OK;
+    return upload_owned(m->allocations, host, count, dst);
 }
 
 // RoPE cos/sin tables with the reference's exact f32 angles
@@ -503,7 +426,7 @@ void build_groups(const svl_text_model *m, Batch &b, int max_groups) {
 }
 
 svl_status ensure_workspace(svl_text_model *m, const Batch &b, int64_t feat_floats,
-                            int dims_total) {
+                            bool need_featmap, int dims_total) {
     const int64_t T = std::max<int64_t>(b.T, 1);
     HIP_TRY(m->h.ensure(T * m->H));
     HIP_TRY(m->n.ensure(T * m->H));
@@ -522,10 +445,8 @@ svl_status ensure_workspace(svl_text_model *m, const Batch &b, int64_t feat_floa
     HIP_TRY(m->pooled.ensure((size_t)b.B * m->E));
     HIP_TRY(m->normalized.ensure((size_t)b.B * m->E));
     HIP_TRY(m->flag.ensure(1));
-    if (feat_floats > 0) {
-        HIP_TRY(m->feats.ensure(feat_floats));
-        HIP_TRY(m->featmap.ensure(T));
-    }
+    if (feat_floats > 0) HIP_TRY(m->feats.ensure(feat_floats));
+    if (need_featmap) HIP_TRY(m->featmap.ensure(T));
     if (dims_total > 0) HIP_TRY(m->trunc.ensure((size_t)b.B * dims_total));
     return SVL_OK;
 }
@@ -535,8 +456,11 @@ svl_status ensure_workspace(svl_text_model *m, const Batch &b, int64_t feat_floa
 // m->featmap / m->feats when has_features). Every buffer is addressed at the
 // group's token (or row) range; the per-layer-width QKV and attention
 // buffers are carved at their widest layer so the groups never overlap.
+// d_featmap (per token: feature row or -1) and d_feats are null without
+// multimodal features.
 svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hipStream_t s,
-                         const uint32_t *d_ids, bool has_features, const int32_t *d_dims,
+                         const uint32_t *d_ids, const int32_t *d_featmap, const float *d_feats,
+                         const int32_t *d_dims,
                          int n_dims, int dims_total, float *d_trunc, float *h_hidden) {
     const int64_t T = grp.T, H = m->H, P = m->P, L = m->L, E = m->E, t0 = grp.t0;
     if (T == 0) return SVL_OK;
@@ -553,8 +477,8 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
     HIP_TRY(launch_positions(offs, grp.nrows, pos, rowlen, s));
     {
         Timer tm(m, s, KC_GATHER, Td * H * 4 * 3);
-        HIP_TRY(launch_gather(d_ids + t0, m->embed, m->V, has_features ? m->featmap.p + t0 : nullptr,
-                              has_features ? m->feats.p : nullptr, m->embedding_scale,
+        HIP_TRY(launch_gather(d_ids + t0, m->embed, m->V, d_featmap ? d_featmap + t0 : nullptr,
+                              d_feats, m->embedding_scale,
                               m->layers[0].ln_in, h, n, T, (int)H, m->eps, flag, s));
     }
     if (h_hidden)
@@ -682,7 +606,8 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
 // which waits for everything s0 has enqueued so far and is joined back into
 // s0 at the end.
 svl_status enqueue_forward(svl_text_model *m, const Batch &b, hipStream_t s0,
-                           const uint32_t *d_ids, bool has_features, const int32_t *d_dims,
+                           const uint32_t *d_ids, const int32_t *d_featmap, const float *d_feats,
+                           const int32_t *d_dims,
                            int n_dims, int dims_total, float *d_trunc, float *h_hidden) {
     const size_t ng = b.groups.size();
     if (ng > 1) {
@@ -692,7 +617,7 @@ svl_status enqueue_forward(svl_text_model *m, const Batch &b, hipStream_t s0,
     }
     for (size_t gi = 0; gi < ng; ++gi)
         ST_TRY(enqueue_group(m, b, b.groups[gi], gi == 0 ? s0 : m->extra[gi - 1], d_ids,
-                             has_features, d_dims, n_dims, dims_total, d_trunc, h_hidden));
+                             d_featmap, d_feats, d_dims, n_dims, dims_total, d_trunc, h_hidden));
     for (size_t gi = 1; gi < ng; ++gi) {
         HIP_TRY(hipEventRecord(m->ev_join[gi - 1], m->extra[gi - 1]));
         HIP_TRY(hipStreamWaitEvent(s0, m->ev_join[gi - 1], 0));
@@ -825,6 +750,40 @@ void parallel_for(size_t n, F f) {
 
 }  // namespace
 
+namespace svl {
+
+int text_device(const svl_text_model *m) { return m->device; }
+int64_t text_hidden_size(const svl_text_model *m) { return m->H; }
+int64_t text_embedding_dim(const svl_text_model *m) { return m->E; }
+int64_t text_pad_token(const svl_text_model *m) { return m->pad; }
+
+svl_status text_forward_with_device_features(svl_text_model *m, const uint32_t *ids,
+                                             const int64_t *offsets, int32_t batch,
+                                             const int32_t *featmap, const float *d_feats,
+                                             float *out_normalized) {
+    std::lock_guard<std::mutex> lock(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    Batch b;
+    ST_TRY(prepare_batch(m, offsets, batch, b));
+    if (batch == 0) return SVL_OK;
+    for (int r = 0; r < batch; ++r)
+        ST_TRY(validate_row(m, r, ids + offsets[r], offsets[r + 1] - offsets[r]));
+    if (m->pad < 0)
+        return fail(SVL_UNSUPPORTED, "model has no padding token for multimodal inputs");
+    ST_TRY(ensure_workspace(m, b, 0, true, 0));
+    hipStream_t s = m->stream;
+    HIP_TRY(hipMemcpyAsync(m->ids.p, ids, (size_t)b.T * 4, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(m->featmap.p, featmap, (size_t)b.T * 4, hipMemcpyHostToDevice, s));
+    ST_TRY(upload_batch_meta(m, b, s));
+    ST_TRY(enqueue_forward(m, b, s, m->ids.p, m->featmap.p, d_feats, nullptr, 0, 0, nullptr,
+                           nullptr));
+    HIP_TRY(hipMemcpyAsync(out_normalized, m->normalized.p, (size_t)(batch * m->E) * 4,
+                           hipMemcpyDeviceToHost, s));
+    return finish(m, s);
+}
+
+}  // namespace svl
+
 // ===========================================================================
 // C ABI
 // ===========================================================================
@@ -864,38 +823,9 @@ svl_status svl_text_model_create(svl_ctx *ctx, const svl_text_config *cfg,
 
     // Inventory (weights.rs:130-165).
     const auto shapes = tensor_shapes(cfg);
-    std::map<std::string, const svl_tensor_view *> by_name;
-    for (size_t i = 0; i < n_tensors; ++i) {
-        if (!tensors[i].name) return fail(SVL_USAGE, "tensor %zu has no name", i);
-        by_name[tensors[i].name] = &tensors[i];
-    }
-    std::map<std::string, size_t> expected;
-    for (size_t i = 0; i < shapes.size(); ++i) expected[shapes[i].first] = i;
-    for (auto &kv : by_name)
-        if (kv.first.rfind("language_model.", 0) == 0 && !expected.count(kv.first))
-            return fail(SVL_CORRUPT, "unexpected text tensor %s in the weight file",
-                        kv.first.c_str());
-    int64_t parameters = 0;
-    for (auto &sh : shapes) {
-        auto it = by_name.find(sh.first);
-        if (it == by_name.end())
-            return fail(SVL_CORRUPT, "text weight %s is missing from the Safetensors file",
-                        sh.first.c_str());
-        const svl_tensor_view *t = it->second;
-        bool same = t->ndim == (int32_t)sh.second.size();
-        for (size_t d = 0; same && d < sh.second.size(); ++d) same = t->shape[d] == sh.second[d];
-        if (!same) return fail(SVL_CORRUPT, "text weight %s has an unexpected shape", sh.first.c_str());
-        int64_t numel = 1;
-        for (int64_t d : sh.second) numel *= d;
-        if (numel > MAX_TENSOR_ELEMENTS)
-            return fail(SVL_LIMIT, "tensor %s has %lld elements, above the cap", sh.first.c_str(),
-                        (long long)numel);
-        parameters += numel;
-        if (parameters > MAX_WEIGHT_ELEMENTS)
-            return fail(SVL_LIMIT, "text weights exceed the %lld-element cap",
-                        (long long)MAX_WEIGHT_ELEMENTS);
-        if (!t->data) return fail(SVL_USAGE, "tensor %s has no data", sh.first.c_str());
-    }
+    TensorIndex by_name;
+    ST_TRY(check_inventory(tensors, n_tensors, shapes, {"language_model."}, "text",
+                           MAX_WEIGHT_ELEMENTS, by_name));
 
     auto m = new svl_text_model();
     std::unique_ptr<svl_text_model> guard(m);
@@ -923,10 +853,7 @@ svl_status svl_text_model_create(svl_ctx *ctx, const svl_text_config *cfg,
     if (m->E > 4096) return fail(SVL_UNSUPPORTED, "embedding dimension above 4096");
 
     auto get = [&](const std::string &name, std::vector<float> &buf) -> svl_status {
-        const svl_tensor_view *t = by_name[name];
-        int64_t numel = 1;
-        for (int d = 0; d < t->ndim; ++d) numel *= t->shape[d];
-        return decode_f32(*t, numel, buf);
+        return decode_named(by_name, name, buf);
     };
     std::vector<float> a, b2, c2;
     ST_TRY(get("language_model.embed_tokens.weight", a));
@@ -960,17 +887,9 @@ svl_status svl_text_model_create(svl_ctx *ctx, const svl_text_config *cfg,
         ST_TRY(upload(m, qkv.data(), qkv.size(), &ly.w_qkv));
         ST_TRY(get(p + "self_attn.o_proj.weight", a));
         ST_TRY(upload(m, a.data(), a.size(), &ly.w_o));
-        // gate/up interleaved in 32-row blocks: [g 0..31, u 0..31, g 32..63, ...]
         ST_TRY(get(p + "mlp.gate_proj.weight", b2));
         ST_TRY(get(p + "mlp.up_proj.weight", c2));
-        std::vector<float> gu((size_t)(2 * m->I_pad * H), 0.f);
-        for (int64_t j = 0; j < m->I; ++j) {
-            const int64_t blk = j / 32, off = j % 32;
-            std::copy(b2.begin() + j * H, b2.begin() + (j + 1) * H,
-                      gu.begin() + (64 * blk + off) * H);
-            std::copy(c2.begin() + j * H, c2.begin() + (j + 1) * H,
-                      gu.begin() + (64 * blk + 32 + off) * H);
-        }
+        const std::vector<float> gu = interleave_gate_up(b2, c2, m->I, m->I_pad, m->H);
         ST_TRY(upload(m, gu.data(), gu.size(), &ly.w_gu));
         ST_TRY(get(p + "mlp.down_proj.weight", a));
         ST_TRY(upload(m, a.data(), a.size(), &ly.w_down));
@@ -1070,7 +989,7 @@ svl_status svl_text_forward_batch(svl_text_model *m, const uint32_t *ids, const 
         }
         if (feat_floats == 0) featmap.clear();
     }
-    ST_TRY(ensure_workspace(m, b, feat_floats, 0));
+    ST_TRY(ensure_workspace(m, b, feat_floats, feat_floats > 0, 0));
     hipStream_t s = m->stream;
     HIP_TRY(hipMemcpyAsync(m->ids.p, ids, (size_t)b.T * 4, hipMemcpyHostToDevice, s));
     if (feat_floats > 0) {
@@ -1086,7 +1005,8 @@ svl_status svl_text_forward_batch(svl_text_model *m, const uint32_t *ids, const 
         }
     }
     ST_TRY(upload_batch_meta(m, b, s));
-    ST_TRY(enqueue_forward(m, b, s, m->ids.p, feat_floats > 0, nullptr, 0, 0, nullptr,
+    ST_TRY(enqueue_forward(m, b, s, m->ids.p, feat_floats > 0 ? m->featmap.p : nullptr,
+                           feat_floats > 0 ? m->feats.p : nullptr, nullptr, 0, 0, nullptr,
                            out_hidden));
     HIP_TRY(hipMemcpyAsync(out_normalized, m->normalized.p, (size_t)(batch * m->E) * 4,
                            hipMemcpyDeviceToHost, s));
@@ -1118,12 +1038,13 @@ svl_status svl_text_forward_device(svl_text_model *m, const uint32_t *d_ids,
     if (batch == 0) return SVL_OK;
     for (int r = 0; r < batch; ++r)
         ST_TRY(validate_row(m, r, nullptr, offsets[r + 1] - offsets[r]));
-    ST_TRY(ensure_workspace(m, b, 0, dims_total));
+    ST_TRY(ensure_workspace(m, b, 0, false, dims_total));
     HIP_TRY(m->dims.ensure(n_dims));
     hipStream_t s = stream ? (hipStream_t)stream : m->stream;
     HIP_TRY(hipMemcpyAsync(m->dims.p, dims, n_dims * 4, hipMemcpyHostToDevice, s));
     ST_TRY(upload_batch_meta(m, b, s));
-    ST_TRY(enqueue_forward(m, b, s, d_ids, false, m->dims.p, n_dims, dims_total, d_out, nullptr));
+    ST_TRY(enqueue_forward(m, b, s, d_ids, nullptr, nullptr, m->dims.p, n_dims, dims_total, d_out,
+                           nullptr));
     return finish(m, s);
 }
 

@@ -3,3 +3,4 @@
 #include "gemm.hip"
 #include "rows.hip"
 #include "attention.hip"
+#include "vision.hip"

@@ -121,4 +121,23 @@ hipError_t launch_geglu(const float *g, const float *u, float *y, int64_t n, hip
 hipError_t launch_add(const float *a, const float *b, float *y, int64_t n, hipStream_t s);
 hipError_t launch_finite_check(const float *x, int64_t n, int *flag, hipStream_t s);
 
+// ---- vision tower row kernels ------------------------------------------------
+// y = 2 * (x - 0.5), n % 4 == 0.
+hipError_t launch_patch_scale(const float *x, float *y, int64_t n, hipStream_t s);
+// h[t] += table[0][x_t] + table[1][y_t] with pos [T, 2] (x, y) and table
+// [2, pos_size, width]; n[t] = rms(h[t], w). width % 4 == 0, <= 2048.
+hipError_t launch_patch_pos(float *h, const int32_t *pos, const float *table, int64_t pos_size,
+                            const float *w, float *n, int64_t rows, int width, float eps,
+                            int *flag, hipStream_t s);
+// In place on qkv[T, ld]: per-head q RMSNorm(qn) + axial RoPE, k RMSNorm(kn)
+// + axial RoPE, v unscaled RMSNorm. cos/sin tables are [coordinate, hd/4].
+hipError_t launch_qkv_post_axial(float *qkv, int64_t ld, int64_t tokens, int nh, int nkv, int hd,
+                                 const float *qn, const float *kn, const float *cos_t,
+                                 const float *sin_t, const int32_t *pos, float eps, int *flag,
+                                 hipStream_t s);
+// out[s] = unscaled_rms((sum of h over bin s in patch order / divisor) * scale).
+hipError_t launch_pool_bins(const float *h, const int32_t *bin_start, const int32_t *bin_patch,
+                            int64_t soft_tokens, int width, float divisor, float scale, float eps,
+                            float *out, int *flag, hipStream_t s);
+
 }  // namespace svl

@@ -1,0 +1,631 @@
+// Host runtime of the vision tower and the image prompt glue: the
+// svl_vision_* / svl_image_* part of include/svl_hip.h.
+//
+// It plays the role of the reference's VisionModel (src/model/vision.rs:
+// 686-959) and ImageEmbedder::embed_impl (src/model/image.rs:209-253). The
+// weights are validated like VisionWeights::decode (vision.rs:556-610) and
+// packed once (fused QKV, interleaved gate/up). A forward call packs the
+// real patches of every image of the batch back to back, runs the whole
+// tower as one launch sequence on the model's stream, and reads back only
+// the projected soft tokens (plus optional captures). Padding patches are
+// never uploaded: like the reference, only the first valid_patches rows of
+// each image take part.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/svl_hip.h"
+#include "host_common.hpp"
+#include "svl_internal.hpp"
+
+namespace {
+
+using namespace svl;
+
+// vision.rs:29-56 caps; media/preprocess.rs:22-43 patch geometry.
+constexpr int64_t MAX_VISION_HIDDEN = 16384;
+constexpr int64_t MAX_VISION_INTERMEDIATE = 65536;
+constexpr int64_t MAX_VISION_LAYERS = 128;
+constexpr int64_t MAX_VISION_HEADS = 128;
+constexpr int64_t MAX_VISION_HEAD_DIM = 1024;
+constexpr int64_t MAX_POSITION_EMBEDDINGS = 1048576;
+constexpr int64_t MAX_VISION_WEIGHT_ELEMENTS = int64_t(1) << 30;
+constexpr int64_t PATCH_VALUES = 16 * 16 * 3;
+constexpr int64_t POOL = 3;
+// image.rs: the text context of an image prompt (config.rs:27).
+constexpr int64_t MAX_TEXT_TOKENS = 8192;
+// attn_simple_kernel bound for head dims without an MFMA attention kernel.
+constexpr int64_t SIMPLE_ATTENTION_MAX_KEYS = 8192;
+
+struct VisLayer {
+    float *w_qkv = nullptr, *w_o = nullptr, *w_gu = nullptr, *w_down = nullptr;
+    float *ln_in = nullptr, *ln_post_attn = nullptr, *ln_pre_ff = nullptr, *ln_post_ff = nullptr,
+          *q_norm = nullptr, *k_norm = nullptr;
+};
+
+}  // namespace
+
+struct svl_vision_model {
+    int device = 0;
+    int64_t H = 0, I = 0, L = 0, NH = 0, NKV = 0, hd = 0, pos_size = 0, text_hidden = 0;
+    int64_t I_pad = 0, qd = 0, kd = 0;
+    float eps = 0.f, theta = 0.f;
+    std::vector<float> inv_freq;  // axial_inv_freq, hd / 4 entries
+    std::vector<float *> allocations;
+    float *w_in = nullptr, *pos_table = nullptr, *w_proj = nullptr;
+    std::vector<VisLayer> layers;
+    // axial RoPE angle tables [n_coord, hd/4] for coordinates 0..n_coord-1
+    DevBuf<float> cos_t, sin_t;
+    int64_t n_coord = 0;
+    // workspace
+    DevBuf<float> pix, h, n, tmp, qkv, attn, act, pooled, soft;
+    DevBuf<int32_t> coord, apos, rowlen, bin_start, bin_patch;
+    DevBuf<int64_t> offsets;
+    DevBuf<AttnTile> tiles;
+    DevBuf<int> flag;
+    int *h_flag = nullptr;
+    hipStream_t stream = nullptr;
+    std::mutex mu;
+
+    ~svl_vision_model() {
+        if (device >= 0) (void)hipSetDevice(device);
+        for (float *p : allocations) (void)hipFree(p);
+        cos_t.release(); sin_t.release();
+        pix.release(); h.release(); n.release(); tmp.release(); qkv.release(); attn.release();
+        act.release(); pooled.release(); soft.release();
+        coord.release(); apos.release(); rowlen.release(); bin_start.release();
+        bin_patch.release(); offsets.release(); tiles.release(); flag.release();
+        if (h_flag) (void)hipHostFree(h_flag);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+// VisionConfig invariants (vision.rs:128-272) on an already parsed config.
+svl_status validate_vision_config(const svl_vision_config *c, int64_t text_hidden) {
+    if (!c) return fail(SVL_USAGE, "vision configuration is null");
+    if (!std::isfinite((float)c->rms_norm_eps) || c->rms_norm_eps < 0)
+        return fail(SVL_CORRUPT, "vision RMSNorm epsilon must be finite and non-negative");
+    if (c->head_dim <= 0 || c->head_dim % 4)
+        return fail(SVL_UNSUPPORTED,
+                    "vision head dimension must be positive and divisible by four for axial RoPE");
+    if (c->num_attention_heads <= 0 || c->num_key_value_heads <= 0)
+        return fail(SVL_CORRUPT, "vision attention head counts must be positive");
+    if (c->num_attention_heads % c->num_key_value_heads)
+        return fail(SVL_CORRUPT,
+                    "vision query head count is not a multiple of the key/value head count");
+    const int64_t qd = c->num_attention_heads * c->head_dim;
+    const int64_t kd = c->num_key_value_heads * c->head_dim;
+    if (c->hidden_size <= 0 || c->hidden_size > MAX_VISION_HIDDEN || qd > MAX_VISION_HIDDEN ||
+        kd > MAX_VISION_HIDDEN)
+        return fail(SVL_LIMIT, "vision dimensions exceed the %lld-element hidden cap",
+                    (long long)MAX_VISION_HIDDEN);
+    if (c->intermediate_size <= 0 || c->intermediate_size > MAX_VISION_INTERMEDIATE)
+        return fail(SVL_LIMIT, "vision intermediate size %lld exceeds the %lld cap",
+                    (long long)c->intermediate_size, (long long)MAX_VISION_INTERMEDIATE);
+    if (c->num_hidden_layers < 0 || c->num_hidden_layers > MAX_VISION_LAYERS)
+        return fail(SVL_LIMIT, "vision layer count %lld exceeds the %lld cap",
+                    (long long)c->num_hidden_layers, (long long)MAX_VISION_LAYERS);
+    if (c->num_attention_heads > MAX_VISION_HEADS || c->head_dim > MAX_VISION_HEAD_DIM)
+        return fail(SVL_LIMIT, "vision attention layout exceeds its documented cap");
+    if (c->position_embedding_size <= 0 || c->position_embedding_size > MAX_POSITION_EMBEDDINGS)
+        return fail(SVL_LIMIT, "vision position table size %lld is outside 1..=%lld",
+                    (long long)c->position_embedding_size, (long long)MAX_POSITION_EMBEDDINGS);
+    if (!std::isfinite((float)c->rope_theta) || (float)c->rope_theta <= 0.f)
+        return fail(SVL_CORRUPT, "vision RoPE theta must be finite and positive");
+    if (text_hidden <= 0 || text_hidden > MAX_VISION_HIDDEN)
+        return fail(SVL_LIMIT, "text hidden size %lld is outside 1..=%lld", (long long)text_hidden,
+                    (long long)MAX_VISION_HIDDEN);
+    return SVL_OK;
+}
+
+// VisionConfig::tensor_shapes (vision.rs:345-414).
+ShapeList vision_tensor_shapes(const svl_vision_config *c, int64_t text_hidden) {
+    const int64_t H = c->hidden_size, I = c->intermediate_size, hd = c->head_dim;
+    const int64_t qd = c->num_attention_heads * hd, kd = c->num_key_value_heads * hd;
+    ShapeList s;
+    s.push_back({"vision_tower.patch_embedder.input_proj.weight", {H, PATCH_VALUES}});
+    s.push_back({"vision_tower.patch_embedder.position_embedding_table",
+                 {2, c->position_embedding_size, H}});
+    for (int64_t l = 0; l < c->num_hidden_layers; ++l) {
+        const std::string p = "vision_tower.encoder.layers." + std::to_string(l);
+        s.push_back({p + ".input_layernorm.weight", {H}});
+        s.push_back({p + ".post_attention_layernorm.weight", {H}});
+        s.push_back({p + ".pre_feedforward_layernorm.weight", {H}});
+        s.push_back({p + ".post_feedforward_layernorm.weight", {H}});
+        s.push_back({p + ".self_attn.q_proj.linear.weight", {qd, H}});
+        s.push_back({p + ".self_attn.k_proj.linear.weight", {kd, H}});
+        s.push_back({p + ".self_attn.v_proj.linear.weight", {kd, H}});
+        s.push_back({p + ".self_attn.o_proj.linear.weight", {H, qd}});
+        s.push_back({p + ".self_attn.q_norm.weight", {hd}});
+        s.push_back({p + ".self_attn.k_norm.weight", {hd}});
+        s.push_back({p + ".mlp.gate_proj.linear.weight", {I, H}});
+        s.push_back({p + ".mlp.up_proj.linear.weight", {I, H}});
+        s.push_back({p + ".mlp.down_proj.linear.weight", {H, I}});
+    }
+    s.push_back({"embed_vision.embedding_projection.weight", {text_hidden, H}});
+    return s;
+}
+
+// axial_inv_freq (vision.rs:1047-1065) and the per-coordinate angle tables
+// of axial_rope (vision.rs:1105-1121): angle = (coord as f32) * inv_freq[i],
+// cos / sin in f32 on the host, exactly as the reference evaluates them.
+svl_status ensure_axial_tables(svl_vision_model *v, int64_t n_coord) {
+    if (n_coord <= v->n_coord) return SVL_OK;
+    const int64_t q = v->hd / 4;
+    std::vector<float> c((size_t)(n_coord * q)), s((size_t)(n_coord * q));
+    for (int64_t p = 0; p < n_coord; ++p)
+        for (int64_t i = 0; i < q; ++i) {
+            const float angle = (float)p * v->inv_freq[(size_t)i];
+            c[(size_t)(p * q + i)] = std::cos(angle);
+            s[(size_t)(p * q + i)] = std::sin(angle);
+        }
+    v->cos_t.release();
+    v->sin_t.release();
+    v->n_coord = 0;
+    HIP_TRY(v->cos_t.ensure(c.size()));
+    HIP_TRY(v->sin_t.ensure(s.size()));
+    HIP_TRY(hipMemcpy(v->cos_t.p, c.data(), c.size() * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(v->sin_t.p, s.data(), s.size() * 4, hipMemcpyHostToDevice));
+    v->n_coord = n_coord;
+    return SVL_OK;
+}
+
+// Per-call geometry of a batch of images.
+struct VisBatch {
+    int32_t B = 0;
+    int64_t T = 0, S = 0;                 // real patches, soft tokens
+    std::vector<int64_t> offsets;         // patch offsets per image [B + 1]
+    std::vector<int64_t> soft_offsets;    // soft-token offsets per image [B + 1]
+    std::vector<int32_t> coord;           // [T, 2] (x, y)
+    std::vector<int32_t> bin_start;       // [S + 1]
+    std::vector<int32_t> bin_patch;       // [T] global patch index, bin-major, patch order
+    std::vector<AttnTile> tiles;
+    int64_t max_coord = 0;
+    double attn_flops = 0;
+};
+
+svl_status checked_len(int i, int64_t rows, int64_t width, const char *label) {
+    if (width != 0 && rows > INT64_MAX / width)
+        return fail(SVL_LIMIT, "image %d: %s size overflow", i, label);
+    if (rows * width > MAX_ACTIVATION_ELEMENTS)
+        return fail(SVL_LIMIT, "image %d: %s would allocate %lld elements, above the cap", i,
+                    label, (long long)(rows * width));
+    return SVL_OK;
+}
+
+// Validation in the order VisionModel::forward meets each condition
+// (vision.rs:743-809, then pool_patches :981-1032), and the batch layout.
+svl_status prepare_images(const svl_vision_model *v, const svl_image_patches *im, int32_t batch,
+                          bool need_pixels, VisBatch &b) {
+    if (batch < 0) return fail(SVL_USAGE, "negative batch");
+    if (batch > 0 && !im) return fail(SVL_USAGE, "images are null");
+    b.B = batch;
+    b.offsets.assign(1, 0);
+    b.soft_offsets.assign(1, 0);
+    for (int i = 0; i < batch; ++i) {
+        const svl_image_patches &p = im[i];
+        const int64_t valid = p.valid_patches;
+        if (valid <= 0) return fail(SVL_CORRUPT, "image %d: vision tower received zero real patches", i);
+        if (valid > p.max_patches)
+            return fail(SVL_INTERNAL,
+                        "image %d: vision tower received more real patches than the padded tensor", i);
+        ST_TRY(checked_len(i, valid, PATCH_VALUES, "vision patch tensor"));
+        ST_TRY(checked_len(i, valid, v->H, "vision hidden state"));
+        ST_TRY(checked_len(i, valid, v->qd, "vision query rows"));
+        ST_TRY(checked_len(i, valid, v->kd, "vision key rows"));
+        ST_TRY(checked_len(i, valid, v->I, "vision feed-forward buffer"));
+        if (need_pixels && !p.pixel_values)
+            return fail(SVL_USAGE, "image %d: pixel values are null", i);
+        if (!p.positions) return fail(SVL_USAGE, "image %d: positions are null", i);
+        for (int64_t k = 0; k < valid; ++k) {
+            const int32_t x = p.positions[2 * k], y = p.positions[2 * k + 1];
+            if (x < 0) return fail(SVL_INTERNAL, "image %d: vision patch x position is negative", i);
+            if (y < 0) return fail(SVL_INTERNAL, "image %d: vision patch y position is negative", i);
+            if (x >= v->pos_size || y >= v->pos_size)
+                return fail(SVL_CORRUPT,
+                            "image %d: vision patch position (%d, %d) is outside the %lld-entry table",
+                            i, x, y, (long long)v->pos_size);
+        }
+        if (v->hd != 0 && attn_block_vectors((int)v->hd) == 0 && valid > SIMPLE_ATTENTION_MAX_KEYS)
+            return fail(SVL_UNSUPPORTED, "image %d: %lld patches at head dimension %lld", i,
+                        (long long)valid, (long long)v->hd);
+        // pool_patches geometry (vision.rs:981-1032)
+        if (p.grid_width < 0 || p.grid_height < 0 || p.grid_width % POOL || p.grid_height % POOL)
+            return fail(SVL_INTERNAL, "image %d: vision patch grid is not divisible by the pooling kernel", i);
+        const int64_t pw = p.grid_width / POOL, ph = p.grid_height / POOL;
+        if (ph != 0 && pw > INT64_MAX / ph)
+            return fail(SVL_LIMIT, "image %d: vision pooled grid overflow", i);
+        if (pw * ph != p.soft_tokens)
+            return fail(SVL_INTERNAL,
+                        "image %d: vision pooler produces %lld tokens, preprocessing declared %lld",
+                        i, (long long)(pw * ph), (long long)p.soft_tokens);
+        ST_TRY(checked_len(i, p.soft_tokens, v->H, "vision pooled state"));
+        for (int64_t k = 0; k < valid; ++k) {
+            const int64_t x = p.positions[2 * k], y = p.positions[2 * k + 1];
+            if (x / POOL + pw * (y / POOL) >= p.soft_tokens)
+                return fail(SVL_INTERNAL, "image %d: vision pooler computed an out-of-range bin", i);
+        }
+        b.offsets.push_back(b.offsets.back() + valid);
+        b.soft_offsets.push_back(b.soft_offsets.back() + p.soft_tokens);
+    }
+    b.T = b.offsets.back();
+    b.S = b.soft_offsets.back();
+    if (b.T > (int64_t)INT32_MAX / 8 || b.S > (int64_t)INT32_MAX / 8)
+        return fail(SVL_LIMIT, "batch holds too many patches");
+    b.coord.resize((size_t)(2 * b.T));
+    b.bin_start.assign((size_t)b.S + 1, 0);
+    b.bin_patch.resize((size_t)b.T);
+    std::vector<int32_t> bin_of((size_t)b.T);
+    for (int i = 0; i < batch; ++i) {
+        const svl_image_patches &p = im[i];
+        const int64_t t0 = b.offsets[i], s0 = b.soft_offsets[i], pw = p.grid_width / POOL;
+        for (int64_t k = 0; k < p.valid_patches; ++k) {
+            const int32_t x = p.positions[2 * k], y = p.positions[2 * k + 1];
+            b.coord[(size_t)(2 * (t0 + k))] = x;
+            b.coord[(size_t)(2 * (t0 + k) + 1)] = y;
+            b.max_coord = std::max<int64_t>(b.max_coord, std::max(x, y));
+            const int64_t bin = s0 + x / POOL + pw * (y / POOL);
+            bin_of[(size_t)(t0 + k)] = (int32_t)bin;
+            b.bin_start[(size_t)bin + 1] += 1;
+        }
+    }
+    for (int64_t s = 0; s < b.S; ++s) b.bin_start[(size_t)s + 1] += b.bin_start[(size_t)s];
+    {
+        std::vector<int32_t> fill(b.bin_start.begin(), b.bin_start.end() - 1);
+        for (int64_t t = 0; t < b.T; ++t) b.bin_patch[(size_t)fill[(size_t)bin_of[(size_t)t]]++] = (int32_t)t;
+    }
+    // attention work items, longest images first
+    const int bv = attn_block_vectors((int)v->hd);
+    std::vector<int> order(batch);
+    for (int i = 0; i < batch; ++i) order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) {
+        return im[x].valid_patches > im[y].valid_patches;
+    });
+    const int G = (int)(v->NH / v->NKV);
+    if (bv > 0)
+        for (int i : order) {
+            const int64_t len = im[i].valid_patches;
+            for (int kv = 0; kv < v->NKV; ++kv)
+                for (int64_t v0 = 0; v0 < len * G; v0 += bv)
+                    b.tiles.push_back({(int32_t)b.offsets[i], (int32_t)len, kv, (int32_t)v0});
+        }
+    for (int i = 0; i < batch; ++i) {
+        const double len = (double)im[i].valid_patches;
+        b.attn_flops += 4.0 * (double)v->hd * (double)v->NH * len * len;
+    }
+    return SVL_OK;
+}
+
+svl_status ensure_vis_workspace(svl_vision_model *v, const VisBatch &b) {
+    const int64_t T = std::max<int64_t>(b.T, 1), S = std::max<int64_t>(b.S, 1);
+    HIP_TRY(v->pix.ensure(T * PATCH_VALUES));
+    HIP_TRY(v->h.ensure(T * v->H));
+    HIP_TRY(v->n.ensure(T * v->H));
+    HIP_TRY(v->tmp.ensure(T * v->H));
+    HIP_TRY(v->qkv.ensure(T * (v->qd + 2 * v->kd)));
+    HIP_TRY(v->attn.ensure(T * v->qd));
+    HIP_TRY(v->act.ensure(T * v->I));
+    HIP_TRY(v->pooled.ensure(S * v->H));
+    HIP_TRY(v->soft.ensure(S * v->text_hidden));
+    HIP_TRY(v->coord.ensure(2 * T));
+    HIP_TRY(v->apos.ensure(T));
+    HIP_TRY(v->rowlen.ensure(T));
+    HIP_TRY(v->bin_start.ensure(S + 1));
+    HIP_TRY(v->bin_patch.ensure(T));
+    HIP_TRY(v->offsets.ensure((size_t)b.B + 1));
+    HIP_TRY(v->tiles.ensure(std::max<size_t>(b.tiles.size(), 1)));
+    HIP_TRY(v->flag.ensure(1));
+    return SVL_OK;
+}
+
+svl_status upload_vis_meta(svl_vision_model *v, const VisBatch &b, hipStream_t s) {
+    HIP_TRY(hipMemcpyAsync(v->coord.p, b.coord.data(), b.coord.size() * 4, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(v->bin_start.p, b.bin_start.data(), b.bin_start.size() * 4,
+                           hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(v->bin_patch.p, b.bin_patch.data(), b.bin_patch.size() * 4,
+                           hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(v->offsets.p, b.offsets.data(), b.offsets.size() * 8,
+                           hipMemcpyHostToDevice, s));
+    if (!b.tiles.empty())
+        HIP_TRY(hipMemcpyAsync(v->tiles.p, b.tiles.data(), b.tiles.size() * sizeof(AttnTile),
+                               hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemsetAsync(v->flag.p, 0, sizeof(int), s));
+    return SVL_OK;
+}
+
+// The tower over the packed patches in d_pix (overwritten with the rescaled
+// values), enqueued on s (vision.rs:760-951). Soft tokens land in v->soft.
+svl_status enqueue_vision(svl_vision_model *v, const VisBatch &b, float *d_pix, hipStream_t s,
+                          float *h_hidden) {
+    const int64_t T = b.T, H = v->H, S = b.S;
+    if (T == 0) return SVL_OK;
+    int *flag = v->flag.p;
+    HIP_TRY(launch_positions(v->offsets.p, b.B, v->apos.p, v->rowlen.p, s));
+    HIP_TRY(launch_patch_scale(d_pix, d_pix, T * PATCH_VALUES, s));
+    {
+        GemmArgs g{d_pix, PATCH_VALUES, v->w_in, PATCH_VALUES, v->h.p, H, (int)T, (int)H,
+                   (int)PATCH_VALUES, EPI_STORE, 1.f, nullptr, 0, 0};
+        HIP_TRY(launch_gemm(g, s));
+    }
+    // position add fused with layer 0's input norm (the model has >= 1 layer)
+    HIP_TRY(launch_patch_pos(v->h.p, v->coord.p, v->pos_table, v->pos_size, v->layers[0].ln_in,
+                             v->n.p, T, (int)H, v->eps, flag, s));
+    if (h_hidden)
+        HIP_TRY(hipMemcpyAsync(h_hidden, v->h.p, (size_t)(T * H) * 4, hipMemcpyDeviceToHost, s));
+
+    const int64_t ldqkv = v->qd + 2 * v->kd;
+    for (int64_t l = 0; l < v->L; ++l) {
+        const VisLayer &ly = v->layers[(size_t)l];
+        {
+            GemmArgs g{v->n.p, H, ly.w_qkv, H, v->qkv.p, ldqkv, (int)T, (int)ldqkv, (int)H,
+                       EPI_STORE, 1.f, nullptr, 0, 0};
+            HIP_TRY(launch_gemm(g, s));
+        }
+        HIP_TRY(launch_qkv_post_axial(v->qkv.p, ldqkv, T, (int)v->NH, (int)v->NKV, (int)v->hd,
+                                      ly.q_norm, ly.k_norm, v->cos_t.p, v->sin_t.p, v->coord.p,
+                                      v->eps, flag, s));
+        {
+            AttnArgs a{};
+            a.q = v->qkv.p;
+            a.k = v->qkv.p + v->qd;
+            a.v = v->qkv.p + v->qd + v->kd;
+            a.out = v->attn.p;
+            a.ldq = a.ldk = a.ldv = ldqkv;
+            a.ldo = v->qd;
+            a.nh = (int)v->NH;
+            a.nkv = (int)v->NKV;
+            a.hd = (int)v->hd;
+            a.window = -1;   // vision.rs:880 sliding_window: None
+            a.scale = 1.0f;  // vision.rs:881
+            a.tiles = v->tiles.p;
+            a.n_tiles = (int)b.tiles.size();
+            a.pos = v->apos.p;
+            a.rowlen = v->rowlen.p;
+            a.tokens = T;
+            a.flag = flag;
+            HIP_TRY(launch_attention(a, s));
+        }
+        {
+            GemmArgs g{v->attn.p, v->qd, ly.w_o, v->qd, v->tmp.p, H, (int)T, (int)H, (int)v->qd,
+                       EPI_STORE, 1.f, nullptr, 0, 0};
+            HIP_TRY(launch_gemm(g, s));
+        }
+        HIP_TRY(launch_resnorm(v->tmp.p, ly.ln_post_attn, v->h.p, v->h.p, ly.ln_pre_ff, v->n.p,
+                               1.0f, T, (int)H, v->eps, flag, s));
+        {
+            GemmArgs g{v->n.p, H, ly.w_gu, H, v->act.p, v->I, (int)T, (int)(2 * v->I_pad), (int)H,
+                       EPI_GEGLU, 1.f, nullptr, 0, (int)v->I};
+            HIP_TRY(launch_gemm(g, s));
+        }
+        {
+            GemmArgs g{v->act.p, v->I, ly.w_down, v->I, v->tmp.p, H, (int)T, (int)H, (int)v->I,
+                       EPI_STORE, 1.f, nullptr, 0, 0};
+            HIP_TRY(launch_gemm(g, s));
+        }
+        const float *next = l + 1 < v->L ? v->layers[(size_t)l + 1].ln_in : nullptr;
+        HIP_TRY(launch_resnorm(v->tmp.p, ly.ln_post_ff, v->h.p, v->h.p, next,
+                               next ? v->n.p : nullptr, 1.0f, T, (int)H, v->eps, flag, s));
+        if (h_hidden)
+            HIP_TRY(hipMemcpyAsync(h_hidden + (size_t)((l + 1) * T * H), v->h.p,
+                                   (size_t)(T * H) * 4, hipMemcpyDeviceToHost, s));
+    }
+
+    // pool_patches + rms_norm_rows_unscaled + embedding projection
+    // (vision.rs:937-951).
+    HIP_TRY(launch_pool_bins(v->h.p, v->bin_start.p, v->bin_patch.p, S, (int)H, (float)(POOL * POOL),
+                             std::sqrt((float)H), v->eps, v->pooled.p, flag, s));
+    {
+        GemmArgs g{v->pooled.p, H, v->w_proj, H, v->soft.p, v->text_hidden, (int)S,
+                   (int)v->text_hidden, (int)H, EPI_STORE, 1.f, nullptr, 0, 0};
+        HIP_TRY(launch_gemm(g, s));
+    }
+    HIP_TRY(launch_finite_check(v->soft.p, S * v->text_hidden, flag, s));
+    return SVL_OK;
+}
+
+svl_status vis_finish(svl_vision_model *v, hipStream_t s) {
+    HIP_TRY(hipMemcpyAsync(v->h_flag, v->flag.p, sizeof(int), hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    if (*v->h_flag & FLAG_NONFINITE)
+        return fail(SVL_INTERNAL, "the vision tower produced a non-finite value");
+    return SVL_OK;
+}
+
+// Runs the tower for a batch with host pixels; the soft tokens stay in
+// v->soft (and are copied to out_soft when given). Caller holds v->mu.
+svl_status run_vision_host(svl_vision_model *v, const svl_image_patches *images, int32_t batch,
+                           VisBatch &b, float *out_soft, float *out_hidden) {
+    HIP_TRY(hipSetDevice(v->device));
+    ST_TRY(prepare_images(v, images, batch, true, b));
+    if (batch == 0) return SVL_OK;
+    ST_TRY(ensure_axial_tables(v, b.max_coord + 1));
+    ST_TRY(ensure_vis_workspace(v, b));
+    hipStream_t s = v->stream;
+    for (int i = 0; i < batch; ++i)
+        HIP_TRY(hipMemcpyAsync(v->pix.p + b.offsets[i] * PATCH_VALUES, images[i].pixel_values,
+                               (size_t)(images[i].valid_patches * PATCH_VALUES) * 4,
+                               hipMemcpyHostToDevice, s));
+    ST_TRY(upload_vis_meta(v, b, s));
+    ST_TRY(enqueue_vision(v, b, v->pix.p, s, out_hidden));
+    if (out_soft)
+        HIP_TRY(hipMemcpyAsync(out_soft, v->soft.p, (size_t)(b.S * v->text_hidden) * 4,
+                               hipMemcpyDeviceToHost, s));
+    return vis_finish(v, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+svl_status svl_vision_model_create(svl_ctx *ctx, const svl_vision_config *cfg, int64_t text_hidden,
+                                   const svl_tensor_view *tensors, size_t n_tensors,
+                                   svl_vision_model **out) {
+    if (!ctx || !out) return fail(SVL_USAGE, "context or output pointer is null");
+    ST_TRY(validate_vision_config(cfg, text_hidden));
+    const int device = ctx->device;
+    HIP_TRY(hipSetDevice(device));
+    const ShapeList shapes = vision_tensor_shapes(cfg, text_hidden);
+    TensorIndex by_name;
+    ST_TRY(check_inventory(tensors, n_tensors, shapes, {"vision_tower.", "embed_vision."}, "vision",
+                           MAX_VISION_WEIGHT_ELEMENTS, by_name));
+
+    auto v = new svl_vision_model();
+    std::unique_ptr<svl_vision_model> guard(v);
+    v->device = device;
+    v->H = cfg->hidden_size;
+    v->I = cfg->intermediate_size;
+    v->L = cfg->num_hidden_layers;
+    v->NH = cfg->num_attention_heads;
+    v->NKV = cfg->num_key_value_heads;
+    v->hd = cfg->head_dim;
+    v->pos_size = cfg->position_embedding_size;
+    v->text_hidden = text_hidden;
+    v->eps = (float)cfg->rms_norm_eps;
+    v->theta = (float)cfg->rope_theta;
+    v->I_pad = (v->I + 31) / 32 * 32;
+    v->qd = v->NH * v->hd;
+    v->kd = v->NKV * v->hd;
+    if (v->H % 4 || v->H > 2048)
+        return fail(SVL_UNSUPPORTED, "vision hidden size %lld is not a multiple of 4 up to 2048",
+                    (long long)v->H);
+    if (v->L == 0) return fail(SVL_UNSUPPORTED, "a vision tower without layers is not supported");
+    // axial_inv_freq (vision.rs:1047-1065)
+    const int64_t spatial = v->hd / 2;
+    for (int64_t i = 0; i < spatial / 2; ++i) {
+        const float exponent = (float)(2 * i) / (float)spatial;
+        const float value = 1.0f / std::pow(v->theta, exponent);
+        if (!std::isfinite(value)) return fail(SVL_INTERNAL, "axial RoPE frequency is not finite");
+        v->inv_freq.push_back(value);
+    }
+
+    auto up = [&](const std::string &name, float **dst) -> svl_status {
+        std::vector<float> a;
+        ST_TRY(decode_named(by_name, name, a));
+        return upload_owned(v->allocations, a.data(), a.size(), dst);
+    };
+    ST_TRY(up("vision_tower.patch_embedder.input_proj.weight", &v->w_in));
+    ST_TRY(up("vision_tower.patch_embedder.position_embedding_table", &v->pos_table));
+    ST_TRY(up("embed_vision.embedding_projection.weight", &v->w_proj));
+    v->layers.resize((size_t)v->L);
+    std::vector<float> a, b2, c2;
+    for (int64_t l = 0; l < v->L; ++l) {
+        VisLayer &ly = v->layers[(size_t)l];
+        const std::string p = "vision_tower.encoder.layers." + std::to_string(l) + ".";
+        std::vector<float> qkv((size_t)((v->qd + 2 * v->kd) * v->H));
+        ST_TRY(decode_named(by_name, p + "self_attn.q_proj.linear.weight", a));
+        std::copy(a.begin(), a.end(), qkv.begin());
+        ST_TRY(decode_named(by_name, p + "self_attn.k_proj.linear.weight", a));
+        std::copy(a.begin(), a.end(), qkv.begin() + v->qd * v->H);
+        ST_TRY(decode_named(by_name, p + "self_attn.v_proj.linear.weight", a));
+        std::copy(a.begin(), a.end(), qkv.begin() + (v->qd + v->kd) * v->H);
+        ST_TRY(upload_owned(v->allocations, qkv.data(), qkv.size(), &ly.w_qkv));
+        ST_TRY(up(p + "self_attn.o_proj.linear.weight", &ly.w_o));
+        ST_TRY(decode_named(by_name, p + "mlp.gate_proj.linear.weight", b2));
+        ST_TRY(decode_named(by_name, p + "mlp.up_proj.linear.weight", c2));
+        const std::vector<float> gu = interleave_gate_up(b2, c2, v->I, v->I_pad, v->H);
+        ST_TRY(upload_owned(v->allocations, gu.data(), gu.size(), &ly.w_gu));
+        ST_TRY(up(p + "mlp.down_proj.linear.weight", &ly.w_down));
+        ST_TRY(up(p + "input_layernorm.weight", &ly.ln_in));
+        ST_TRY(up(p + "post_attention_layernorm.weight", &ly.ln_post_attn));
+        ST_TRY(up(p + "pre_feedforward_layernorm.weight", &ly.ln_pre_ff));
+        ST_TRY(up(p + "post_feedforward_layernorm.weight", &ly.ln_post_ff));
+        ST_TRY(up(p + "self_attn.q_norm.weight", &ly.q_norm));
+        ST_TRY(up(p + "self_attn.k_norm.weight", &ly.k_norm));
+    }
+    HIP_TRY(hipStreamCreateWithFlags(&v->stream, hipStreamNonBlocking));
+    HIP_TRY(hipHostMalloc((void **)&v->h_flag, sizeof(int), hipHostMallocDefault));
+    *out = guard.release();
+    return SVL_OK;
+}
+
+svl_status svl_vision_model_destroy(svl_vision_model *model) {
+    delete model;
+    return SVL_OK;
+}
+
+svl_status svl_vision_forward_batch(svl_vision_model *v, const svl_image_patches *images,
+                                    int32_t batch, float *out_soft, float *out_hidden) {
+    if (!v || !out_soft) return fail(SVL_USAGE, "model and out_soft are required");
+    std::lock_guard<std::mutex> lock(v->mu);
+    VisBatch b;
+    return run_vision_host(v, images, batch, b, out_soft, out_hidden);
+}
+
+svl_status svl_vision_forward_device(svl_vision_model *v, float *d_pixels,
+                                     const svl_image_patches *images, int32_t batch, float *d_out,
+                                     void *stream) {
+    if (!v || !d_pixels || !d_out) return fail(SVL_USAGE, "model, pixels and output are required");
+    std::lock_guard<std::mutex> lock(v->mu);
+    HIP_TRY(hipSetDevice(v->device));
+    VisBatch b;
+    ST_TRY(prepare_images(v, images, batch, false, b));
+    if (batch == 0) return SVL_OK;
+    ST_TRY(ensure_axial_tables(v, b.max_coord + 1));
+    ST_TRY(ensure_vis_workspace(v, b));
+    hipStream_t s = stream ? (hipStream_t)stream : v->stream;
+    ST_TRY(upload_vis_meta(v, b, s));
+    ST_TRY(enqueue_vision(v, b, d_pixels, s, nullptr));
+    HIP_TRY(hipMemcpyAsync(d_out, v->soft.p, (size_t)(b.S * v->text_hidden) * 4,
+                           hipMemcpyDeviceToDevice, s));
+    return vis_finish(v, s);
+}
+
+svl_status svl_image_embed_batch(svl_vision_model *v, svl_text_model *text,
+                                 const svl_image_special_tokens *tokens,
+                                 const svl_image_patches *images, int32_t batch, int64_t dimension,
+                                 float *out) {
+    if (!v || !text || !tokens || !out)
+        return fail(SVL_USAGE, "models, special tokens and output are required");
+    // image.rs:215-221
+    const int64_t E = text_embedding_dim(text);
+    if (dimension <= 0 || dimension > E)
+        return fail(SVL_INTERNAL, "embedding dimension %lld is outside 1..=%lld",
+                    (long long)dimension, (long long)E);
+    if (text_device(text) != v->device)
+        return fail(SVL_USAGE, "the vision and text models live on different devices");
+    if (text_hidden_size(text) != v->text_hidden)
+        return fail(SVL_USAGE, "the vision projection width %lld is not the text hidden size %lld",
+                    (long long)v->text_hidden, (long long)text_hidden_size(text));
+    std::lock_guard<std::mutex> lock(v->mu);
+    VisBatch b;
+    ST_TRY(run_vision_host(v, images, batch, b, nullptr, nullptr));
+    if (batch == 0) return SVL_OK;
+    // image.rs:224-244: <bos> <boi> <image> x soft <eoi> <eos>, features at 2.
+    std::vector<int64_t> offsets(1, 0);
+    for (int i = 0; i < batch; ++i) {
+        const int64_t seq = images[i].soft_tokens + 4;
+        if (seq > MAX_TEXT_TOKENS)
+            return fail(SVL_LIMIT, "image %d: image prompt has %lld tokens, above the %lld-token context",
+                        i, (long long)seq, (long long)MAX_TEXT_TOKENS);
+        offsets.push_back(offsets.back() + seq);
+    }
+    std::vector<uint32_t> ids((size_t)offsets.back());
+    std::vector<int32_t> featmap((size_t)offsets.back(), -1);
+    for (int i = 0; i < batch; ++i) {
+        const int64_t o = offsets[i], soft = images[i].soft_tokens;
+        ids[(size_t)o] = tokens->bos;
+        ids[(size_t)o + 1] = tokens->boi;
+        for (int64_t k = 0; k < soft; ++k) {
+            ids[(size_t)(o + 2 + k)] = tokens->image;
+            featmap[(size_t)(o + 2 + k)] = (int32_t)(b.soft_offsets[i] + k);
+        }
+        ids[(size_t)(o + 2 + soft)] = tokens->eoi;
+        ids[(size_t)(o + 3 + soft)] = tokens->eos;
+    }
+    std::vector<float> normalized((size_t)(batch * E));
+    ST_TRY(text_forward_with_device_features(text, ids.data(), offsets.data(), batch,
+                                             featmap.data(), v->soft.p, normalized.data()));
+    for (int i = 0; i < batch; ++i)
+        ST_TRY(svl_truncate_and_normalize(normalized.data() + (size_t)i * E, (size_t)E,
+                                          (size_t)dimension, out + (size_t)i * dimension));
+    return SVL_OK;
+}
+
+}  // extern "C"

@@ -99,6 +99,8 @@ EXPORTED = [
     "svl_linear", "svl_rms_norm_rows", "svl_rope_with_inv_freq", "svl_rope_inv_freq",
     "svl_bidirectional_attention", "svl_gelu_tanh", "svl_geglu", "svl_add", "svl_mean_pool",
     "svl_l2_normalize", "svl_synth_uniform", "svl_synth_ids", "svl_synth_lengths",
+    "svl_vision_model_create", "svl_vision_model_destroy", "svl_vision_forward_batch",
+    "svl_vision_forward_device", "svl_image_embed_batch",
 ]
 
 _lib = None
@@ -167,6 +169,12 @@ def lib():
                                     ctypes.c_size_t, vp]
         L.svl_synth_lengths.argtypes = [ctypes.c_uint64, ctypes.c_uint64, i64, i64,
                                         ctypes.c_size_t, vp]
+        L.svl_vision_model_create.argtypes = [vp, vp, i64, ctypes.POINTER(_TensorView),
+                                              ctypes.c_size_t, ctypes.POINTER(vp)]
+        L.svl_vision_model_destroy.argtypes = [vp]
+        L.svl_vision_forward_batch.argtypes = [vp, vp, i32, vp, vp]
+        L.svl_vision_forward_device.argtypes = [vp, vp, vp, i32, vp, vp]
+        L.svl_image_embed_batch.argtypes = [vp, vp, vp, vp, i32, i64, vp]
         _lib = L
         return L
 
@@ -467,6 +475,34 @@ class Device:
         return cls._cache[ordinal]
 
 
+def tensor_views(weights: dict):
+    """svl_tensor_view array over a name -> RawTensor / array mapping.
+    Returns (array, count, keep-alive list); F32 and BF16 payloads pass
+    through unchanged, F16 is rejected (src/tensor/dtype.rs)."""
+    views, keep = [], []
+    for name, t in weights.items():
+        if isinstance(t, RawTensor):
+            dtype, shape, data = (1 if t.dtype == "BF16" else 0), t.shape, t.data
+        else:
+            a = np.asarray(t)
+            if a.dtype == np.float16:
+                raise _unsupported(f"tensor {name} is F16, which is forbidden")
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            dtype, shape, data = 0, a.shape, a
+        data = np.ascontiguousarray(data)
+        bname = name.encode()
+        keep += [data, bname]
+        v = _TensorView()
+        v.name = bname
+        v.dtype = dtype
+        v.ndim = len(shape)
+        for i, d in enumerate(shape):
+            v.shape[i] = int(d)
+        v.data = data.ctypes.data
+        views.append(v)
+    return (_TensorView * len(views))(*views), len(views), keep
+
+
 class ForwardOutput:
     """text.rs:38-75."""
 
@@ -496,32 +532,10 @@ class TextModel:
     def __init__(self, config: TextConfig, weights: dict, device: Device | None = None):
         self.config = config
         self.device = device or Device.get(0)
-        names, views, keep = [], [], []
-        for name, t in weights.items():
-            if isinstance(t, RawTensor):
-                dtype, shape, data = (1 if t.dtype == "BF16" else 0), t.shape, t.data
-            else:
-                a = np.asarray(t)
-                if a.dtype == np.float16:
-                    raise _unsupported(f"tensor {name} is F16, which is forbidden")
-                a = np.ascontiguousarray(a, dtype=np.float32)
-                dtype, shape, data = 0, a.shape, a
-            data = np.ascontiguousarray(data)
-            keep.append(data)
-            bname = name.encode()
-            names.append(bname)
-            v = _TensorView()
-            v.name = bname
-            v.dtype = dtype
-            v.ndim = len(shape)
-            for i, d in enumerate(shape):
-                v.shape[i] = int(d)
-            v.data = data.ctypes.data
-            views.append(v)
-        arr = (_TensorView * len(views))(*views)
+        arr, n, keep = tensor_views(weights)  # alive until the library has copied them
         cfg = config._c()
         h = ctypes.c_void_p()
-        _check(lib().svl_text_model_create(self.device.handle, ctypes.byref(cfg), arr, len(views),
+        _check(lib().svl_text_model_create(self.device.handle, ctypes.byref(cfg), arr, n,
                                            ctypes.byref(h)))
         self.handle = h
 

@@ -96,3 +96,69 @@ def row_lengths(batch: int, lo: int, hi: int, seed: int = 1):
 
 def dumps(config: dict) -> str:
     return json.dumps(config)
+
+
+# ---- vision tower -------------------------------------------------------------
+#
+# Config V is the frozen gemma4_vision shape (docs/architecture.md:553-558:
+# hidden 768, 16 layers, 12 heads of dim 64, FFN 3072, axial theta 100, eps
+# 1e-6, patch 16, pool 3). position_embedding_size is not stated there; 10240
+# entries per axis covers every patch grid the preprocessing can produce and
+# only sets the size of the position table. Weights, one SplitMix64 stream per
+# tensor in VisionConfig::tensor_shapes order after an offset of 100000:
+#   linear [out, in]        U(-sqrt(3/in), +sqrt(3/in))
+#   position table          U(-0.5, 0.5)
+#   RMSNorm weights         1 + U(-0.1, 0.1)
+#   q_norm, k_norm          U(0.3, 0.4)   (score std ~ 1 at head_dim 64, scale 1.0)
+# Images: uint8 uniform noise rescaled by 1/255 (as preprocess.rs does),
+# generated directly per patch value (iid noise, so the patch cut does not
+# change the distribution).
+
+VISION_STREAM_BASE = 100_000
+
+
+def config_v(layers=16, text=None) -> dict:
+    """Composite config: text config (shape A by default) plus vision_config V."""
+    c = {"text_config": text or config_a()}
+    c["vision_config"] = {
+        "model_type": "gemma4_vision", "dtype": "float32", "hidden_size": 768,
+        "intermediate_size": 3072, "num_hidden_layers": layers, "num_attention_heads": 12,
+        "num_key_value_heads": 12, "head_dim": 64, "patch_size": 16, "pooling_kernel_size": 3,
+        "position_embedding_size": 10240, "rms_norm_eps": 1e-06,
+        "hidden_activation": "gelu_pytorch_tanh", "attention_bias": False,
+        "attention_dropout": 0.0, "use_clipped_linears": False, "standardize": False,
+        "rope_parameters": {"rope_type": "axial", "rope_theta": 100.0}}
+    return c
+
+
+def vision_weights(config: dict, text_hidden: int, seed: int = 0) -> dict:
+    import svl_vision
+    vc = svl_vision.VisionConfig.from_json_value(config)
+    out = {}
+    for k, (name, shape) in enumerate(vc.tensor_shapes(text_hidden)):
+        n = int(np.prod(shape))
+        if name.endswith("position_embedding_table"):
+            lo, hi = -0.5, 0.5
+        elif name.endswith("q_norm.weight") or name.endswith("k_norm.weight"):
+            lo, hi = 0.3, 0.4
+        elif len(shape) == 1:
+            lo, hi = 0.9, 1.1
+        else:
+            b = math.sqrt(3.0 / shape[-1])
+            lo, hi = -b, b
+        out[name] = svl_amd.synth_uniform(seed, VISION_STREAM_BASE + k, lo, hi, n).reshape(shape)
+    return out
+
+
+def image_patches(batch: int, grid_width: int = 48, grid_height: int = 48, seed: int = 2,
+                  max_patches: int | None = None):
+    """`batch` noise images of grid_width x grid_height patches (768 x 768
+    pixels at the default 48 x 48), one id stream per image."""
+    import svl_vision
+    out = []
+    valid = grid_width * grid_height
+    for i in range(batch):
+        u8 = svl_amd.synth_ids(seed, 10 + i, 256, valid * svl_vision.PATCH_VALUES)
+        pix = u8.astype(np.float32) * svl_vision.RESCALE_FACTOR
+        out.append(svl_vision.ImagePatches.from_grid(pix, grid_width, grid_height, max_patches))
+    return out

@@ -90,3 +90,74 @@ def randomize_1d(w, seed=0):
         else:
             out[k] = a
     return out
+
+
+# ---- vision tower (src/model/vision.rs:742-1148) ---------------------------------
+
+def axial_inv_freq64(hd, theta):
+    spatial = hd // 2
+    return 1.0 / (float(theta) ** (np.arange(0, spatial, 2, dtype=np.float64) / spatial))
+
+
+def axial_rope64(x, pos, inv_freq):
+    """x [seq, heads, hd]; half 0 rotates by pos[:, 0] (x), half 1 by pos[:, 1]
+    (y); within a half, quarter i pairs with quarter i + hd/4."""
+    hd = x.shape[-1]
+    half, q = hd // 2, hd // 4
+    out = np.array(x, dtype=np.float64)
+    for hf in (0, 1):
+        ang = pos[:, hf].astype(np.float64)[:, None] * np.asarray(inv_freq, np.float64)[None, :]
+        c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+        a = x[..., hf * half: hf * half + q].astype(np.float64)
+        b = x[..., hf * half + q: (hf + 1) * half].astype(np.float64)
+        out[..., hf * half: hf * half + q] = a * c - b * s
+        out[..., hf * half + q: (hf + 1) * half] = b * c + a * s
+    return out
+
+
+def pool_patches64(h, pos, grid_w, grid_h, soft):
+    pw = grid_w // 3
+    out = np.zeros((soft, h.shape[1]))
+    for p in range(h.shape[0]):
+        out[pos[p, 0] // 3 + pw * (pos[p, 1] // 3)] += h[p]
+    return out / 9.0 * np.sqrt(h.shape[1])
+
+
+def vision_forward64(vc, w, pix, pos, grid, soft, swap_axes=False):
+    """vc: oracle.resolve_vision_config(...) dict; w: name -> array;
+    pix [valid, 768]; pos [valid, 2]. swap_axes rotates the first half by y
+    and the second by x (a planted mistake for the sensitivity test)."""
+    H, L = vc["hidden_size"], vc["num_hidden_layers"]
+    NH, NKV, hd, eps = vc["num_attention_heads"], vc["num_key_value_heads"], vc["head_dim"], vc["rms_norm_eps"]
+    f64 = lambda n: w[n].astype(np.float64)
+    valid = pix.shape[0]
+    h = (2.0 * (pix.astype(np.float64) - 0.5)) @ f64("vision_tower.patch_embedder.input_proj.weight").T
+    table = f64("vision_tower.patch_embedder.position_embedding_table")
+    h = h + table[0][pos[:, 0]] + table[1][pos[:, 1]]
+    states = [h.copy()]
+    inv = axial_inv_freq64(hd, vc["rope_theta"])
+    rpos = pos[:, ::-1] if swap_axes else pos
+    for l in range(L):
+        p = f"vision_tower.encoder.layers.{l}."
+        n = rms(h, w[p + "input_layernorm.weight"], eps)
+        q = (n @ f64(p + "self_attn.q_proj.linear.weight").T).reshape(valid, NH, hd)
+        k = (n @ f64(p + "self_attn.k_proj.linear.weight").T).reshape(valid, NKV, hd)
+        v = (n @ f64(p + "self_attn.v_proj.linear.weight").T).reshape(valid, NKV, hd)
+        q = axial_rope64(rms(q, w[p + "self_attn.q_norm.weight"], eps), rpos, inv)
+        k = axial_rope64(rms(k, w[p + "self_attn.k_norm.weight"], eps), rpos, inv)
+        v = rms(v, None, eps)
+        out = np.zeros((valid, NH, hd))
+        for hh in range(NH):
+            g = hh // (NH // NKV)
+            s = q[:, hh] @ k[:, g].T
+            pr = np.exp(s - s.max(1, keepdims=True))
+            out[:, hh] = (pr / pr.sum(1, keepdims=True)) @ v[:, g]
+        a = out.reshape(valid, NH * hd) @ f64(p + "self_attn.o_proj.linear.weight").T
+        h = h + rms(a, w[p + "post_attention_layernorm.weight"], eps)
+        n = rms(h, w[p + "pre_feedforward_layernorm.weight"], eps)
+        act = gelu(n @ f64(p + "mlp.gate_proj.linear.weight").T) * (n @ f64(p + "mlp.up_proj.linear.weight").T)
+        h = h + rms(act @ f64(p + "mlp.down_proj.linear.weight").T, w[p + "post_feedforward_layernorm.weight"], eps)
+        states.append(h.copy())
+    pooled = pool_patches64(h, pos, grid[0], grid[1], soft)
+    proj = rms(pooled, None, eps) @ f64("embed_vision.embedding_projection.weight").T
+    return dict(pooled=proj, hidden_states=np.stack(states))

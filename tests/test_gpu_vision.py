@@ -1,0 +1,313 @@
+"""GPU parity of the vision tower (VisionModel::forward, src/model/vision.rs:
+742-959) and of the image prompt glue (ImageEmbedder::embed_impl,
+src/model/image.rs:209-253) through the C ABI.
+
+* a small random tower (hidden 64, 4 heads / 2 KV heads of dim 16: the
+  generic attention kernel) and config V at 2 layers (12 heads of dim 64: the
+  MFMA attention kernel) against the CPU oracle, image by image, over ragged
+  batches with padding rows;
+* config V at full depth on a full 768 x 768 image (48 x 48 patches): every
+  stage checked against a float64 restatement applied to the GPU's own
+  input of that stage (patch embedding, layers 1 / 8 / 16, pooling and
+  projection), since the scalar oracle needs minutes at that size;
+* batching and device-resident variants bit-identical to single calls;
+* the image embedder (tower + prompt + text encoder with soft tokens)
+  against the oracle chain at Matryoshka dims 768 and 128;
+* the error taxonomy of vision.rs / image.rs."""
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+
+import ref64
+import svl_amd as S
+import svl_synth
+import svl_vision as V
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 1e-4
+MIN_COS = 0.99999
+
+
+def cosine(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def small_config(layers=2):
+    c = svl_synth.config_v(layers)
+    c["vision_config"].update(hidden_size=64, intermediate_size=96, num_attention_heads=4,
+                              num_key_value_heads=2, head_dim=16, position_embedding_size=16)
+    return c
+
+
+def build(c, text_hidden, seed=7):
+    w = svl_synth.vision_weights(c, text_hidden, seed=seed)
+    gpu = V.VisionModel(V.VisionConfig.from_json_value(c), w, text_hidden)
+    return w, gpu, O.OracleVisionModel(c, w, text_hidden)
+
+
+def oracle_all(om, patches, capture=False):
+    with ThreadPoolExecutor(max_workers=min(8, len(patches))) as ex:
+        return list(ex.map(lambda p: om.forward(p, capture_hidden=capture), patches))
+
+
+def check_soft(got, want, label):
+    d = float(np.abs(got - want).max())
+    c = cosine(got, want)
+    print(f"{label}: soft tokens {got.shape} max-abs {d:.3g} cosine {c:.9f}", flush=True)
+    assert d <= MAX_ABS and c >= MIN_COS, f"{label}: max-abs {d:.3g} cosine {c:.9f}"
+
+
+@pytest.fixture(scope="module")
+def small():
+    return build(small_config(), 48)
+
+
+@pytest.fixture(scope="module")
+def tower_v2():
+    return build(svl_synth.config_v(2), 768, seed=11)
+
+
+def test_small_tower_matches_oracle(small):
+    w, gpu, om = small
+    patches = [svl_synth.image_patches(1, 6, 9, seed=21, max_patches=63)[0],
+               svl_synth.image_patches(1, 9, 6, seed=22)[0]]
+    got = gpu.forward_batch(patches, capture_hidden=True)
+    want = oracle_all(om, patches, capture=True)
+    for i, (g, o) in enumerate(zip(got, want)):
+        assert g.soft_tokens() == o["soft_tokens"] == 6
+        hs = np.stack(g.hidden_states())
+        np.testing.assert_allclose(hs, o["hidden_states"], rtol=1e-4, atol=1e-4)
+        check_soft(g.pooled(), o["pooled"], f"small image {i}")
+
+
+def test_config_v_two_layers_matches_oracle(tower_v2):
+    w, gpu, om = tower_v2
+    patches = [svl_synth.image_patches(1, 12, 12, seed=31, max_patches=160)[0],
+               svl_synth.image_patches(1, 9, 15, seed=32)[0],
+               svl_synth.image_patches(1, 6, 6, seed=33)[0]]
+    got = gpu.forward_batch(patches, capture_hidden=True)
+    want = oracle_all(om, patches, capture=True)
+    for i, (g, o) in enumerate(zip(got, want)):
+        hs = np.stack(g.hidden_states())
+        d = np.abs(hs - o["hidden_states"]).max(axis=(1, 2))
+        print(f"image {i}: per-layer hidden max-abs {d}", flush=True)
+        np.testing.assert_allclose(hs, o["hidden_states"], rtol=1e-4, atol=2e-4)
+        check_soft(g.pooled(), o["pooled"], f"config V image {i}")
+
+
+def test_batch_is_bit_identical_to_single_calls(tower_v2):
+    w, gpu, om = tower_v2
+    patches = svl_synth.image_patches(3, 12, 9, seed=41)
+    patches.append(svl_synth.image_patches(1, 6, 15, seed=42)[0])
+    batch = gpu.forward_batch(patches)
+    for i, p in enumerate(patches):
+        one = gpu.forward(p).pooled()
+        assert np.array_equal(one, batch[i].pooled()), f"image {i}"
+    again = gpu.forward_batch(patches[::-1])
+    for i, p in enumerate(patches[::-1]):
+        assert np.array_equal(again[i].pooled(), batch[len(patches) - 1 - i].pooled())
+
+
+def test_device_resident_matches_host(tower_v2):
+    import torch
+    w, gpu, om = tower_v2
+    patches = svl_synth.image_patches(2, 12, 12, seed=51)
+    host = np.concatenate([p.pooled() for p in gpu.forward_batch(patches)])
+    pix = np.concatenate([p.pixel_values[: p.valid_patches] for p in patches])
+    d_pix = torch.from_numpy(pix).to("cuda:0")
+    d_out = torch.empty((sum(p.soft_tokens for p in patches), 768), device="cuda:0")
+    torch.cuda.synchronize()
+    gpu.forward_device(d_pix.data_ptr(), patches, d_out.data_ptr())
+    assert np.array_equal(d_out.cpu().numpy(), host)
+
+
+def test_full_size_image_every_stage(tmp_path):
+    """Config V, 16 layers, one 768 x 768 image (2304 patches, 256 soft
+    tokens). Each checked stage is recomputed in float64 from the GPU's own
+    input to that stage."""
+    c = svl_synth.config_v(16)
+    w = svl_synth.vision_weights(c, 768, seed=13)
+    gpu = V.VisionModel(V.VisionConfig.from_json_value(c), w, 768)
+    p = svl_synth.image_patches(1, 48, 48, seed=2)[0]
+    out = gpu.forward(p, capture_hidden=True)
+    hs = out.hidden_states()
+    assert len(hs) == 17 and hs[0].shape == (2304, 768)
+    assert out.pooled().shape == (256, 768)
+    vc = O.resolve_vision_config(c)
+    pos = p.positions[:2304]
+
+    def rel(g, r):
+        return float(np.abs(g - r).max() / np.abs(r).max())
+
+    # patch embedding + position add
+    pe = (2.0 * (p.pixel_values[:2304].astype(np.float64) - 0.5)) @ \
+        w["vision_tower.patch_embedder.input_proj.weight"].astype(np.float64).T
+    table = w["vision_tower.patch_embedder.position_embedding_table"].astype(np.float64)
+    pe += table[0][pos[:, 0]] + table[1][pos[:, 1]]
+    e = rel(hs[0], pe)
+    print(f"patch embedding: relative max error {e:.3g}", flush=True)
+    assert e <= 1e-5
+
+    # single layers: restate layer l in float64 from the GPU's layer l-1 output
+    one = dict(vc, num_hidden_layers=1)
+    for l in (1, 8, 16):
+        wl = {k: v for k, v in w.items() if not k.startswith("vision_tower.encoder.layers.")}
+        pre = f"vision_tower.encoder.layers.{l - 1}."
+        for k, v in w.items():
+            if k.startswith(pre):
+                wl["vision_tower.encoder.layers.0." + k[len(pre):]] = v
+        ref = _layer64(one, wl, hs[l - 1].astype(np.float64), pos)
+        e = rel(hs[l], ref)
+        print(f"layer {l}: relative max error {e:.3g}", flush=True)
+        assert e <= 1e-4
+
+    # pool + unscaled norm + projection from the GPU's last hidden state
+    pooled = ref64.pool_patches64(hs[16].astype(np.float64), pos, 48, 48, 256)
+    soft = ref64.rms(pooled, None, vc["rms_norm_eps"]) @ \
+        w["embed_vision.embedding_projection.weight"].astype(np.float64).T
+    d = float(np.abs(out.pooled() - soft).max())
+    c_ = cosine(out.pooled(), soft)
+    print(f"soft tokens: max-abs {d:.3g} cosine {c_:.9f}", flush=True)
+    assert d <= MAX_ABS and c_ >= MIN_COS
+    assert np.isfinite(out.pooled()).all()
+
+
+def _layer64(vc, w, h, pos):
+    """One encoder layer of vision.rs:816-935 in float64 (ref64's loop body)."""
+    H, NH, NKV, hd, eps = (vc["hidden_size"], vc["num_attention_heads"],
+                           vc["num_key_value_heads"], vc["head_dim"], vc["rms_norm_eps"])
+    f64 = lambda n: w[n].astype(np.float64)
+    p = "vision_tower.encoder.layers.0."
+    valid = h.shape[0]
+    inv = ref64.axial_inv_freq64(hd, vc["rope_theta"])
+    n = ref64.rms(h, w[p + "input_layernorm.weight"], eps)
+    q = (n @ f64(p + "self_attn.q_proj.linear.weight").T).reshape(valid, NH, hd)
+    k = (n @ f64(p + "self_attn.k_proj.linear.weight").T).reshape(valid, NKV, hd)
+    v = (n @ f64(p + "self_attn.v_proj.linear.weight").T).reshape(valid, NKV, hd)
+    q = ref64.axial_rope64(ref64.rms(q, w[p + "self_attn.q_norm.weight"], eps), pos, inv)
+    k = ref64.axial_rope64(ref64.rms(k, w[p + "self_attn.k_norm.weight"], eps), pos, inv)
+    v = ref64.rms(v, None, eps)
+    out = np.zeros((valid, NH, hd))
+    for hh in range(NH):
+        g = hh // (NH // NKV)
+        s = q[:, hh] @ k[:, g].T
+        pr = np.exp(s - s.max(1, keepdims=True))
+        out[:, hh] = (pr / pr.sum(1, keepdims=True)) @ v[:, g]
+    a = out.reshape(valid, NH * hd) @ f64(p + "self_attn.o_proj.linear.weight").T
+    h = h + ref64.rms(a, w[p + "post_attention_layernorm.weight"], eps)
+    n = ref64.rms(h, w[p + "pre_feedforward_layernorm.weight"], eps)
+    act = ref64.gelu(n @ f64(p + "mlp.gate_proj.linear.weight").T) * \
+        (n @ f64(p + "mlp.up_proj.linear.weight").T)
+    return h + ref64.rms(act @ f64(p + "mlp.down_proj.linear.weight").T,
+                         w[p + "post_feedforward_layernorm.weight"], eps)
+
+
+# ---- image prompt glue ----------------------------------------------------------------
+
+TOKENS = V.ImageSpecialTokens(bos=2, eos=1, pad=0, boi=1000, image=1001, eoi=1002)
+
+
+@pytest.fixture(scope="module")
+def embedder():
+    tc = svl_synth.config_a(layers=2, vocab=1024)
+    c = svl_synth.config_v(2, text=tc)
+    tw = svl_synth.weights(tc, seed=3)
+    vw = svl_synth.vision_weights(c, 768, seed=17)
+    tm = S.TextModel(S.TextConfig.from_json_value(tc), tw)
+    vm = V.VisionModel(V.VisionConfig.from_json_value(c), vw, 768)
+    return (V.ImageEmbedder(tm, vm, TOKENS), O.OracleTextModel(tc, tw),
+            O.OracleVisionModel(c, vw, 768))
+
+
+def test_image_embedder_matches_oracle(embedder):
+    emb, ot, ov = embedder
+    patches = [svl_synth.image_patches(1, 12, 12, seed=61)[0],
+               svl_synth.image_patches(1, 9, 6, seed=62)[0]]
+    for dim in (768, 128):
+        got = emb.embed_batch(patches, dim)
+        for i, p in enumerate(patches):
+            soft = ov.forward(p)["pooled"]
+            ids = [TOKENS.bos, TOKENS.boi] + [TOKENS.image] * p.soft_tokens + [TOKENS.eoi,
+                                                                                TOKENS.eos]
+            ref = ot.forward(ids, features=soft, feature_start=2,
+                             feature_count=p.soft_tokens)["normalized"]
+            ref = O.truncate_and_normalize(ref, dim)
+            d = float(np.abs(got[i] - ref).max())
+            c = cosine(got[i], ref)
+            print(f"image {i} dim {dim}: max-abs {d:.3g} cosine {c:.9f}", flush=True)
+            assert d <= MAX_ABS and c >= MIN_COS
+    one = emb.embed_patches(patches[1], 768)
+    assert np.array_equal(one, emb.embed_batch(patches, 768)[1])
+
+
+def test_image_embedder_rejects_bad_dimensions(embedder):
+    emb, _, _ = embedder
+    p = svl_synth.image_patches(1, 6, 6, seed=63)[0]
+    for dim in (0, 769):
+        with pytest.raises(S.SvlError) as e:
+            emb.embed_patches(p, dim)
+        assert e.value.kind == "Internal"
+
+
+# ---- error taxonomy ---------------------------------------------------------------------
+
+def test_vision_error_taxonomy(small):
+    w, gpu, om = small
+
+    def fresh():
+        return svl_synth.image_patches(1, 6, 6, seed=71)[0]
+
+    p = fresh()
+    p.valid_patches = 0
+    with pytest.raises(S.SvlError) as e:
+        gpu.forward(p)
+    assert e.value.kind == "Corrupt"
+    p = fresh()
+    p.positions[3] = [16, 0]
+    with pytest.raises(S.SvlError) as e:
+        gpu.forward(p)
+    assert e.value.kind == "Corrupt"
+    p = fresh()
+    p.positions[2] = [-1, 0]
+    with pytest.raises(S.SvlError) as e:
+        gpu.forward(p)
+    assert e.value.kind == "Internal"
+    p = fresh()
+    p.patch_grid = (4, 9)
+    with pytest.raises(S.SvlError) as e:
+        gpu.forward(p)
+    assert e.value.kind == "Internal"
+    p = fresh()
+    p.max_patches = 10
+    with pytest.raises(S.SvlError) as e:
+        gpu.forward(p)
+    assert e.value.kind == "Internal"
+    # the model still works after rejected calls
+    ok = gpu.forward(fresh()).pooled()
+    assert np.isfinite(ok).all()
+
+
+def test_vision_weight_inventory(small):
+    w, gpu, om = small
+    c = small_config()
+    vc = V.VisionConfig.from_json_value(c)
+    missing = dict(w)
+    del missing["vision_tower.encoder.layers.1.mlp.up_proj.linear.weight"]
+    with pytest.raises(S.SvlError) as e:
+        V.VisionModel(vc, missing, 48)
+    assert e.value.kind == "Corrupt"
+    extra = dict(w)
+    extra["vision_tower.encoder.layers.2.input_layernorm.weight"] = np.ones(64, np.float32)
+    with pytest.raises(S.SvlError) as e:
+        V.VisionModel(vc, extra, 48)
+    assert e.value.kind == "Corrupt"
+    bad = dict(w)
+    bad["embed_vision.embedding_projection.weight"] = np.zeros((47, 64), np.float32)
+    with pytest.raises(S.SvlError) as e:
+        V.VisionModel(vc, bad, 48)
+    assert e.value.kind == "Corrupt"
