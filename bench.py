@@ -44,6 +44,8 @@ def parse():
                     help="rows of the workload timed on the CPU oracle (default: one per core, "
                          "at most 16; 0 skips the CPU baseline)")
     ap.add_argument("--t1-runs", type=int, default=20)
+    ap.add_argument("--image-steps", type=int, default=5,
+                    help="timed batches of the image workload (0 skips it)")
     ap.add_argument("--row-groups", type=int, default=3,
                     help="row groups (streams) the batch is split into")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -95,6 +97,69 @@ def cpu_baseline(cfg, weights, rows_all, n_rows):
             "sample": f"first {n} rows of the same batch ({toks} tokens, lengths "
                       f"{min(len(r) for r in rows)}-{max(len(r) for r in rows)}), one row per "
                       f"thread, scalar C oracle (-O2, no FMA contraction), {wall:.1f} s wall"}
+
+
+def image_leg(text_model, dev, steps):
+    """Image workload: batch 4 synthetic 768x768 RGB noise images (seed 2),
+    48x48 = 2304 patches each, through the 16-layer vision tower (config V,
+    random-init weights seed 0) and the text encoder (prompt of 260 tokens
+    with the 256 soft tokens substituted). Patches resident in HBM."""
+    import numpy as np
+    import torch
+
+    import svl_synth
+    import svl_vision
+
+    n_img, grid = 4, 48
+    c = svl_synth.config_v(16)
+    vw = svl_synth.vision_weights(c, 768, seed=0)
+    vm = svl_vision.VisionModel(svl_vision.VisionConfig.from_json_value(c), vw, 768, dev)
+    del vw
+    patches = svl_synth.image_patches(n_img, grid, grid, seed=2)
+    src = torch.from_numpy(np.concatenate([p.pixel_values[: p.valid_patches]
+                                           for p in patches])).to("cuda:0")
+    pix = torch.empty_like(src)
+    soft = torch.empty((sum(p.soft_tokens for p in patches), 768), device="cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+    emb = svl_vision.ImageEmbedder(text_model, vm, svl_vision.ImageSpecialTokens())
+
+    def tower():
+        pix.copy_(src)  # the tower rescales its input in place
+        vm.forward_device(pix.data_ptr(), patches, soft.data_ptr(), stream)
+
+    def embed():
+        pix.copy_(src)
+        return emb.embed_device(pix.data_ptr(), patches, 768)
+
+    def timed(f):
+        f()
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(steps):
+            a = time.perf_counter()
+            f()
+            torch.cuda.synchronize()
+            ms.append((time.perf_counter() - a) * 1e3)
+        return float(np.median(ms))
+
+    tower_ms = timed(tower)
+    embed_ms = timed(embed)
+    out = embed()
+    assert np.isfinite(out).all()
+    P, H, I, L, hd, nh = grid * grid, 768, 3072, 16, 64, 12
+    per_img = (2 * P * 768 * H + L * (2 * P * H * (3 * nh * hd + H + 3 * I) + 4 * hd * nh * P * P)
+               + 2 * (P // 9) * H * 768)
+    flops = n_img * per_img
+    return {"workload": "batch 4 synthetic 768x768 RGB noise images (seed 2), 2304 patches "
+                        "each: 16-layer vision tower (hidden 768, 12 heads of 64, FFN 3072) "
+                        "+ text encoder over the 260-token image prompt; patches in HBM",
+            "images_per_s": round(n_img / (embed_ms * 1e-3), 2),
+            "p50_ms_per_batch": round(embed_ms, 3),
+            "tower_p50_ms_per_batch": round(tower_ms, 3),
+            "tower_tflops": round(flops / (tower_ms * 1e-3) / 1e12, 2),
+            "tower_frac_of_fp32_mfma_peak": round(flops / (tower_ms * 1e-3) / 1e12
+                                                  / PEAK_FP32_MFMA_TFLOPS, 4),
+            "tower_flops_per_batch": flops, "steps": steps}
 
 
 def main():
@@ -204,6 +269,7 @@ def main():
                 "flops_per_launch": gu_flops, "avg_launch_ms": round(gu_ms, 4),
                 "launches": gu["launches"]}
 
+    image = image_leg(model, dev, args.image_steps) if args.image_steps > 0 else None
     cpu = cpu_baseline(cfg, weights, rows, args.cpu_sample_rows)
 
     breakdown = {k: {"ms_per_step": round(v["ms"] / args.steps, 3),
@@ -233,6 +299,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": breakdown,
+        "image": image,
     }
     if cpu:
         line["speedup_vs_cpu_baseline"] = round(value / cpu["value"], 1)

@@ -282,6 +282,14 @@ svl_status svl_image_embed_batch(svl_vision_model *vision, svl_text_model *text,
                                  const svl_image_patches *images, int32_t batch,
                                  int64_t dimension, float *out);
 
+/* The same with the images' patches already in HBM: d_pixels as in
+ * svl_vision_forward_device (rescaled in place; images[i].pixel_values is
+ * ignored). out [batch, dimension] on the host. */
+svl_status svl_image_embed_device(svl_vision_model *vision, svl_text_model *text,
+                                  const svl_image_special_tokens *tokens, float *d_pixels,
+                                  const svl_image_patches *images, int32_t batch,
+                                  int64_t dimension, float *out);
+
 /* ---- deterministic synthetic data (benchmark and tests) ------------------ */
 /* Counter-based SplitMix64: element i of stream s under seed k is
  * u = (splitmix64(k ^ (s * 0x9E3779B97F4A7C15) + i) >> 40) / 2^24 in [0, 1),

@@ -438,26 +438,83 @@ svl_status vis_finish(svl_vision_model *v, hipStream_t s) {
     return SVL_OK;
 }
 
-// Runs the tower for a batch with host pixels; the soft tokens stay in
-// v->soft (and are copied to out_soft when given). Caller holds v->mu.
-svl_status run_vision_host(svl_vision_model *v, const svl_image_patches *images, int32_t batch,
-                           VisBatch &b, float *out_soft, float *out_hidden) {
+// Runs the tower for a batch; the soft tokens stay in v->soft (and are
+// copied to out_soft when given). Pixels come from the host images, or from
+// d_pixels ([sum valid, 768] in HBM, rescaled in place) when it is given.
+// Caller holds v->mu.
+svl_status run_vision(svl_vision_model *v, const svl_image_patches *images, int32_t batch,
+                      float *d_pixels, hipStream_t s, VisBatch &b, float *out_soft,
+                      float *out_hidden) {
     HIP_TRY(hipSetDevice(v->device));
-    ST_TRY(prepare_images(v, images, batch, true, b));
+    ST_TRY(prepare_images(v, images, batch, d_pixels == nullptr, b));
     if (batch == 0) return SVL_OK;
     ST_TRY(ensure_axial_tables(v, b.max_coord + 1));
     ST_TRY(ensure_vis_workspace(v, b));
-    hipStream_t s = v->stream;
-    for (int i = 0; i < batch; ++i)
-        HIP_TRY(hipMemcpyAsync(v->pix.p + b.offsets[i] * PATCH_VALUES, images[i].pixel_values,
-                               (size_t)(images[i].valid_patches * PATCH_VALUES) * 4,
-                               hipMemcpyHostToDevice, s));
+    if (!d_pixels) {
+        for (int i = 0; i < batch; ++i)
+            HIP_TRY(hipMemcpyAsync(v->pix.p + b.offsets[i] * PATCH_VALUES, images[i].pixel_values,
+                                   (size_t)(images[i].valid_patches * PATCH_VALUES) * 4,
+                                   hipMemcpyHostToDevice, s));
+        d_pixels = v->pix.p;
+    }
     ST_TRY(upload_vis_meta(v, b, s));
-    ST_TRY(enqueue_vision(v, b, v->pix.p, s, out_hidden));
+    ST_TRY(enqueue_vision(v, b, d_pixels, s, out_hidden));
     if (out_soft)
         HIP_TRY(hipMemcpyAsync(out_soft, v->soft.p, (size_t)(b.S * v->text_hidden) * 4,
                                hipMemcpyDeviceToHost, s));
     return vis_finish(v, s);
+}
+
+// ImageEmbedder::embed_impl (image.rs:209-253) for a batch; see
+// svl_image_embed_batch.
+svl_status image_embed(svl_vision_model *v, svl_text_model *text,
+                       const svl_image_special_tokens *tokens, const svl_image_patches *images,
+                       int32_t batch, float *d_pixels, int64_t dimension, float *out) {
+    if (!v || !text || !tokens || !out)
+        return fail(SVL_USAGE, "models, special tokens and output are required");
+    // image.rs:215-221
+    const int64_t E = text_embedding_dim(text);
+    if (dimension <= 0 || dimension > E)
+        return fail(SVL_INTERNAL, "embedding dimension %lld is outside 1..=%lld",
+                    (long long)dimension, (long long)E);
+    if (text_device(text) != v->device)
+        return fail(SVL_USAGE, "the vision and text models live on different devices");
+    if (text_hidden_size(text) != v->text_hidden)
+        return fail(SVL_USAGE, "the vision projection width %lld is not the text hidden size %lld",
+                    (long long)v->text_hidden, (long long)text_hidden_size(text));
+    std::lock_guard<std::mutex> lock(v->mu);
+    VisBatch b;
+    ST_TRY(run_vision(v, images, batch, d_pixels, v->stream, b, nullptr, nullptr));
+    if (batch == 0) return SVL_OK;
+    // image.rs:224-244: <bos> <boi> <image> x soft <eoi> <eos>, features at 2.
+    std::vector<int64_t> offsets(1, 0);
+    for (int i = 0; i < batch; ++i) {
+        const int64_t seq = images[i].soft_tokens + 4;
+        if (seq > MAX_TEXT_TOKENS)
+            return fail(SVL_LIMIT, "image %d: image prompt has %lld tokens, above the %lld-token context",
+                        i, (long long)seq, (long long)MAX_TEXT_TOKENS);
+        offsets.push_back(offsets.back() + seq);
+    }
+    std::vector<uint32_t> ids((size_t)offsets.back());
+    std::vector<int32_t> featmap((size_t)offsets.back(), -1);
+    for (int i = 0; i < batch; ++i) {
+        const int64_t o = offsets[i], soft = images[i].soft_tokens;
+        ids[(size_t)o] = tokens->bos;
+        ids[(size_t)o + 1] = tokens->boi;
+        for (int64_t k = 0; k < soft; ++k) {
+            ids[(size_t)(o + 2 + k)] = tokens->image;
+            featmap[(size_t)(o + 2 + k)] = (int32_t)(b.soft_offsets[i] + k);
+        }
+        ids[(size_t)(o + 2 + soft)] = tokens->eoi;
+        ids[(size_t)(o + 3 + soft)] = tokens->eos;
+    }
+    std::vector<float> normalized((size_t)(batch * E));
+    ST_TRY(text_forward_with_device_features(text, ids.data(), offsets.data(), batch,
+                                             featmap.data(), v->soft.p, normalized.data()));
+    for (int i = 0; i < batch; ++i)
+        ST_TRY(svl_truncate_and_normalize(normalized.data() + (size_t)i * E, (size_t)E,
+                                          (size_t)dimension, out + (size_t)i * dimension));
+    return SVL_OK;
 }
 
 }  // namespace
@@ -555,7 +612,7 @@ svl_status svl_vision_forward_batch(svl_vision_model *v, const svl_image_patches
     if (!v || !out_soft) return fail(SVL_USAGE, "model and out_soft are required");
     std::lock_guard<std::mutex> lock(v->mu);
     VisBatch b;
-    return run_vision_host(v, images, batch, b, out_soft, out_hidden);
+    return run_vision(v, images, batch, nullptr, v->stream, b, out_soft, out_hidden);
 }
 
 svl_status svl_vision_forward_device(svl_vision_model *v, float *d_pixels,
@@ -563,69 +620,29 @@ svl_status svl_vision_forward_device(svl_vision_model *v, float *d_pixels,
                                      void *stream) {
     if (!v || !d_pixels || !d_out) return fail(SVL_USAGE, "model, pixels and output are required");
     std::lock_guard<std::mutex> lock(v->mu);
-    HIP_TRY(hipSetDevice(v->device));
-    VisBatch b;
-    ST_TRY(prepare_images(v, images, batch, false, b));
-    if (batch == 0) return SVL_OK;
-    ST_TRY(ensure_axial_tables(v, b.max_coord + 1));
-    ST_TRY(ensure_vis_workspace(v, b));
     hipStream_t s = stream ? (hipStream_t)stream : v->stream;
-    ST_TRY(upload_vis_meta(v, b, s));
-    ST_TRY(enqueue_vision(v, b, d_pixels, s, nullptr));
+    VisBatch b;
+    ST_TRY(run_vision(v, images, batch, d_pixels, s, b, nullptr, nullptr));
+    if (batch == 0) return SVL_OK;
     HIP_TRY(hipMemcpyAsync(d_out, v->soft.p, (size_t)(b.S * v->text_hidden) * 4,
                            hipMemcpyDeviceToDevice, s));
-    return vis_finish(v, s);
+    HIP_TRY(hipStreamSynchronize(s));
+    return SVL_OK;
 }
 
 svl_status svl_image_embed_batch(svl_vision_model *v, svl_text_model *text,
                                  const svl_image_special_tokens *tokens,
                                  const svl_image_patches *images, int32_t batch, int64_t dimension,
                                  float *out) {
-    if (!v || !text || !tokens || !out)
-        return fail(SVL_USAGE, "models, special tokens and output are required");
-    // image.rs:215-221
-    const int64_t E = text_embedding_dim(text);
-    if (dimension <= 0 || dimension > E)
-        return fail(SVL_INTERNAL, "embedding dimension %lld is outside 1..=%lld",
-                    (long long)dimension, (long long)E);
-    if (text_device(text) != v->device)
-        return fail(SVL_USAGE, "the vision and text models live on different devices");
-    if (text_hidden_size(text) != v->text_hidden)
-        return fail(SVL_USAGE, "the vision projection width %lld is not the text hidden size %lld",
-                    (long long)v->text_hidden, (long long)text_hidden_size(text));
-    std::lock_guard<std::mutex> lock(v->mu);
-    VisBatch b;
-    ST_TRY(run_vision_host(v, images, batch, b, nullptr, nullptr));
-    if (batch == 0) return SVL_OK;
-    // image.rs:224-244: <bos> <boi> <image> x soft <eoi> <eos>, features at 2.
-    std::vector<int64_t> offsets(1, 0);
-    for (int i = 0; i < batch; ++i) {
-        const int64_t seq = images[i].soft_tokens + 4;
-        if (seq > MAX_TEXT_TOKENS)
-            return fail(SVL_LIMIT, "image %d: image prompt has %lld tokens, above the %lld-token context",
-                        i, (long long)seq, (long long)MAX_TEXT_TOKENS);
-        offsets.push_back(offsets.back() + seq);
-    }
-    std::vector<uint32_t> ids((size_t)offsets.back());
-    std::vector<int32_t> featmap((size_t)offsets.back(), -1);
-    for (int i = 0; i < batch; ++i) {
-        const int64_t o = offsets[i], soft = images[i].soft_tokens;
-        ids[(size_t)o] = tokens->bos;
-        ids[(size_t)o + 1] = tokens->boi;
-        for (int64_t k = 0; k < soft; ++k) {
-            ids[(size_t)(o + 2 + k)] = tokens->image;
-            featmap[(size_t)(o + 2 + k)] = (int32_t)(b.soft_offsets[i] + k);
-        }
-        ids[(size_t)(o + 2 + soft)] = tokens->eoi;
-        ids[(size_t)(o + 3 + soft)] = tokens->eos;
-    }
-    std::vector<float> normalized((size_t)(batch * E));
-    ST_TRY(text_forward_with_device_features(text, ids.data(), offsets.data(), batch,
-                                             featmap.data(), v->soft.p, normalized.data()));
-    for (int i = 0; i < batch; ++i)
-        ST_TRY(svl_truncate_and_normalize(normalized.data() + (size_t)i * E, (size_t)E,
-                                          (size_t)dimension, out + (size_t)i * dimension));
-    return SVL_OK;
+    return image_embed(v, text, tokens, images, batch, nullptr, dimension, out);
+}
+
+svl_status svl_image_embed_device(svl_vision_model *v, svl_text_model *text,
+                                  const svl_image_special_tokens *tokens, float *d_pixels,
+                                  const svl_image_patches *images, int32_t batch, int64_t dimension,
+                                  float *out) {
+    if (!d_pixels) return fail(SVL_USAGE, "pixels are required");
+    return image_embed(v, text, tokens, images, batch, d_pixels, dimension, out);
 }
 
 }  // extern "C"

@@ -100,7 +100,7 @@ EXPORTED = [
     "svl_bidirectional_attention", "svl_gelu_tanh", "svl_geglu", "svl_add", "svl_mean_pool",
     "svl_l2_normalize", "svl_synth_uniform", "svl_synth_ids", "svl_synth_lengths",
     "svl_vision_model_create", "svl_vision_model_destroy", "svl_vision_forward_batch",
-    "svl_vision_forward_device", "svl_image_embed_batch",
+    "svl_vision_forward_device", "svl_image_embed_batch", "svl_image_embed_device",
 ]
 
 _lib = None
@@ -175,6 +175,7 @@ def lib():
         L.svl_vision_forward_batch.argtypes = [vp, vp, i32, vp, vp]
         L.svl_vision_forward_device.argtypes = [vp, vp, vp, i32, vp, vp]
         L.svl_image_embed_batch.argtypes = [vp, vp, vp, vp, i32, i64, vp]
+        L.svl_image_embed_device.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp]
         _lib = L
         return L
 

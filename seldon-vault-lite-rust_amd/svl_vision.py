@@ -399,3 +399,15 @@ class ImageEmbedder:
                                            ctypes.byref(tok), arr, len(patches_list),
                                            int(dimension), ctypes.c_void_p(out.ctypes.data)))
         return out[: len(patches_list)]
+
+    def embed_device(self, pixels_dev_ptr: int, patches_list, dimension: int):
+        """embed_batch with the patches already in HBM ([sum valid, 768],
+        rescaled in place); returns [batch, dimension] on the host."""
+        arr, keep = _images(patches_list, with_pixels=False)
+        out = np.empty((max(len(patches_list), 1), int(dimension)), np.float32)
+        tok = self.tokens._c()
+        _check(lib().svl_image_embed_device(self.vision.handle, self.model.handle,
+                                            ctypes.byref(tok), ctypes.c_void_p(pixels_dev_ptr),
+                                            arr, len(patches_list), int(dimension),
+                                            ctypes.c_void_p(out.ctypes.data)))
+        return out[: len(patches_list)]

@@ -242,7 +242,13 @@ def test_image_embedder_matches_oracle(embedder):
             print(f"image {i} dim {dim}: max-abs {d:.3g} cosine {c:.9f}", flush=True)
             assert d <= MAX_ABS and c >= MIN_COS
     one = emb.embed_patches(patches[1], 768)
-    assert np.array_equal(one, emb.embed_batch(patches, 768)[1])
+    batch = emb.embed_batch(patches, 768)
+    assert np.array_equal(one, batch[1])
+    import torch
+    pix = np.concatenate([p.pixel_values[: p.valid_patches] for p in patches])
+    d_pix = torch.from_numpy(pix).to("cuda:0")
+    torch.cuda.synchronize()
+    assert np.array_equal(emb.embed_device(d_pix.data_ptr(), patches, 768), batch)
 
 
 def test_image_embedder_rejects_bad_dimensions(embedder):
