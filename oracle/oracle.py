@@ -443,3 +443,170 @@ class OracleVisionModel:
         if capture_hidden:
             out["hidden_states"] = hidden.reshape(L + 1, valid, H)
         return out
+
+
+# ---- audio tower (src/model/audio.rs) ---------------------------------------------
+
+AUDIO_GLOBAL_TENSORS = 5
+AUDIO_LAYER_TENSORS = 62
+_BOUNDS = ["input_min", "input_max", "output_min", "output_max"]
+
+
+def audio_tensor_names(num_layers: int) -> list[str]:
+    """Names in AudioConfig::tensor_shapes order (audio.rs:394-498)."""
+    p = "audio_tower.subsample_conv_projection."
+    names = [p + "layer0.conv.weight", p + "layer0.norm.weight", p + "layer1.conv.weight",
+             p + "layer1.norm.weight", p + "input_proj_linear.weight"]
+    for i in range(num_layers):
+        q = f"audio_tower.layers.{i}."
+        for ff in ("feed_forward1", "feed_forward2"):
+            b = q + ff + "."
+            names += [b + "pre_layer_norm.weight", b + "post_layer_norm.weight",
+                      b + "ffw_layer_1.linear.weight", b + "ffw_layer_2.linear.weight"]
+            for lin in ("ffw_layer_1", "ffw_layer_2"):
+                names += [f"{b}{lin}.{x}" for x in _BOUNDS]
+        for proj in ("q_proj", "k_proj", "v_proj", "post"):
+            names.append(f"{q}self_attn.{proj}.linear.weight")
+            names += [f"{q}self_attn.{proj}.{x}" for x in _BOUNDS]
+        names += [q + "self_attn.relative_k_proj.weight", q + "self_attn.per_dim_scale",
+                  q + "lconv1d.pre_layer_norm.weight", q + "lconv1d.linear_start.linear.weight",
+                  q + "lconv1d.linear_end.linear.weight"]
+        for lin in ("linear_start", "linear_end"):
+            names += [f"{q}lconv1d.{lin}.{x}" for x in _BOUNDS]
+        names += [q + "lconv1d.depthwise_conv1d.weight", q + "lconv1d.conv_norm.weight",
+                  q + "norm_pre_attn.weight", q + "norm_post_attn.weight", q + "norm_out.weight"]
+    names += ["audio_tower.output_proj.weight", "audio_tower.output_proj.bias",
+              "embed_audio.embedding_projection.weight"]
+    return names
+
+
+class _AudCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in (
+        "hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads", "head_dim",
+        "conv_kernel_size", "conv_channels0", "conv_channels1", "attention_chunk_size",
+        "attention_context_left", "attention_context_right", "output_proj_dims")] + [
+        (n, ctypes.c_float) for n in ("attention_logit_cap", "rms_norm_eps", "residual_weight",
+                                      "gradient_clipping")]
+
+
+def _audio_lib():
+    L = lib()
+    if not getattr(L, "_audio_ready", False):
+        f = ctypes.POINTER(ctypes.c_float)
+        sz = ctypes.c_size_t
+        L.svlo_silu_value.restype = ctypes.c_float
+        L.svlo_silu_value.argtypes = [ctypes.c_float]
+        L.svlo_sigmoid_value.restype = ctypes.c_float
+        L.svlo_sigmoid_value.argtypes = [ctypes.c_float]
+        L.svlo_softplus_value.restype = ctypes.c_float
+        L.svlo_softplus_value.argtypes = [ctypes.c_float]
+        L.svlo_clamp_value.restype = ctypes.c_float
+        L.svlo_clamp_value.argtypes = [ctypes.c_float] * 3
+        L.svlo_clipped_linear.argtypes = [f, f, f, sz, sz, sz, f]
+        L.svlo_audio_position_embeddings.argtypes = [sz, sz, f]
+        L.svlo_audio_attention_core.argtypes = [f, f, f, f, ctypes.POINTER(ctypes.c_ubyte), sz, sz,
+                                                sz, sz, sz, sz, ctypes.c_float, f]
+        L.svlo_audio_subsampled_frames.restype = sz
+        L.svlo_audio_subsampled_frames.argtypes = [sz]
+        L.svlo_audio_forward.argtypes = [ctypes.POINTER(_AudCfg), ctypes.POINTER(f), sz, f,
+                                         ctypes.POINTER(ctypes.c_ubyte), sz,
+                                         ctypes.POINTER(sz), f, f, f, ctypes.c_char_p, sz]
+        L._audio_ready = True
+    return L
+
+
+def silu_value(x):
+    return _audio_lib().svlo_silu_value(float(x))
+
+
+def sigmoid_value(x):
+    return _audio_lib().svlo_sigmoid_value(float(x))
+
+
+def softplus_value(x):
+    return _audio_lib().svlo_softplus_value(float(x))
+
+
+def clipped_linear(x, w, bounds, rows, in_f, out_f):
+    x, w, b = _f32(x), _f32(w), _f32(bounds)
+    out = np.empty(rows * out_f, np.float32)
+    _check(_audio_lib().svlo_clipped_linear(_fp(x), _fp(w), _fp(b), rows, in_f, out_f, _fp(out)),
+           "clipped_linear")
+    return out
+
+
+def audio_position_embeddings(hidden, positions):
+    out = np.empty(positions * hidden, np.float32)
+    _check(_audio_lib().svlo_audio_position_embeddings(hidden, positions, _fp(out)), "positions")
+    return out.reshape(positions, hidden)
+
+
+def audio_attention_core(q, k, v, relk, mask, heads, chunk, left, right, cap):
+    """q, k, v [rows, heads * hd] (already projected and scaled), relk
+    [positions, heads * hd], mask [rows]."""
+    q, k, v, relk = _f32(q), _f32(k), _f32(v), _f32(relk)
+    m = np.ascontiguousarray(np.asarray(mask, np.uint8).reshape(-1))
+    rows, width = q.shape
+    out = np.empty((rows, width), np.float32)
+    _check(_audio_lib().svlo_audio_attention_core(
+        _fp(q), _fp(k), _fp(v), _fp(relk), m.ctypes.data_as(ctypes.POINTER(ctypes.c_ubyte)), rows,
+        heads, width // heads, chunk, left, right, cap, _fp(out)), "audio attention")
+    return out
+
+
+def resolve_audio_config(config: dict) -> dict:
+    """The fields of AudioConfig (audio.rs:94-294) that the forward pass uses."""
+    a = config["audio_config"]
+    H, NH = int(a["hidden_size"]), int(a["num_attention_heads"])
+    c0, c1 = (int(x) for x in a["subsampling_conv_channels"])
+    f32 = lambda k: float(np.float32(float(a[k])))
+    return dict(hidden_size=H, intermediate_size=4 * H, num_hidden_layers=int(a["num_hidden_layers"]),
+                num_attention_heads=NH, head_dim=H // NH, conv_kernel_size=int(a["conv_kernel_size"]),
+                conv_channels0=c0, conv_channels1=c1,
+                attention_chunk_size=int(a["attention_chunk_size"]),
+                attention_context_left=int(a["attention_context_left"]),
+                attention_context_right=int(a["attention_context_right"]),
+                output_proj_dims=int(a["output_proj_dims"]),
+                attention_logit_cap=f32("attention_logit_cap"), rms_norm_eps=f32("rms_norm_eps"),
+                residual_weight=f32("residual_weight"), gradient_clipping=f32("gradient_clipping"))
+
+
+class OracleAudioModel:
+    """The reference AudioModel restated on the CPU (audio.rs:932-1134)."""
+
+    def __init__(self, config: dict, weights: dict, text_hidden: int):
+        self.cfg = c = resolve_audio_config(config)
+        self.text_hidden = int(text_hidden)
+        self._c = _AudCfg(*[c[n] for n, _ in _AudCfg._fields_])
+        names = audio_tensor_names(c["num_hidden_layers"])
+        self._arrays = [_f32(weights[n]).reshape(-1) for n in names]
+        self._ptrs = (ctypes.POINTER(ctypes.c_float) * len(names))(*[_fp(a) for a in self._arrays])
+
+    def forward(self, features, mask, capture_hidden=False):
+        """features [frames, 128] log-mel, mask [frames] bool. Returns
+        dict(pooled [tokens, text_hidden], audio_tokens, sscp_output, hidden_states)."""
+        c = self.cfg
+        feats = _f32(features).reshape(-1)
+        m = np.ascontiguousarray(np.asarray(mask, np.uint8).reshape(-1))
+        frames = m.size
+        rows = _audio_lib().svlo_audio_subsampled_frames(frames)
+        H, L = c["hidden_size"], c["num_hidden_layers"]
+        pooled = np.empty(max(rows, 1) * self.text_hidden, np.float32)
+        sscp = np.empty(max(rows, 1) * H, np.float32) if capture_hidden else None
+        hidden = np.empty(max(L, 1) * max(rows, 1) * H, np.float32) if capture_hidden else None
+        tokens = ctypes.c_size_t(0)
+        msg = ctypes.create_string_buffer(256)
+        st = _audio_lib().svlo_audio_forward(
+            ctypes.byref(self._c), self._ptrs, self.text_hidden, _fp(feats),
+            m.ctypes.data_as(ctypes.POINTER(ctypes.c_ubyte)), frames, ctypes.byref(tokens),
+            _fp(pooled), None if sscp is None else _fp(sscp), None if hidden is None else _fp(hidden),
+            msg, 256)
+        if st != 0:
+            raise OracleError(st, msg.value.decode())
+        n = tokens.value
+        out = dict(pooled=pooled[: n * self.text_hidden].reshape(n, self.text_hidden),
+                   audio_tokens=n)
+        if capture_hidden:
+            out["sscp_output"] = sscp[: n * H].reshape(n, H)
+            out["hidden_states"] = hidden[: L * n * H].reshape(L, n, H)
+        return out

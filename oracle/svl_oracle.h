@@ -152,6 +152,71 @@ int svlo_vision_forward(const svlo_vision_config *cfg, const float *const *weigh
                         size_t soft_tokens, float *out_pooled, float *out_hidden, char *msg,
                         size_t msg_len);
 
+/* ---- audio tower (src/model/audio.rs) ----------------------------------- */
+
+/* Validated audio configuration (audio.rs:62-80). */
+typedef struct {
+    int64_t hidden_size;
+    int64_t intermediate_size; /* 4 * hidden_size */
+    int64_t num_hidden_layers;
+    int64_t num_attention_heads;
+    int64_t head_dim; /* hidden_size / num_attention_heads */
+    int64_t conv_kernel_size;
+    int64_t conv_channels0;
+    int64_t conv_channels1;
+    int64_t attention_chunk_size;
+    int64_t attention_context_left;
+    int64_t attention_context_right;
+    int64_t output_proj_dims;
+    float attention_logit_cap;
+    float rms_norm_eps;
+    float residual_weight;
+    float gradient_clipping;
+} svlo_audio_config;
+
+/*
+ * Weights in the order of AudioConfig::tensor_shapes (audio.rs:394-498):
+ * 5 subsampling tensors (layer0 conv [C0,1,3,3], layer0 norm [C0], layer1 conv
+ * [C1,C0,3,3], layer1 norm [C1], input_proj_linear [H, C0/4*C1]), 62 per layer
+ * (feed_forward1 and feed_forward2: pre/post norms, two linears, 4 bounds each;
+ * q/k/v/post: weight + 4 bounds each; relative_k_proj; per_dim_scale; light
+ * conv: pre norm, start/end linears, their bounds, depthwise weight, conv
+ * norm; norm_pre_attn, norm_post_attn, norm_out), then output_proj weight and
+ * bias and embed_audio.embedding_projection. Scalars are 1-element arrays.
+ */
+#define SVLO_AUDIO_GLOBAL_TENSORS 5
+#define SVLO_AUDIO_LAYER_TENSORS 62
+
+float svlo_clamp_value(float value, float minimum, float maximum); /* audio.rs:1339 */
+float svlo_silu_value(float value);                                /* audio.rs:1349 */
+float svlo_sigmoid_value(float value);                             /* audio.rs:1357 */
+float svlo_softplus_value(float value);                            /* audio.rs:1366 */
+/* audio.rs:558-601; bounds = {input_min, input_max, output_min, output_max}. */
+int svlo_clipped_linear(const float *input, const float *weight, const float *bounds, size_t rows,
+                        size_t in_features, size_t out_features, float *out);
+/* audio.rs:1257-1288; out [positions, hidden]. */
+int svlo_audio_position_embeddings(size_t hidden, size_t positions, float *out);
+/* audio.rs:1579-1661 chunked local attention on projected, scaled q and k:
+ * [rows, heads * head_dim] each, relk [positions, heads * head_dim], mask
+ * [rows] (0/1). att [rows, heads * head_dim]. */
+int svlo_audio_attention_core(const float *q, const float *k, const float *v, const float *relk,
+                              const unsigned char *mask, size_t rows, size_t heads,
+                              size_t head_dim, size_t chunk, size_t context_left,
+                              size_t context_right, float cap, float *att);
+/* Rows after the two stride-2 subsampling convolutions: ceil(ceil(frames/2)/2). */
+size_t svlo_audio_subsampled_frames(size_t frames);
+/*
+ * AudioModel::forward (audio.rs:981-1134) on log-mel features [frames, 128]
+ * with the frame mask (0/1 bytes). out_pooled [subsampled frames, text_hidden]
+ * receives the valid tokens first (*out_tokens of them, AudioOutput::pooled);
+ * out_sscp (optional, [tokens, hidden]) the subsampling output and out_hidden
+ * (optional, [layers, tokens, hidden]) each layer's output, valid rows only.
+ */
+int svlo_audio_forward(const svlo_audio_config *cfg, const float *const *weights,
+                       size_t text_hidden, const float *features, const unsigned char *mask,
+                       size_t frames, size_t *out_tokens, float *out_pooled, float *out_sscp,
+                       float *out_hidden, char *msg, size_t msg_len);
+
 #ifdef __cplusplus
 }
 #endif
