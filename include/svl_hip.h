@@ -290,6 +290,93 @@ svl_status svl_image_embed_device(svl_vision_model *vision, svl_text_model *text
                                   const svl_image_patches *images, int32_t batch,
                                   int64_t dimension, float *out);
 
+/* ---- audio tower and audio prompts ---------------------------------------- */
+
+typedef struct svl_audio_model svl_audio_model;
+
+/* Validated audio configuration (src/model/audio.rs:62-80 AudioConfig; the
+ * intermediate size is 4 * hidden_size and head_dim hidden / heads, as
+ * audio.rs:185-192 derives them). */
+typedef struct {
+    int64_t hidden_size;
+    int64_t num_hidden_layers;
+    int64_t num_attention_heads;
+    int64_t conv_kernel_size;
+    int64_t conv_channels0; /* subsampling_conv_channels[0] */
+    int64_t conv_channels1; /* subsampling_conv_channels[1] */
+    int64_t attention_chunk_size;
+    int64_t attention_context_left;
+    int64_t attention_context_right;
+    int64_t output_proj_dims;
+    double attention_logit_cap;
+    double rms_norm_eps;
+    double residual_weight;
+    double gradient_clipping;
+} svl_audio_config;
+
+/* One clip's log-mel spectrogram (src/media/audio_preprocess.rs:50-90
+ * MelSpectrogram): features [frames, 128] row-major, mask [frames] (1 for
+ * frames whose window holds real audio). */
+typedef struct {
+    const float *features;
+    const uint8_t *mask;
+    int64_t frames;
+} svl_mel;
+
+/* src/model/audio_embedder.rs:32-46 AudioSpecialTokens. */
+typedef struct {
+    uint32_t bos, eos, pad, boa, audio, eoa;
+} svl_audio_special_tokens;
+
+/* Validates the inventory like AudioWeights::decode (audio.rs:717-794):
+ * unexpected audio_tower. / embed_audio. tensors, missing or mis-shaped ones
+ * and inverted clipping bounds -> CORRUPT; packs the weights into HBM and
+ * computes each layer's relative keys once. Replaces AudioModel::new
+ * (audio.rs:940-964) with its weights. */
+svl_status svl_audio_model_create(svl_ctx *ctx, const svl_audio_config *cfg,
+                                  int64_t text_hidden, const svl_tensor_view *tensors,
+                                  size_t n_tensors, svl_audio_model **out);
+svl_status svl_audio_model_destroy(svl_audio_model *model);
+
+/* Number of valid audio tokens of a clip: subsampled row t is valid when
+ * mask[4 t] is set (the two stride-2 subsamplings of audio.rs:1187-1240). */
+int64_t svl_audio_token_count(const uint8_t *mask, int64_t frames);
+
+/* AudioModel::forward (audio.rs:981-1134) for `batch` clips at once; clip
+ * i's result equals the reference's forward(clip i).
+ *  out_tokens  NULL or [batch] valid tokens per clip (AudioOutput::audio_tokens)
+ *  out_soft    [sum tokens, text_hidden] (AudioOutput::pooled, clips back to back)
+ *  out_sscp    NULL or [sum tokens, hidden] (AudioOutput::sscp_output)
+ *  out_hidden  NULL or [num_hidden_layers, sum tokens, hidden] (hidden_states)
+ * Validation follows the reference: zero frames or no valid subsampled token
+ * -> CORRUPT, activation caps -> LIMIT, a non-finite value -> INTERNAL. */
+svl_status svl_audio_forward_batch(svl_audio_model *model, const svl_mel *mels, int32_t batch,
+                                   int64_t *out_tokens, float *out_soft, float *out_sscp,
+                                   float *out_hidden);
+
+/* Device-resident variant: d_features holds the clips' mel frames back to
+ * back in HBM ([sum frames, 128]); mels[i].features is ignored, the masks
+ * stay on the host. Soft tokens go to d_out [sum tokens, text_hidden] on
+ * `stream` (NULL = the model's stream); the call returns after it drained. */
+svl_status svl_audio_forward_device(svl_audio_model *model, const float *d_features,
+                                    const svl_mel *mels, int32_t batch, float *d_out,
+                                    void *stream);
+
+/* AudioEmbedder::embed_impl (audio_embedder.rs:223-267) for `batch` clips:
+ * the tower, then <bos> <boa> <audio> x tokens <eoa> <eos> through the text
+ * model with the soft tokens replacing positions [2, 2 + tokens), then
+ * ForwardOutput::embedding(dimension). out [batch, dimension]. The soft
+ * tokens stay in HBM between the two models. */
+svl_status svl_audio_embed_batch(svl_audio_model *audio, svl_text_model *text,
+                                 const svl_audio_special_tokens *tokens, const svl_mel *mels,
+                                 int32_t batch, int64_t dimension, float *out);
+/* The same with the mel frames already in HBM (d_features as in
+ * svl_audio_forward_device). */
+svl_status svl_audio_embed_device(svl_audio_model *audio, svl_text_model *text,
+                                  const svl_audio_special_tokens *tokens, const float *d_features,
+                                  const svl_mel *mels, int32_t batch, int64_t dimension,
+                                  float *out);
+
 /* ---- deterministic synthetic data (benchmark and tests) ------------------ */
 /* Counter-based SplitMix64: element i of stream s under seed k is
  * u = (splitmix64(k ^ (s * 0x9E3779B97F4A7C15) + i) >> 40) / 2^24 in [0, 1),

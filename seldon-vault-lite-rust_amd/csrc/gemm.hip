@@ -54,9 +54,33 @@ struct GemmShape {
 
 // Epilogue shared by the GEMM kernels. Accumulator register r of a 32x32
 // tile holds row 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.
+// True for the epilogues whose W rows come in interleaved 32-row pairs.
+template <int EPI>
+constexpr bool paired_epi() {
+    return EPI == EPI_GEGLU || EPI == EPI_CLIP_GLU;
+}
+
+template <int EPI>
+constexpr bool clipped_epi() {
+    return EPI == EPI_CLIP_STORE || EPI == EPI_CLIP_SILU || EPI == EPI_CLIP_GLU;
+}
+
+// Clip segment of an output tile starting at column n0 (tiles never straddle
+// segments: the host keeps clip_cols a multiple of the widest tile).
+__device__ __forceinline__ int clip_segment(const GemmArgs &p, int n0) {
+    return p.clip_cols > 0 ? n0 / p.clip_cols : 0;
+}
+
+// Epilogue shared by the GEMM kernels. Accumulator register r of a 32x32
+// tile holds row 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.
 template <int TM, int TN, int EPI>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x16 (&acc)[TM][TN],
-                                              int mw, int nw, int l32, int hh) {
+                                              int mw, int nw, int l32, int hh, int seg) {
+    float olo = 0.f, ohi = 0.f;
+    if constexpr (clipped_epi<EPI>()) {
+        olo = p.clip[seg][2];
+        ohi = p.clip[seg][3];
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -64,11 +88,16 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x16 (&
             const int m = mw + i * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
             if (m >= p.M) continue;
             float *crow = p.C + (int64_t)m * p.ldc;
-            if constexpr (EPI == EPI_GEGLU) {
+            if constexpr (paired_epi<EPI>()) {
 #pragma unroll
                 for (int j = 0; j < TN; j += 2) {
                     const int oc = nw / 2 + (j / 2) * 32 + l32;
-                    if (oc < p.n_out) crow[oc] = gelu_tanh(acc[i][j][r]) * acc[i][j + 1][r];
+                    if (oc >= p.n_out) continue;
+                    if constexpr (EPI == EPI_GEGLU)
+                        crow[oc] = gelu_tanh(acc[i][j][r]) * acc[i][j + 1][r];
+                    else
+                        crow[oc] = clamp_ref(acc[i][j][r], olo, ohi) *
+                                   sigmoid_ref(clamp_ref(acc[i][j + 1][r], olo, ohi));
                 }
             } else {
 #pragma unroll
@@ -79,6 +108,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x16 (&
                     if constexpr (EPI == EPI_SCALE) v = v * p.alpha;
                     if constexpr (EPI == EPI_GELU_MUL)
                         v = gelu_tanh(v) * p.aux[(int64_t)m * p.ldaux + n];
+                    if constexpr (EPI == EPI_BIAS) v = v + p.aux[n];
+                    if constexpr (EPI == EPI_CLIP_STORE) v = clamp_ref(v, olo, ohi);
+                    if constexpr (EPI == EPI_CLIP_SILU) v = silu_ref(clamp_ref(v, olo, ohi));
                     crow[n] = v;
                 }
             }
@@ -105,6 +137,12 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
     const int wm = wave >> 1, wn = wave & 1;
     const int l32 = lane & 31, hh = lane >> 5;
     const int M = p.M, N = p.N, K = p.K;
+    const int seg = clip_segment(p, n0);
+    float alo = 0.f, ahi = 0.f;
+    if constexpr (clipped_epi<EPI>()) {
+        alo = p.clip[seg][0];
+        ahi = p.clip[seg][1];
+    }
 
     f32x16 acc[S::TM][S::TN];
 #pragma unroll
@@ -159,7 +197,10 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
         for (int kk = 0; kk < S::BK; kk += 8) {
             f32x4 a[S::TM], b[S::TN];
 #pragma unroll
-            for (int i = 0; i < S::TM; ++i) a[i] = *(const f32x4 *)(as + i * 32 * S::LDS + kk);
+            for (int i = 0; i < S::TM; ++i) {
+                a[i] = *(const f32x4 *)(as + i * 32 * S::LDS + kk);
+                if constexpr (clipped_epi<EPI>()) a[i] = clamp4(a[i], alo, ahi);
+            }
 #pragma unroll
             for (int j = 0; j < S::TN; ++j) b[j] = *(const f32x4 *)(ws + j * 32 * S::LDS + kk);
 #pragma unroll
@@ -175,7 +216,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
         __syncthreads();
     }
 
-    gemm_epilogue<S::TM, S::TN, EPI>(p, acc, m0 + wm * S::WM, n0 + wn * S::WN, l32, hh);
+    gemm_epilogue<S::TM, S::TN, EPI>(p, acc, m0 + wm * S::WM, n0 + wn * S::WN, l32, hh, seg);
 }
 
 // s_waitcnt vmcnt(N): at most N vector-memory operations of this wave in flight.
@@ -196,7 +237,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     constexpr int A_CH = BM / RPK / 4;          // DMA instructions per wave per slice
     constexpr int W_CH = BN / RPK / 4;
     static_assert(BM % 64 == 0 && BN % 64 == 0 && A_CH >= 1 && W_CH >= 1, "tile shape");
-    static_assert(EPI != EPI_GEGLU || TN % 2 == 0, "GeGLU pairs 32-column tiles");
+    static_assert(!paired_epi<EPI>() || TN % 2 == 0, "paired epilogues take 32-column tile pairs");
     __shared__ float As[2][BM * BK];
     __shared__ float Ws[2][BN * BK];
 
@@ -211,6 +252,12 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     const int wm = wave >> 1, wn = wave & 1;
     const int l32 = lane & 31, hh = lane >> 5;
     const int M = p.M, N = p.N;
+    const int seg = clip_segment(p, n0);
+    float alo = 0.f, ahi = 0.f;
+    if constexpr (clipped_epi<EPI>()) {
+        alo = p.clip[seg][0];
+        ahi = p.clip[seg][1];
+    }
 
     // Operand windows: [valid rows of this tile] x lda floats; reads past
     // the last valid row return zero.
@@ -269,7 +316,10 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
             const int pos = ((kk >> 2) + hh) ^ sw;
             f32x4 a[TM], b[TN];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) a[i] = *(const f32x4 *)(as + i * 32 * BK + 4 * pos);
+            for (int i = 0; i < TM; ++i) {
+                a[i] = *(const f32x4 *)(as + i * 32 * BK + 4 * pos);
+                if constexpr (clipped_epi<EPI>()) a[i] = clamp4(a[i], alo, ahi);
+            }
 #pragma unroll
             for (int j = 0; j < TN; ++j) b[j] = *(const f32x4 *)(ws + j * 32 * BK + 4 * pos);
 #pragma unroll
@@ -282,7 +332,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
                                                                          acc[i][j], 0, 0, 0);
         }
     }
-    gemm_epilogue<TM, TN, EPI>(p, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2), l32, hh);
+    gemm_epilogue<TM, TN, EPI>(p, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2), l32, hh, seg);
 #endif
 }
 
@@ -291,27 +341,47 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_nt_simple(GemmArgs p) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int ncols = EPI == EPI_GEGLU ? p.n_out : p.N;
+    const int ncols = paired_epi<EPI>() ? p.n_out : p.N;
     if (idx >= (int64_t)p.M * ncols) return;
     const int m = (int)(idx / ncols), n = (int)(idx % ncols);
     const float *a = p.A + (int64_t)m * p.lda;
     float *crow = p.C + (int64_t)m * p.ldc;
-    if constexpr (EPI == EPI_GEGLU) {
-        // Interleaved rows: gate row of column n is 64*(n/32) + n%32, up row +32.
+    float alo = 0.f, ahi = 0.f, olo = 0.f, ohi = 0.f;
+    if constexpr (clipped_epi<EPI>()) {
+        const int seg = p.clip_cols > 0 ? (paired_epi<EPI>() ? 0 : n / p.clip_cols) : 0;
+        alo = p.clip[seg][0];
+        ahi = p.clip[seg][1];
+        olo = p.clip[seg][2];
+        ohi = p.clip[seg][3];
+    }
+    if constexpr (paired_epi<EPI>()) {
+        // Interleaved rows: first row of column n is 64*(n/32) + n%32, second +32.
         const float *wg = p.W + (int64_t)(64 * (n / 32) + n % 32) * p.ldw;
         const float *wu = wg + 32 * p.ldw;
         float g = 0.f, u = 0.f;
         for (int k = 0; k < p.K; ++k) {
-            g += a[k] * wg[k];
-            u += a[k] * wu[k];
+            float x = a[k];
+            if constexpr (clipped_epi<EPI>()) x = clamp_ref(x, alo, ahi);
+            g += x * wg[k];
+            u += x * wu[k];
         }
-        crow[n] = gelu_tanh(g) * u;
+        if constexpr (EPI == EPI_GEGLU)
+            crow[n] = gelu_tanh(g) * u;
+        else
+            crow[n] = clamp_ref(g, olo, ohi) * sigmoid_ref(clamp_ref(u, olo, ohi));
     } else {
         const float *w = p.W + (int64_t)n * p.ldw;
         float s = 0.f;
-        for (int k = 0; k < p.K; ++k) s += a[k] * w[k];
+        for (int k = 0; k < p.K; ++k) {
+            float x = a[k];
+            if constexpr (clipped_epi<EPI>()) x = clamp_ref(x, alo, ahi);
+            s += x * w[k];
+        }
         if constexpr (EPI == EPI_SCALE) s = s * p.alpha;
         if constexpr (EPI == EPI_GELU_MUL) s = gelu_tanh(s) * p.aux[(int64_t)m * p.ldaux + n];
+        if constexpr (EPI == EPI_BIAS) s = s + p.aux[n];
+        if constexpr (EPI == EPI_CLIP_STORE) s = clamp_ref(s, olo, ohi);
+        if constexpr (EPI == EPI_CLIP_SILU) s = silu_ref(clamp_ref(s, olo, ohi));
         crow[n] = s;
     }
 }
@@ -330,7 +400,7 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 template <int EPI>
 static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
     const int64_t tiles128 = (int64_t)((a.M + 127) / 128) * ((a.N + 127) / 128);
-    if constexpr (EPI != EPI_GEGLU) {
+    if constexpr (!paired_epi<EPI>()) {
         if (a.N <= 256 && a.K % 32 == 0) return launch_dma<64, 64, 32, EPI, 4>(a, s);
         if (tiles128 < 4 * 256) return launch_dma<128, 64, 16, EPI, 4>(a, s);
     }
@@ -346,7 +416,7 @@ static hipError_t launch_mfma(const GemmArgs &a, hipStream_t s) {
 
 template <int EPI>
 static hipError_t launch_simple(const GemmArgs &a, hipStream_t s) {
-    const int ncols = EPI == EPI_GEGLU ? a.n_out : a.N;
+    const int ncols = paired_epi<EPI>() ? a.n_out : a.N;
     const int64_t n = (int64_t)a.M * ncols;
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL((gemm_nt_simple<EPI>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
@@ -367,6 +437,10 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
             case EPI_SCALE: return launch_dma_auto<EPI_SCALE>(a, s);
             case EPI_GEGLU: return launch_dma_auto<EPI_GEGLU>(a, s);
             case EPI_GELU_MUL: return launch_dma_auto<EPI_GELU_MUL>(a, s);
+            case EPI_BIAS: return launch_dma_auto<EPI_BIAS>(a, s);
+            case EPI_CLIP_STORE: return launch_dma_auto<EPI_CLIP_STORE>(a, s);
+            case EPI_CLIP_SILU: return launch_dma_auto<EPI_CLIP_SILU>(a, s);
+            case EPI_CLIP_GLU: return launch_dma_auto<EPI_CLIP_GLU>(a, s);
         }
         return hipErrorInvalidValue;
     }
@@ -375,6 +449,10 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
         case EPI_SCALE: return launch_mfma<128, 128, EPI_SCALE>(a, s);
         case EPI_GEGLU: return launch_mfma<128, 128, EPI_GEGLU>(a, s);
         case EPI_GELU_MUL: return launch_mfma<128, 128, EPI_GELU_MUL>(a, s);
+        case EPI_BIAS: return launch_mfma<128, 128, EPI_BIAS>(a, s);
+        case EPI_CLIP_STORE: return launch_mfma<128, 128, EPI_CLIP_STORE>(a, s);
+        case EPI_CLIP_SILU: return launch_mfma<128, 128, EPI_CLIP_SILU>(a, s);
+        case EPI_CLIP_GLU: return launch_mfma<128, 128, EPI_CLIP_GLU>(a, s);
     }
     return hipErrorInvalidValue;
 }
@@ -385,6 +463,10 @@ hipError_t launch_gemm_simple(const GemmArgs &a, hipStream_t s) {
         case EPI_SCALE: return launch_simple<EPI_SCALE>(a, s);
         case EPI_GEGLU: return launch_simple<EPI_GEGLU>(a, s);
         case EPI_GELU_MUL: return launch_simple<EPI_GELU_MUL>(a, s);
+        case EPI_BIAS: return launch_simple<EPI_BIAS>(a, s);
+        case EPI_CLIP_STORE: return launch_simple<EPI_CLIP_STORE>(a, s);
+        case EPI_CLIP_SILU: return launch_simple<EPI_CLIP_SILU>(a, s);
+        case EPI_CLIP_GLU: return launch_simple<EPI_CLIP_GLU>(a, s);
     }
     return hipErrorInvalidValue;
 }

@@ -4,3 +4,4 @@
 #include "rows.hip"
 #include "attention.hip"
 #include "vision.hip"
+#include "audio.hip"

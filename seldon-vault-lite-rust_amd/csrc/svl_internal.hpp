@@ -21,6 +21,13 @@ enum GemmEpi : int {
     EPI_SCALE = 1,     // C[m,n] = acc * alpha
     EPI_GEGLU = 2,     // W rows interleaved in 32-blocks (gate, up); C[m,j] = gelu(g) * u
     EPI_GELU_MUL = 3,  // C[m,n] = gelu(acc) * aux[m * ldaux + n]
+    EPI_BIAS = 4,      // C[m,n] = acc + aux[n]
+    // Clipped linears (audio tower): A elements are clamped to
+    // [clip[s][0], clip[s][1]] before the product and the sum to
+    // [clip[s][2], clip[s][3]], s = n / clip_cols (0 when clip_cols == 0).
+    EPI_CLIP_STORE = 5,  // C[m,n] = clamp(acc)
+    EPI_CLIP_SILU = 6,   // C[m,n] = silu(clamp(acc))
+    EPI_CLIP_GLU = 7,    // W rows interleaved in 32-blocks (x, y); C[m,j] = clamp(x) * sigmoid(clamp(y))
 };
 
 struct GemmArgs {
@@ -35,7 +42,9 @@ struct GemmArgs {
     float alpha;
     const float *aux;
     int64_t ldaux;
-    int n_out;  // EPI_GEGLU: number of real output columns (intermediate size)
+    int n_out;  // EPI_GEGLU / EPI_CLIP_GLU: number of real output columns
+    int clip_cols = 0;         // output columns per clip segment (0: one segment)
+    float clip[4][4] = {};     // per segment: input min, input max, output min, output max
 };
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
@@ -139,5 +148,55 @@ hipError_t launch_qkv_post_axial(float *qkv, int64_t ld, int64_t tokens, int nh,
 hipError_t launch_pool_bins(const float *h, const int32_t *bin_start, const int32_t *bin_patch,
                             int64_t soft_tokens, int width, float divisor, float scale, float eps,
                             float *out, int *flag, hipStream_t s);
+
+// ---- audio tower kernels -----------------------------------------------------
+
+// One output row of a subsampling convolution: its input rows are
+// [base, base + len) of the packed input (the clip's rows), and it is row t
+// of the clip's output.
+struct SscpRow {
+    int32_t base;
+    int32_t t;
+    int32_t len;
+};
+
+// Mel [frames, 128] -> layer 0 [rows, 64, C0] (conv 3x3 stride 2 pad 1,
+// masked frames skipped, LayerNorm + ReLU). C0 <= 512.
+hipError_t launch_sscp_conv0(const float *mel, const uint8_t *mask, const SscpRow *rows,
+                             int64_t n_rows, const float *w, const float *ln, int C0, float eps,
+                             float *out, int *flag, hipStream_t s);
+// Layer 0 -> layer 1 [rows, 32, C1]; wt = layer-1 weight as [C0][3][3][C1].
+size_t sscp_conv1_lds_bytes(int C0, int C1);
+hipError_t launch_sscp_conv1(const float *l0, const uint8_t *mask0, const SscpRow *rows,
+                             int64_t n_rows, const float *wt, const float *ln, int C0, int C1,
+                             float eps, float *out, int *flag, hipStream_t s);
+// t = w1 ? rms(clamp(x, +-c1), w1) : x; h = res ? res + t * rw : t (-> h_out);
+// if w2: n_out = rms(clamp(h, +-c2), w2).
+hipError_t launch_audio_rows(const float *x, float c1, const float *w1, const float *res, float rw,
+                             float *h_out, float c2, const float *w2, float *n_out, int64_t rows,
+                             int width, float eps, int *flag, hipStream_t s);
+
+struct AudioAttnArgs {
+    const float *q, *k, *v;      // head h of row i at q + i * ldq + h * head_dim
+    int64_t ldq, ldk, ldv;
+    const float *relk;           // [positions, heads * head_dim]
+    const float *qf;             // [head_dim] query scale per dimension
+    float k_scale, cap;
+    const uint8_t *mask;         // [rows] valid rows
+    const int32_t *pos, *rowlen; // row index within its clip, clip length
+    float *out;
+    int64_t ldo;
+    int64_t rows;
+    int heads, head_dim, chunk, left, context, positions;
+    int *flag;
+};
+hipError_t launch_audio_attention(const AudioAttnArgs &a, hipStream_t s);
+// Causal depthwise conv (dw [width, K]) within each clip, clamp, RMSNorm(w), SiLU.
+hipError_t launch_lconv(const float *gated, const float *dw, int K, const int32_t *pos, float clip,
+                        const float *w, float *out, int64_t rows, int width, float eps, int *flag,
+                        hipStream_t s);
+// out[j] = unscaled_rms(x[idx[j]]).
+hipError_t launch_compact_rms(const float *x, const int32_t *idx, float *out, int64_t rows,
+                              int width, float eps, int *flag, hipStream_t s);
 
 }  // namespace svl

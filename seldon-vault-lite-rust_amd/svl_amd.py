@@ -101,6 +101,9 @@ EXPORTED = [
     "svl_l2_normalize", "svl_synth_uniform", "svl_synth_ids", "svl_synth_lengths",
     "svl_vision_model_create", "svl_vision_model_destroy", "svl_vision_forward_batch",
     "svl_vision_forward_device", "svl_image_embed_batch", "svl_image_embed_device",
+    "svl_audio_model_create", "svl_audio_model_destroy", "svl_audio_token_count",
+    "svl_audio_forward_batch", "svl_audio_forward_device", "svl_audio_embed_batch",
+    "svl_audio_embed_device",
 ]
 
 _lib = None
@@ -488,8 +491,8 @@ def tensor_views(weights: dict):
             a = np.asarray(t)
             if a.dtype == np.float16:
                 raise _unsupported(f"tensor {name} is F16, which is forbidden")
-            a = np.ascontiguousarray(a, dtype=np.float32)
-            dtype, shape, data = 0, a.shape, a
+            # shape first: ascontiguousarray turns a rank-0 scalar into shape (1,)
+            dtype, shape, data = 0, a.shape, np.ascontiguousarray(a, dtype=np.float32)
         data = np.ascontiguousarray(data)
         bname = name.encode()
         keep += [data, bname]

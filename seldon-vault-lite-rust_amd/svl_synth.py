@@ -162,3 +162,70 @@ def image_patches(batch: int, grid_width: int = 48, grid_height: int = 48, seed:
         pix = u8.astype(np.float32) * svl_vision.RESCALE_FACTOR
         out.append(svl_vision.ImagePatches.from_grid(pix, grid_width, grid_height, max_patches))
     return out
+
+
+# ---- audio tower --------------------------------------------------------------
+#
+# Config AU is the frozen gemma4_audio shape (docs/architecture.md:566-578:
+# hidden 1024, 12 layers, 8 heads, conv kernel 5, SSCP channels [128, 32],
+# chunk 12, left context 13, right 0, logit cap 50, output projection 1536,
+# residual weight 0.5, clipping 1e10, SiLU). Weights, one SplitMix64 stream
+# per tensor in AudioConfig::tensor_shapes order after an offset of 200000:
+#   linear / conv weights   U(-sqrt(3/fan_in), +sqrt(3/fan_in))
+#   RMSNorm / LayerNorm     1 + U(-0.1, 0.1)
+#   per_dim_scale           U(-0.5, 0.5)
+#   output_proj bias        U(-0.1, 0.1)
+#   clipping bounds         input/output min -U(2.5, 4), max +U(2.5, 4)
+# Mel input: log-mel-shaped frames U(-7, 2) per bin (one stream per clip),
+# every frame valid unless a mask is given; 30 s at 16 kHz is 2999 frames.
+
+AUDIO_STREAM_BASE = 200_000
+
+
+def config_au(layers=12, text=None) -> dict:
+    c = {"text_config": text or config_a()}
+    c["audio_config"] = {
+        "model_type": "gemma4_audio", "dtype": "float32", "hidden_size": 1024,
+        "num_hidden_layers": layers, "num_attention_heads": 8, "conv_kernel_size": 5,
+        "subsampling_conv_channels": [128, 32], "attention_chunk_size": 12,
+        "attention_context_left": 13, "attention_context_right": 0,
+        "attention_logit_cap": 50.0, "rms_norm_eps": 1e-06, "output_proj_dims": 1536,
+        "residual_weight": 0.5, "gradient_clipping": 1e10, "hidden_act": "silu",
+        "use_clipped_linears": True, "attention_invalid_logits_value": -1e9}
+    return c
+
+
+def audio_weights(config: dict, text_hidden: int, seed: int = 0) -> dict:
+    import svl_audio
+    ac = svl_audio.AudioConfig.from_json_value(config)
+    out = {}
+    for k, (name, shape) in enumerate(ac.tensor_shapes(text_hidden)):
+        n = int(np.prod(shape)) if shape else 1
+        stream = AUDIO_STREAM_BASE + k
+        if name.endswith(("input_min", "output_min")):
+            v = -svl_amd.synth_uniform(seed, stream, 2.5, 4.0, 1)
+        elif name.endswith(("input_max", "output_max")):
+            v = svl_amd.synth_uniform(seed, stream, 2.5, 4.0, 1)
+        elif name.endswith("per_dim_scale"):
+            v = svl_amd.synth_uniform(seed, stream, -0.5, 0.5, n)
+        elif name.endswith("output_proj.bias"):
+            v = svl_amd.synth_uniform(seed, stream, -0.1, 0.1, n)
+        elif len(shape) == 1:
+            v = svl_amd.synth_uniform(seed, stream, 0.9, 1.1, n)
+        else:
+            fan_in = int(np.prod(shape[1:]))
+            b = math.sqrt(3.0 / fan_in)
+            v = svl_amd.synth_uniform(seed, stream, -b, b, n)
+        out[name] = np.asarray(v, np.float32).reshape(shape)
+    return out
+
+
+def mel_clips(frames, seed: int = 3, masks=None):
+    """Synthetic log-mel spectrograms, one per entry of `frames`."""
+    import svl_audio
+    out = []
+    for i, f in enumerate(frames):
+        feats = svl_amd.synth_uniform(seed, 20 + i, -7.0, 2.0, int(f) * 128).reshape(int(f), 128)
+        mask = np.ones(int(f), bool) if masks is None else np.asarray(masks[i], bool)
+        out.append(svl_audio.MelSpectrogram(feats, mask))
+    return out
