@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--t1-runs", type=int, default=20)
     ap.add_argument("--image-steps", type=int, default=5,
                     help="timed batches of the image workload (0 skips it)")
+    ap.add_argument("--audio-steps", type=int, default=5,
+                    help="timed batches of the audio workload (0 skips it)")
     ap.add_argument("--row-groups", type=int, default=3,
                     help="row groups (streams) the batch is split into")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -162,6 +164,71 @@ def image_leg(text_model, dev, steps):
             "tower_flops_per_batch": flops, "steps": steps}
 
 
+def audio_leg(text_model, dev, steps):
+    """Audio workload: batch 4 clips of 30 s (2999 log-mel frames each, all
+    valid; 750 audio tokens after subsampling) through the 12-layer audio
+    tower (config AU, random-init weights seed 0) and the text encoder
+    (754-token prompts with the audio tokens substituted). The log-mel front
+    end is not part of the GPU path: the frames are synthetic log-mel values
+    U(-7, 2) (seed 3), resident in HBM."""
+    import numpy as np
+    import torch
+
+    import svl_audio
+    import svl_synth
+
+    n_clip, frames = 4, 2999
+    c = svl_synth.config_au(12)
+    aw = svl_synth.audio_weights(c, 768, seed=0)
+    am = svl_audio.AudioModel(svl_audio.AudioConfig.from_json_value(c), aw, 768, dev)
+    del aw
+    mels = svl_synth.mel_clips([frames] * n_clip, seed=3)
+    feats = torch.from_numpy(np.concatenate([m.features for m in mels])).to("cuda:0")
+    tokens = sum(m.audio_tokens() for m in mels)
+    soft = torch.empty((tokens, 768), device="cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+    emb = svl_audio.AudioEmbedder(text_model, am, svl_audio.AudioSpecialTokens())
+
+    def tower():
+        am.forward_device(feats.data_ptr(), mels, soft.data_ptr(), stream)
+
+    def embed():
+        return emb.embed_device(feats.data_ptr(), mels, 768)
+
+    def timed(f):
+        f()
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(steps):
+            a = time.perf_counter()
+            f()
+            torch.cuda.synchronize()
+            ms.append((time.perf_counter() - a) * 1e3)
+        return float(np.median(ms))
+
+    tower_ms = timed(tower)
+    embed_ms = timed(embed)
+    out = embed()
+    assert np.isfinite(out).all()
+    H, L, C0, C1, P, T = 1024, 12, 128, 32, 1536, tokens // n_clip
+    f1 = (frames + 1) // 2
+    per_clip = (2 * f1 * 64 * C0 * 9 + 2 * T * 32 * C1 * C0 * 9 + 2 * T * 32 * C1 * H
+                + L * 2 * T * H * (2 * 2 * 4 * H + 3 * H + H + 2 * H + H)
+                + L * 4 * 8 * 128 * T * 12 + 2 * T * H * P + 2 * T * P * 768)
+    flops = n_clip * per_clip
+    return {"workload": "batch 4 clips of 30 s (2999 log-mel frames, 750 tokens each): 12-layer "
+                        "audio tower (hidden 1024, 8 heads of 128, SSCP [128, 32], chunk 12) + "
+                        "text encoder over the 754-token audio prompt; synthetic log-mel frames "
+                        "in HBM",
+            "clips_per_s": round(n_clip / (embed_ms * 1e-3), 2),
+            "p50_ms_per_batch": round(embed_ms, 3),
+            "tower_p50_ms_per_batch": round(tower_ms, 3),
+            "tower_tflops": round(flops / (tower_ms * 1e-3) / 1e12, 2),
+            "tower_frac_of_fp32_mfma_peak": round(flops / (tower_ms * 1e-3) / 1e12
+                                                  / PEAK_FP32_MFMA_TFLOPS, 4),
+            "tower_flops_per_batch": flops, "steps": steps}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -270,6 +337,7 @@ def main():
                 "launches": gu["launches"]}
 
     image = image_leg(model, dev, args.image_steps) if args.image_steps > 0 else None
+    audio = audio_leg(model, dev, args.audio_steps) if args.audio_steps > 0 else None
     cpu = cpu_baseline(cfg, weights, rows, args.cpu_sample_rows)
 
     breakdown = {k: {"ms_per_step": round(v["ms"] / args.steps, 3),
@@ -300,6 +368,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": breakdown,
         "image": image,
+        "audio": audio,
     }
     if cpu:
         line["speedup_vs_cpu_baseline"] = round(value / cpu["value"], 1)

@@ -5,8 +5,8 @@
 // 932-1134) and AudioEmbedder::embed_impl (src/model/audio_embedder.rs:
 // 223-267). Weights are validated like AudioWeights::decode (audio.rs:
 // 717-794, including the inverted-bounds check of :850-870) and packed once:
-// fused Q/K/V, interleaved light-conv start projection, transposed layer-1
-// subsampling kernel, and each layer's relative keys (the sinusoidal table
+// fused Q/K/V, interleaved light-conv start projection, and each layer's
+// relative keys (the sinusoidal table
 // times relative_k_proj, input-independent) computed on the GPU at load.
 // A forward call packs every clip's mel frames back to back and runs the
 // tower as one launch sequence; the subsampled rows of all clips are
@@ -70,11 +70,11 @@ struct svl_audio_model {
             right = 0, P = 0, text_hidden = 0, context = 0, positions = 0, H_pad = 0;
     float cap = 0.f, eps = 0.f, rw = 0.f, clip = 0.f, k_scale = 0.f;
     std::vector<float *> allocations;
-    float *w_conv0 = nullptr, *ln0 = nullptr, *w_conv1t = nullptr, *ln1 = nullptr,
+    float *w_conv0 = nullptr, *ln0 = nullptr, *w_conv1 = nullptr, *ln1 = nullptr,
           *w_in = nullptr, *w_out = nullptr, *b_out = nullptr, *w_emb = nullptr;
     std::vector<AuLayer> layers;
     // workspace
-    DevBuf<float> mel, l0, l1, h, n, tmp, act, qkv, att, gated, proj, projn, soft;
+    DevBuf<float> mel, l0, col, l1, h, n, tmp, act, qkv, att, gated, proj, projn, soft;
     DevBuf<uint8_t> mask, mask0, mask1;
     DevBuf<SscpRow> rows0, rows1;
     DevBuf<int32_t> pos, rowlen, valid_idx;
@@ -87,7 +87,7 @@ struct svl_audio_model {
     ~svl_audio_model() {
         if (device >= 0) (void)hipSetDevice(device);
         for (float *p : allocations) (void)hipFree(p);
-        mel.release(); l0.release(); l1.release(); h.release(); n.release(); tmp.release();
+        mel.release(); l0.release(); col.release(); l1.release(); h.release(); n.release(); tmp.release();
         act.release(); qkv.release(); att.release(); gated.release(); proj.release();
         projn.release(); soft.release(); mask.release(); mask0.release(); mask1.release();
         rows0.release(); rows1.release(); pos.release(); rowlen.release(); valid_idx.release();
@@ -305,6 +305,7 @@ svl_status ensure_au_workspace(svl_audio_model *m, const AuBatch &b) {
     HIP_TRY(m->mel.ensure(F * FEATURE_SIZE));
     HIP_TRY(m->mask.ensure(F));
     HIP_TRY(m->l0.ensure(T0 * FREQ0 * m->C0));
+    HIP_TRY(m->col.ensure(T * FREQ1 * 9 * m->C0));
     HIP_TRY(m->l1.ensure(T * FREQ1 * m->C1));
     HIP_TRY(m->h.ensure(T * m->H));
     HIP_TRY(m->n.ensure(T * m->H));
@@ -365,8 +366,15 @@ svl_status enqueue_audio(svl_audio_model *m, const AuBatch &b, const float *d_me
     // Subsampling (audio.rs:1136-1255).
     HIP_TRY(launch_sscp_conv0(d_mel, m->mask.p, m->rows0.p, b.T0, m->w_conv0, m->ln0, (int)m->C0,
                               m->eps, m->l0.p, flag, s));
-    HIP_TRY(launch_sscp_conv1(m->l0.p, m->mask0.p, m->rows1.p, T, m->w_conv1t, m->ln1, (int)m->C0,
-                              (int)m->C1, m->eps, m->l1.p, flag, s));
+    // layer 1: im2col, GEMM against the [C1, 9 C0] weight, LayerNorm + ReLU
+    HIP_TRY(launch_sscp_im2col(m->l0.p, m->mask0.p, m->rows1.p, T, (int)m->C0, m->col.p, s));
+    {
+        const int64_t K = 9 * m->C0;
+        GemmArgs g{m->col.p, K, m->w_conv1, K, m->l1.p, m->C1, (int)(T * FREQ1), (int)m->C1,
+                   (int)K, EPI_STORE, 1.f, nullptr, 0, 0};
+        HIP_TRY(launch_gemm(g, s));
+    }
+    HIP_TRY(launch_sscp_ln_relu(m->l1.p, m->ln1, (int)m->C1, T * FREQ1, m->eps, flag, s));
     {
         const int64_t K = FREQ1 * m->C1;
         GemmArgs g{m->l1.p, K, m->w_in, K, m->h.p, H, (int)T, (int)H, (int)K, EPI_STORE, 1.f,
@@ -627,8 +635,8 @@ svl_status svl_audio_model_create(svl_ctx *ctx, const svl_audio_config *cfg, int
         return fail(SVL_UNSUPPORTED, "audio hidden and projection widths must be multiples of 4 up to 2048");
     if (m->hd > 256 || m->context > 64)
         return fail(SVL_UNSUPPORTED, "audio head dimension above 256 or attention context above 64");
-    if (m->C0 > 512 || sscp_conv1_lds_bytes((int)m->C0, (int)m->C1) > 160 * 1024)
-        return fail(SVL_UNSUPPORTED, "audio subsampling channels exceed the backend's LDS staging");
+    if (m->C0 > 512)
+        return fail(SVL_UNSUPPORTED, "audio subsampling channels above 512 are not supported");
     if ((m->C0 / 4) * m->C1 != FREQ1 * m->C1)
         return fail(SVL_INTERNAL, "audio subsampling output does not match the projection input width");
 
@@ -640,13 +648,7 @@ svl_status svl_audio_model_create(svl_ctx *ctx, const svl_audio_config *cfg, int
     const std::string sp = "audio_tower.subsample_conv_projection.";
     ST_TRY(up(sp + "layer0.conv.weight", &m->w_conv0));
     ST_TRY(up(sp + "layer0.norm.weight", &m->ln0));
-    ST_TRY(decode_named(by_name, sp + "layer1.conv.weight", a));
-    {   // [C1][C0][3][3] -> [C0][3][3][C1]
-        std::vector<float> t(a.size());
-        for (int64_t oc = 0; oc < m->C1; ++oc)
-            for (int64_t r = 0; r < m->C0 * 9; ++r) t[(size_t)(r * m->C1 + oc)] = a[(size_t)(oc * m->C0 * 9 + r)];
-        ST_TRY(upload_owned(m->allocations, t.data(), t.size(), &m->w_conv1t));
-    }
+    ST_TRY(up(sp + "layer1.conv.weight", &m->w_conv1));
     ST_TRY(up(sp + "layer1.norm.weight", &m->ln1));
     ST_TRY(up(sp + "input_proj_linear.weight", &m->w_in));
     ST_TRY(up("audio_tower.output_proj.weight", &m->w_out));

@@ -2,7 +2,8 @@
 // projections are the shared GEMM with the clipped-linear epilogues; what is
 // specific to the tower lives here:
 //  * the two stride-2 3x3 subsampling convolutions, each with its per-position
-//    LayerNorm (weight, no bias) and ReLU (audio.rs:1136-1255, 1290-1322);
+//    LayerNorm (weight, no bias) and ReLU (audio.rs:1136-1255, 1290-1322):
+//    the first direct, the second as im2col + the MFMA GEMM;
 //  * one fused row kernel for every clamp / RMSNorm / residual / next-norm
 //    chain of the conformer block (audio.rs:1374-1433, 1000-1066);
 //  * the chunked local attention with relative positions and the logit soft
@@ -99,88 +100,80 @@ hipError_t launch_sscp_conv0(const float *mel, const uint8_t *mask, const SscpRo
     return hipGetLastError();
 }
 
-// ---- subsampling convolution 1: C0 -> C1 channels + LayerNorm + ReLU -------
-// One workgroup per layer-1 row. The three layer-0 input rows (64 x C0 each,
-// zero where the row is outside the clip or masked) are staged in LDS; each
-// thread computes outputs (f, c) with the reference's summation order
-// (input channel, then kernel row, then kernel column); the raw outputs go
-// to LDS and one wave per frequency applies LayerNorm + ReLU over C1.
-// wt is the layer-1 weight transposed to [C0][3][3][C1].
-__global__ __launch_bounds__(256) void sscp_conv1_kernel(const float *__restrict__ l0,
-                                                         const uint8_t *__restrict__ mask0,
-                                                         const SscpRow *__restrict__ rows,
-                                                         const float *__restrict__ wt,
-                                                         const float *__restrict__ ln, int C0,
-                                                         int C1, float eps, float *__restrict__ out,
-                                                         int *flag) {
-    extern __shared__ float lds[];
-    float *in = lds;                      // [3][FREQ0][C0]
-    float *raw = lds + 3 * FREQ0 * C0;    // [FREQ1][C1]
-    const int r = blockIdx.x, tid = threadIdx.x;
+// ---- subsampling convolution 1 as im2col + GEMM ---------------------------
+// col[(r * 32 + f) * 9 C0 + ic * 9 + kt * 3 + kf] = layer0 input tap, zero
+// where the tap is outside the clip, masked or outside the 64 frequencies:
+// the k order of the layer-1 weight [C1][C0][3][3], so the GEMM against it
+// sums each output in the reference's (channel, row, column) order. One
+// thread per (output position, input channel): coalesced reads over ic.
+__global__ __launch_bounds__(256) void sscp_im2col_kernel(const float *__restrict__ l0,
+                                                          const uint8_t *__restrict__ mask0,
+                                                          const SscpRow *__restrict__ rows,
+                                                          int64_t n_rows, int C0,
+                                                          float *__restrict__ col) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= n_rows * FREQ1 * C0) return;
+    const int ic = (int)(idx % C0);
+    const int64_t pos = idx / C0;
+    const int64_t r = pos / FREQ1;
+    const int f = (int)(pos - r * FREQ1);
     const SscpRow ri = rows[r];
-    const int slice = FREQ0 * C0;
-    for (int i = tid; i < 3 * slice; i += 256) {
-        const int kt = i / slice, it = 2 * ri.t + kt - 1;
-        const bool ok = it >= 0 && it < ri.len && mask0[ri.base + it];
-        in[i] = ok ? l0[(int64_t)(ri.base + it) * slice + (i - kt * slice)] : 0.0f;
-    }
-    __syncthreads();
-    const int n_out = FREQ1 * C1;
-    for (int o = tid; o < n_out; o += 256) {
-        const int f = o / C1, c = o - f * C1;
-        float acc = 0.0f;
-        for (int ic = 0; ic < C0; ++ic) {
+    float *dst = col + pos * (int64_t)(9 * C0) + ic * 9;
 #pragma unroll
-            for (int kt = 0; kt < 3; ++kt)
+    for (int kt = 0; kt < 3; ++kt) {
+        const int it = 2 * ri.t + kt - 1;
+        const bool row_ok = it >= 0 && it < ri.len && mask0[ri.base + it];
 #pragma unroll
-                for (int kf = 0; kf < 3; ++kf) {
-                    const int iff = 2 * f + kf - 1;
-                    if (iff < 0 || iff >= FREQ0) continue;
-                    acc += in[(kt * FREQ0 + iff) * C0 + ic] * wt[((ic * 3 + kt) * 3 + kf) * C1 + c];
-                }
+        for (int kf = 0; kf < 3; ++kf) {
+            const int iff = 2 * f + kf - 1;
+            const bool ok = row_ok && iff >= 0 && iff < FREQ0;
+            dst[kt * 3 + kf] = ok ? l0[((int64_t)(ri.base + it) * FREQ0 + iff) * C0 + ic] : 0.0f;
         }
-        raw[o] = acc;
     }
-    __syncthreads();
-    const int wave = tid >> 6, lane = tid & 63;
+}
+
+hipError_t launch_sscp_im2col(const float *l0, const uint8_t *mask0, const SscpRow *rows,
+                              int64_t n_rows, int C0, float *col, hipStream_t s) {
+    const int64_t n = n_rows * FREQ1 * C0;
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(sscp_im2col_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, l0,
+                       mask0, rows, n_rows, C0, col);
+    return hipGetLastError();
+}
+
+// LayerNorm (weight, no bias) + ReLU over the C channels of each of `n`
+// positions, in place; one wave per position.
+__global__ __launch_bounds__(256) void sscp_ln_relu_kernel(float *__restrict__ x,
+                                                           const float *__restrict__ ln, int C,
+                                                           int64_t n, float eps, int *flag) {
+    const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (p >= n) return;
+    float *row = x + p * C;
+    float s = 0.f;
     bool ok = true;
-    for (int f = wave; f < FREQ1; f += 4) {
-        const float *x = raw + f * C1;
-        float s = 0.f;
-        for (int c = lane; c < C1; c += 64) {
-            ok = ok && isfinite(x[c]);
-            s += x[c];
-        }
-        const float mean = wave_sum(s) / (float)C1;
-        float var = 0.f;
-        for (int c = lane; c < C1; c += 64) {
-            const float d = x[c] - mean;
-            var += d * d;
-        }
-        var = wave_sum(var) / (float)C1;
-        const float inv = 1.0f / sqrtf(var + eps);
-        ok = ok && isfinite(inv);
-        float *o = out + (int64_t)r * n_out + f * C1;
-        for (int c = lane; c < C1; c += 64) o[c] = fmaxf((x[c] - mean) * inv * ln[c], 0.0f);
+    for (int c = lane; c < C; c += 64) {
+        ok = ok && isfinite(row[c]);
+        s += row[c];
     }
+    const float mean = wave_sum(s) / (float)C;
+    float var = 0.f;
+    for (int c = lane; c < C; c += 64) {
+        const float d = row[c] - mean;
+        var += d * d;
+    }
+    var = wave_sum(var) / (float)C;
+    const float inv = 1.0f / sqrtf(var + eps);
+    ok = ok && isfinite(inv);
+    for (int c = lane; c < C; c += 64) row[c] = fmaxf((row[c] - mean) * inv * ln[c], 0.0f);
     if (!ok) raise_flag(flag, FLAG_NONFINITE);
 }
 
-size_t sscp_conv1_lds_bytes(int C0, int C1) {
-    return (size_t)(3 * FREQ0 * C0 + FREQ1 * C1) * sizeof(float);
-}
-
-hipError_t launch_sscp_conv1(const float *l0, const uint8_t *mask0, const SscpRow *rows,
-                             int64_t n_rows, const float *wt, const float *ln, int C0, int C1,
-                             float eps, float *out, int *flag, hipStream_t s) {
-    if (n_rows <= 0) return hipSuccess;
-    const size_t lds = sscp_conv1_lds_bytes(C0, C1);
-    if (lds > 160 * 1024) return hipErrorInvalidValue;
-    hipError_t e = hipFuncSetAttribute((const void *)sscp_conv1_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(sscp_conv1_kernel, dim3((unsigned)n_rows), dim3(256), lds, s, l0, mask0,
-                       rows, wt, ln, C0, C1, eps, out, flag);
+hipError_t launch_sscp_ln_relu(float *x, const float *ln, int C, int64_t n, float eps, int *flag,
+                               hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(sscp_ln_relu_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, x, ln,
+                       C, n, eps, flag);
     return hipGetLastError();
 }
 

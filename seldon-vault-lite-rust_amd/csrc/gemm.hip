@@ -24,9 +24,9 @@
 //    k is unchanged. Every output element sees the same MFMA sequence over k
 //    whatever the tile shape, so results do not depend on the tile chosen
 //    or on a row's position in the batch.
-//  * The tile shape is chosen per launch: 128x128 (3 workgroups per CU) for
-//    wide outputs, 128x64 for mid-size grids, 64x64 x BK 32 (4 per CU) when
-//    N <= 256, where 128x128 tiles would leave most CUs idle.
+//  * The tile shape is chosen per launch from the grid's per-CU work:
+//    128x128 (3 workgroups per CU) for large grids, 128x64 or 64x64 (4 per
+//    CU) when bigger tiles would leave CUs idle or unevenly loaded.
 //  * Tiles are numbered M-major with N fastest and remapped so consecutive
 //    tiles land on the same XCD: the N tiles that share an A block hit that
 //    XCD's L2 instead of HBM.
@@ -394,17 +394,44 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Tile choice: N <= 256 -> 64x64 (x BK 32, 4 workgroups per CU); fewer than
-// four 128x128 tiles per CU -> 128x64; otherwise 128x128 (3 per CU). GeGLU
-// needs 32-column tile pairs, so it always takes 128x128.
+// Tile choice.
+//  * A launch with the whole GPU: workgroups are spread round-robin over the
+//    256 CUs, so it takes about ceil(tiles / 256) tile-times on its busiest
+//    CU; the cost of a tile shape is that count times the tile's MAC count
+//    over the shape's measured efficiency (128x128 at 3 per CU: 1.0; 128x64
+//    and 64x64 at 4 per CU: 0.95 and 0.90). Small grids therefore take
+//    smaller tiles (64x64 for the audio tower's M = 3000 projections), large
+//    ones 128x128. 64x64 uses BK 32 when K is long or N narrow.
+//  * A launch that shares the GPU with other streams (a.cus > 0, the text
+//    path's row groups): measured best is 64x64 for N <= 256, 128x64 below
+//    1024 tiles of 128x128, else 128x128; the other streams' work fills the
+//    partial rounds that the cost model above optimises for.
+//  * Paired epilogues need 32-column tile pairs, so they always take 128x128.
 template <int EPI>
 static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
-    const int64_t tiles128 = (int64_t)((a.M + 127) / 128) * ((a.N + 127) / 128);
-    if constexpr (!paired_epi<EPI>()) {
-        if (a.N <= 256 && a.K % 32 == 0) return launch_dma<64, 64, 32, EPI, 4>(a, s);
-        if (tiles128 < 4 * 256) return launch_dma<128, 64, 16, EPI, 4>(a, s);
+    if constexpr (paired_epi<EPI>()) {
+        return launch_dma<128, 128, 16, EPI, 3>(a, s);
+    } else {
+        auto tiles = [&](int bm, int bn) {
+            return (int64_t)((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn);
+        };
+        if (a.cus > 0) {
+            if (a.N <= 256 && a.K % 32 == 0) return launch_dma<64, 64, 32, EPI, 4>(a, s);
+            if (tiles(128, 128) < 4 * 256) return launch_dma<128, 64, 16, EPI, 4>(a, s);
+            return launch_dma<128, 128, 16, EPI, 3>(a, s);
+        }
+        auto per_cu = [&](int bm, int bn) { return (double)((tiles(bm, bn) + 255) / 256); };
+        const double c128 = per_cu(128, 128) * (128.0 * 128.0);
+        const double c12864 = per_cu(128, 64) * (128.0 * 64.0) / 0.95;
+        const double c64 = per_cu(64, 64) * (64.0 * 64.0) / 0.90;
+        if (c64 < c128 && c64 < c12864) {
+            if (a.K % 32 == 0 && (a.K >= 1024 || a.N <= 256))
+                return launch_dma<64, 64, 32, EPI, 4>(a, s);
+            return launch_dma<64, 64, 16, EPI, 4>(a, s);
+        }
+        if (c12864 < c128) return launch_dma<128, 64, 16, EPI, 4>(a, s);
+        return launch_dma<128, 128, 16, EPI, 3>(a, s);
     }
-    return launch_dma<128, 128, 16, EPI, 3>(a, s);
 }
 
 template <int BM, int BN, int EPI>

@@ -473,6 +473,8 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
     int32_t *pos = m->pos.p + t0, *rowlen = m->rowlen.p + t0;
     const int64_t *offs = m->offsets.p + grp.off_slot;
     const int64_t T_all = b.T;
+    // CUs each launch can expect while the batch's groups run side by side
+    const int cus = b.groups.size() > 1 ? (int)(256 / b.groups.size()) : 0;
 
     HIP_TRY(launch_positions(offs, grp.nrows, pos, rowlen, s));
     {
@@ -489,6 +491,7 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
     {
         GemmArgs g{h, H, m->ple_model, H, ple, L * P, (int)T, (int)(L * P), (int)H, EPI_SCALE,
                    m->ple_scale, nullptr, 0, 0};
+        g.cus = cus;
         Timer tm(m, s, KC_GEMM_PLE_MODEL, 2.0 * Td * H * L * P);
         HIP_TRY(launch_gemm(g, s));
     }
@@ -503,6 +506,7 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
         {
             GemmArgs g{n, H, ly.w_qkv, H, qkv, ldqkv, (int)T, (int)ldqkv, (int)H, EPI_STORE, 1.f,
                        nullptr, 0, 0};
+            g.cus = cus;
             Timer tm(m, s, KC_GEMM_QKV, 2.0 * Td * H * ldqkv);
             HIP_TRY(launch_gemm(g, s));
         }
@@ -537,6 +541,7 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
         {
             GemmArgs g{attn, qd, ly.w_o, qd, tmp, H, (int)T, (int)H, (int)qd, EPI_STORE, 1.f,
                        nullptr, 0, 0};
+            g.cus = cus;
             Timer tm(m, s, KC_GEMM_O, 2.0 * Td * qd * H);
             HIP_TRY(launch_gemm(g, s));
         }
@@ -548,12 +553,14 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
         {
             GemmArgs g{n, H, ly.w_gu, H, act, m->I, (int)T, (int)(2 * m->I_pad), (int)H, EPI_GEGLU,
                        1.f, nullptr, 0, (int)m->I};
+            g.cus = cus;
             Timer tm(m, s, KC_GEMM_GATE_UP, 2.0 * Td * H * 2 * m->I);
             HIP_TRY(launch_gemm(g, s));
         }
         {
             GemmArgs g{act, m->I, ly.w_down, m->I, tmp, H, (int)T, (int)H, (int)m->I, EPI_STORE,
                        1.f, nullptr, 0, 0};
+            g.cus = cus;
             Timer tm(m, s, KC_GEMM_DOWN, 2.0 * Td * m->I * H);
             HIP_TRY(launch_gemm(g, s));
         }
@@ -565,12 +572,14 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
         {
             GemmArgs g{h, H, ly.w_pg, H, pg, P, (int)T, (int)P, (int)H, EPI_GELU_MUL, 1.f,
                        ple + l * P, L * P, 0};
+            g.cus = cus;
             Timer tm(m, s, KC_GEMM_PLE_GATE, 2.0 * Td * H * P);
             HIP_TRY(launch_gemm(g, s));
         }
         {
             GemmArgs g{pg, P, ly.w_pp, P, tmp, H, (int)T, (int)H, (int)P, EPI_STORE, 1.f, nullptr,
                        0, 0};
+            g.cus = cus;
             Timer tm(m, s, KC_GEMM_PLE_PROJ, 2.0 * Td * P * H);
             HIP_TRY(launch_gemm(g, s));
         }
@@ -589,6 +598,7 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
     {
         GemmArgs g{n, H, m->out_proj, H, proj, E, (int)T, (int)E, (int)H, EPI_STORE, 1.f, nullptr,
                    0, 0};
+        g.cus = cus;
         Timer tm(m, s, KC_GEMM_OUT, 2.0 * Td * H * E);
         HIP_TRY(launch_gemm(g, s));
     }

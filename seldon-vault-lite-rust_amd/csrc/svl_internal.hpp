@@ -43,6 +43,7 @@ struct GemmArgs {
     const float *aux;
     int64_t ldaux;
     int n_out;  // EPI_GEGLU / EPI_CLIP_GLU: number of real output columns
+    int cus = 0;               // > 0: the launch shares the GPU with other streams
     int clip_cols = 0;         // output columns per clip segment (0: one segment)
     float clip[4][4] = {};     // per segment: input min, input max, output min, output max
 };
@@ -165,11 +166,13 @@ struct SscpRow {
 hipError_t launch_sscp_conv0(const float *mel, const uint8_t *mask, const SscpRow *rows,
                              int64_t n_rows, const float *w, const float *ln, int C0, float eps,
                              float *out, int *flag, hipStream_t s);
-// Layer 0 -> layer 1 [rows, 32, C1]; wt = layer-1 weight as [C0][3][3][C1].
-size_t sscp_conv1_lds_bytes(int C0, int C1);
-hipError_t launch_sscp_conv1(const float *l0, const uint8_t *mask0, const SscpRow *rows,
-                             int64_t n_rows, const float *wt, const float *ln, int C0, int C1,
-                             float eps, float *out, int *flag, hipStream_t s);
+// Layer-0 taps of every layer-1 output position as rows [pos, 9 C0] in the
+// layer-1 weight's (channel, kernel row, kernel column) order.
+hipError_t launch_sscp_im2col(const float *l0, const uint8_t *mask0, const SscpRow *rows,
+                              int64_t n_rows, int C0, float *col, hipStream_t s);
+// In place: x[p] = relu(layernorm(x[p], ln)) over C channels, n positions.
+hipError_t launch_sscp_ln_relu(float *x, const float *ln, int C, int64_t n, float eps, int *flag,
+                               hipStream_t s);
 // t = w1 ? rms(clamp(x, +-c1), w1) : x; h = res ? res + t * rw : t (-> h_out);
 // if w2: n_out = rms(clamp(h, +-c2), w2).
 hipError_t launch_audio_rows(const float *x, float c1, const float *w1, const float *res, float rw,
