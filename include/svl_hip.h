@@ -377,6 +377,55 @@ svl_status svl_audio_embed_device(svl_audio_model *audio, svl_text_model *text,
                                   const svl_mel *mels, int32_t batch, int64_t dimension,
                                   float *out);
 
+/* ---- log-mel front end ------------------------------------------------------ */
+
+typedef struct svl_log_mel svl_log_mel;
+
+/* Frame layout of log_mel (src/media/audio_preprocess.rs:94-131) for a clip
+ * of `samples` 16 kHz samples (truncated at 480000, the 30 s cap of
+ * src/media/audio.rs:19): mel frames, samples after right-padding to a
+ * multiple of 128, and frames whose analysis window holds real audio.
+ * Empty or too-short clips, and clips with no complete window -> CORRUPT. */
+svl_status svl_log_mel_layout(int64_t samples, int64_t *frames, int64_t *padded_samples,
+                              int64_t *valid_frames);
+
+/* Uploads the Hann window, FFT twiddles and mel filter bank to the current
+ * device of ctx. */
+svl_status svl_log_mel_create(svl_ctx *ctx, svl_log_mel **out);
+svl_status svl_log_mel_destroy(svl_log_mel *lm);
+
+/* log_mel (audio_preprocess.rs:94-200) for `clips` clips of 16 kHz mono
+ * samples: clip i is samples[i][0 .. lengths[i]). features receives the
+ * clips' [frames_i, 128] spectrograms back to back and mask their frame
+ * masks (1 = complete window), frames_i from svl_log_mel_layout. Bit-exact
+ * with the reference's double-precision pipeline. An empty, too-short or
+ * non-finite clip -> CORRUPT; a non-finite feature -> INTERNAL. */
+svl_status svl_log_mel_batch(svl_log_mel *lm, const float *const *samples,
+                             const int64_t *lengths, int32_t clips, float *features,
+                             uint8_t *mask);
+/* Device-resident variant: d_samples holds the clips back to back in HBM
+ * (clip i at offset lengths[0] + ... + lengths[i - 1], all lengths[i]
+ * samples checked for finiteness); d_features [sum frames_i, 128] is
+ * written on `stream` (NULL = the object's stream); mask stays on the host.
+ * Returns after the stream drained. */
+svl_status svl_log_mel_device(svl_log_mel *lm, const float *d_samples, const int64_t *lengths,
+                              int32_t clips, float *d_features, uint8_t *mask, void *stream);
+
+/* AudioEmbedder::embed (audio_embedder.rs:214-267) from 16 kHz samples: the
+ * log-mel spectrogram, the tower and the text model back to back on the
+ * device, without the features leaving HBM. Clips as in svl_log_mel_batch;
+ * out [clips, dimension]. */
+svl_status svl_audio_embed_samples(svl_audio_model *audio, svl_text_model *text,
+                                   const svl_audio_special_tokens *tokens,
+                                   const float *const *samples, const int64_t *lengths,
+                                   int32_t clips, int64_t dimension, float *out);
+/* The same with the samples already in HBM (d_samples as in
+ * svl_log_mel_device). */
+svl_status svl_audio_embed_samples_device(svl_audio_model *audio, svl_text_model *text,
+                                          const svl_audio_special_tokens *tokens,
+                                          const float *d_samples, const int64_t *lengths,
+                                          int32_t clips, int64_t dimension, float *out);
+
 /* ---- deterministic synthetic data (benchmark and tests) ------------------ */
 /* Counter-based SplitMix64: element i of stream s under seed k is
  * u = (splitmix64(k ^ (s * 0x9E3779B97F4A7C15) + i) >> 40) / 2^24 in [0, 1),

@@ -610,3 +610,77 @@ class OracleAudioModel:
             out["sscp_output"] = sscp[: n * H].reshape(n, H)
             out["hidden_states"] = hidden[: L * n * H].reshape(L, n, H)
         return out
+
+
+# ---- audio_preprocess.rs log-mel front end ----------------------------------------
+
+MEL_FEATURES = 128
+
+
+def _mel_lib():
+    L = lib()
+    if not getattr(L, "_mel_ready", False):
+        sz = ctypes.c_size_t
+        d = ctypes.POINTER(ctypes.c_double)
+        L.svlo_hann_window.restype = None
+        L.svlo_hann_window.argtypes = [ctypes.POINTER(ctypes.c_float)]
+        L.svlo_mel_filter_bank.argtypes = [d]
+        L.svlo_fft.argtypes = [d, sz]
+        L.svlo_log_mel_layout.argtypes = [sz, ctypes.POINTER(sz), ctypes.POINTER(sz),
+                                          ctypes.POINTER(sz), ctypes.c_char_p, sz]
+        L.svlo_log_mel.argtypes = [ctypes.POINTER(ctypes.c_float), sz,
+                                   ctypes.POINTER(ctypes.c_float),
+                                   ctypes.POINTER(ctypes.c_ubyte), ctypes.c_char_p, sz]
+        L._mel_ready = True
+    return L
+
+
+def hann_window():
+    out = np.zeros(320, np.float32)
+    _mel_lib().svlo_hann_window(_fp(out))
+    return out
+
+
+def mel_filter_bank():
+    """[257 bins, 128 filters] float64."""
+    out = np.zeros((257, MEL_FEATURES), np.float64)
+    _check(_mel_lib().svlo_mel_filter_bank(out.ctypes.data_as(ctypes.POINTER(ctypes.c_double))),
+           "filter bank")
+    return out
+
+
+def fft(values):
+    """FftPlan::forward on a complex vector of power-of-two length."""
+    v = np.ascontiguousarray(values, np.complex128).copy()
+    _check(_mel_lib().svlo_fft(v.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), v.size), "fft")
+    return v
+
+
+def log_mel_layout(samples):
+    """(frames, padded_samples, valid_frames) for a clip of `samples` samples."""
+    sz = ctypes.c_size_t
+    f, p, v = sz(), sz(), sz()
+    msg = ctypes.create_string_buffer(256)
+    _check(_mel_lib().svlo_log_mel_layout(samples, ctypes.byref(f), ctypes.byref(p),
+                                          ctypes.byref(v), msg, 256), msg.value.decode())
+    return f.value, p.value, v.value
+
+
+def log_mel(samples):
+    """log_mel (audio_preprocess.rs:94-200): (features [frames, 128] f32,
+    mask [frames] bool, padded_samples, valid_frames)."""
+    x = _f32(samples).ravel()
+    msg = ctypes.create_string_buffer(256)
+    if x.size == 0:
+        _check(_mel_lib().svlo_log_mel(_fp(np.zeros(1, np.float32)), 0, None, None, msg, 256),
+               msg.value.decode())
+    try:
+        frames, padded, valid = log_mel_layout(min(x.size, 480000))
+    except OracleError:
+        frames, padded, valid = 1, 0, 0
+    feats = np.zeros((frames, MEL_FEATURES), np.float32)
+    mask = np.zeros(frames, np.uint8)
+    _check(_mel_lib().svlo_log_mel(_fp(x), x.size, _fp(feats),
+                                   mask.ctypes.data_as(ctypes.POINTER(ctypes.c_ubyte)), msg, 256),
+           msg.value.decode())
+    return feats, mask.astype(bool), padded, valid

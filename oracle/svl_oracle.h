@@ -217,6 +217,26 @@ int svlo_audio_forward(const svlo_audio_config *cfg, const float *const *weights
                        size_t frames, size_t *out_tokens, float *out_pooled, float *out_sscp,
                        float *out_hidden, char *msg, size_t msg_len);
 
+/* Log-mel front end, src/media/audio_preprocess.rs:24-46 constants. */
+#define SVLO_MEL_FRAME_LENGTH 320
+#define SVLO_MEL_HOP 160
+#define SVLO_MEL_FFT 512
+#define SVLO_MEL_FEATURES 128
+#define SVLO_MEL_BINS (SVLO_MEL_FFT / 2 + 1)
+#define SVLO_MEL_FLOOR 0.001
+#define SVLO_MEL_PAD_TO 128
+#define SVLO_MEL_MAX_FRAMES 3000
+/* src/media/audio.rs:19: 30 s at 16 kHz */
+#define SVLO_MEL_MAX_SAMPLES 480000
+
+void svlo_hann_window(float *out);
+int svlo_mel_filter_bank(double *out);
+int svlo_fft(double *values, size_t n);
+int svlo_log_mel_layout(size_t samples, size_t *frames, size_t *padded_samples,
+                        size_t *valid_frames, char *msg, size_t msg_len);
+int svlo_log_mel(const float *samples, size_t n_samples, float *features, unsigned char *mask,
+                 char *msg, size_t msg_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,7 @@
 
 #include "../../include/svl_hip.h"
 #include "host_common.hpp"
+#include "mel_host.hpp"
 #include "svl_internal.hpp"
 
 namespace {
@@ -82,9 +83,11 @@ struct svl_audio_model {
     DevBuf<int> flag;
     int *h_flag = nullptr;
     hipStream_t stream = nullptr;
+    svl_log_mel *lm = nullptr;  // log-mel tables, created by the first sample call
     std::mutex mu;
 
     ~svl_audio_model() {
+        delete lm;
         if (device >= 0) (void)hipSetDevice(device);
         for (float *p : allocations) (void)hipFree(p);
         mel.release(); l0.release(); col.release(); l1.release(); h.release(); n.release(); tmp.release();
@@ -541,9 +544,8 @@ svl_status run_audio(svl_audio_model *m, const svl_mel *mels, int32_t batch,
 }
 
 // AudioEmbedder::embed_impl (audio_embedder.rs:223-267) for a batch.
-svl_status audio_embed(svl_audio_model *m, svl_text_model *text,
-                       const svl_audio_special_tokens *tokens, const svl_mel *mels, int32_t batch,
-                       const float *d_features, int64_t dimension, float *out) {
+svl_status embed_checks(svl_audio_model *m, svl_text_model *text,
+                        const svl_audio_special_tokens *tokens, int64_t dimension, float *out) {
     if (!m || !text || !tokens || !out)
         return fail(SVL_USAGE, "models, special tokens and output are required");
     const int64_t E = text_embedding_dim(text);
@@ -555,7 +557,15 @@ svl_status audio_embed(svl_audio_model *m, svl_text_model *text,
     if (text_hidden_size(text) != m->text_hidden)
         return fail(SVL_USAGE, "the audio projection width %lld is not the text hidden size %lld",
                     (long long)m->text_hidden, (long long)text_hidden_size(text));
-    std::lock_guard<std::mutex> lock(m->mu);
+    return SVL_OK;
+}
+
+// The embedder body; caller holds m->mu and ran embed_checks.
+svl_status audio_embed_locked(svl_audio_model *m, svl_text_model *text,
+                              const svl_audio_special_tokens *tokens, const svl_mel *mels,
+                              int32_t batch, const float *d_features, int64_t dimension,
+                              float *out) {
+    const int64_t E = text_embedding_dim(text);
     AuBatch b;
     ST_TRY(run_audio(m, mels, batch, d_features, m->stream, b, nullptr, nullptr, nullptr, nullptr));
     if (batch == 0) return SVL_OK;
@@ -589,6 +599,39 @@ svl_status audio_embed(svl_audio_model *m, svl_text_model *text,
         ST_TRY(svl_truncate_and_normalize(normalized.data() + (size_t)i * E, (size_t)E,
                                           (size_t)dimension, out + (size_t)i * dimension));
     return SVL_OK;
+}
+
+svl_status audio_embed(svl_audio_model *m, svl_text_model *text,
+                       const svl_audio_special_tokens *tokens, const svl_mel *mels, int32_t batch,
+                       const float *d_features, int64_t dimension, float *out) {
+    ST_TRY(embed_checks(m, text, tokens, dimension, out));
+    std::lock_guard<std::mutex> lock(m->mu);
+    return audio_embed_locked(m, text, tokens, mels, batch, d_features, dimension, out);
+}
+
+// AudioEmbedder::embed from 16 kHz samples (audio_embedder.rs:235-237): the
+// log-mel features are computed into HBM on the model's stream and feed the
+// tower directly.
+svl_status audio_embed_samples(svl_audio_model *m, svl_text_model *text,
+                               const svl_audio_special_tokens *tokens,
+                               const float *const *h_samples, const float *d_samples,
+                               const int64_t *lengths, int32_t clips, int64_t dimension,
+                               float *out) {
+    ST_TRY(embed_checks(m, text, tokens, dimension, out));
+    std::lock_guard<std::mutex> lock(m->mu);
+    HIP_TRY(hipSetDevice(m->device));
+    if (!m->lm) ST_TRY(mel_create_on(m->device, &m->lm));
+    MelBatch mb;
+    ST_TRY(mel_plan(lengths, clips, mb));
+    if (clips == 0) return SVL_OK;
+    HIP_TRY(m->lm->features.ensure((size_t)(mb.total_frames * FEATURE_SIZE)));
+    ST_TRY(mel_compute(m->lm, mb, h_samples, d_samples, lengths, m->lm->features.p, m->stream));
+    std::vector<svl_mel> mels((size_t)clips);
+    for (int32_t i = 0; i < clips; ++i)
+        mels[(size_t)i] = {nullptr, mb.mask.data() + mb.frame_off[(size_t)i],
+                           mb.frame_off[(size_t)i + 1] - mb.frame_off[(size_t)i]};
+    return audio_embed_locked(m, text, tokens, mels.data(), clips, m->lm->features.p, dimension,
+                              out);
 }
 
 }  // namespace
@@ -780,6 +823,24 @@ svl_status svl_audio_embed_device(svl_audio_model *m, svl_text_model *text,
                                   float *out) {
     if (!d_features) return fail(SVL_USAGE, "features are required");
     return audio_embed(m, text, tokens, mels, batch, d_features, dimension, out);
+}
+
+svl_status svl_audio_embed_samples(svl_audio_model *audio, svl_text_model *text,
+                                   const svl_audio_special_tokens *tokens,
+                                   const float *const *samples, const int64_t *lengths,
+                                   int32_t clips, int64_t dimension, float *out) {
+    if (clips > 0 && !samples) return fail(SVL_USAGE, "samples are required");
+    return audio_embed_samples(audio, text, tokens, samples, nullptr, lengths, clips, dimension,
+                               out);
+}
+
+svl_status svl_audio_embed_samples_device(svl_audio_model *audio, svl_text_model *text,
+                                          const svl_audio_special_tokens *tokens,
+                                          const float *d_samples, const int64_t *lengths,
+                                          int32_t clips, int64_t dimension, float *out) {
+    if (clips > 0 && !d_samples) return fail(SVL_USAGE, "samples are required");
+    return audio_embed_samples(audio, text, tokens, nullptr, d_samples, lengths, clips, dimension,
+                               out);
 }
 
 }  // extern "C"

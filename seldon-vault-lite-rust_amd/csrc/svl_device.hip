@@ -5,3 +5,4 @@
 #include "attention.hip"
 #include "vision.hip"
 #include "audio.hip"
+#include "mel.hip"

@@ -202,4 +202,27 @@ hipError_t launch_lconv(const float *gated, const float *dw, int K, const int32_
 hipError_t launch_compact_rms(const float *x, const int32_t *idx, float *out, int64_t rows,
                               int width, float eps, int *flag, hipStream_t s);
 
+// ---- log-mel front end ---------------------------------------------------------
+// One clip of packed 16 kHz samples: samples [sample_base, sample_base +
+// samples) (already truncated to 30 s), frames [frame_base, frame_base + frames).
+struct MelClip {
+    int64_t sample_base;
+    int64_t frame_base;
+    int32_t samples;
+    int32_t frames;
+};
+// Device tables: Hann window [320] f32, twiddles [256] (cos, sin) f64, and the
+// non-zero mel filter weights in CSR form: filter f owns entries
+// [filt_start[f], filt_start[f + 1]) of (filt_bin, filt_weight), bins ascending.
+struct MelTables {
+    const float *window;
+    const double *twiddle;
+    const int32_t *filt_start;
+    const int32_t *filt_bin;
+    const double *filt_weight;
+};
+// out [total_frames, 128]; frames whose window is incomplete are zero rows.
+hipError_t launch_log_mel(const float *x, const MelClip *clips, int n_clips, int64_t total_frames,
+                          const MelTables &t, float *out, int *flag, hipStream_t s);
+
 }  // namespace svl

@@ -103,7 +103,9 @@ EXPORTED = [
     "svl_vision_forward_device", "svl_image_embed_batch", "svl_image_embed_device",
     "svl_audio_model_create", "svl_audio_model_destroy", "svl_audio_token_count",
     "svl_audio_forward_batch", "svl_audio_forward_device", "svl_audio_embed_batch",
-    "svl_audio_embed_device",
+    "svl_audio_embed_device", "svl_log_mel_layout", "svl_log_mel_create", "svl_log_mel_destroy",
+    "svl_log_mel_batch", "svl_log_mel_device", "svl_audio_embed_samples",
+    "svl_audio_embed_samples_device",
 ]
 
 _lib = None

@@ -5,9 +5,12 @@ reference crate's API:
 * ``MelSpectrogram`` — the log-mel input of src/media/audio_preprocess.rs:50-90
 * ``AudioModel`` — audio.rs:932-1134 (``forward`` -> ``AudioOutput``), plus
   ``forward_batch`` (many clips, one launch sequence) and ``forward_device``
-* ``AudioEmbedder`` — src/model/audio_embedder.rs:100-267 over mel spectrograms
-  (decoding audio and computing the log-mel spectrogram is the CPU front end,
-  not part of this backend)
+* ``log_mel`` / ``LogMel`` — the log-mel front end of
+  src/media/audio_preprocess.rs:94-200 on the GPU (bit-exact with the
+  reference's double-precision FFT and mel projection)
+* ``AudioEmbedder`` — src/model/audio_embedder.rs:100-267, from 16 kHz samples
+  (``embed``: log-mel, tower and text model without the features leaving
+  HBM) or from mel spectrograms (``embed_mel``)
 
 Compute runs only in libsvl_hip.so; there is no CPU fallback.
 """
@@ -35,6 +38,7 @@ MAX_AUDIO_CONTEXT = 4_096
 MAX_AUDIO_CONFIG_BYTES = 1024 * 1024
 FEATURE_SIZE = 128
 MAX_MEL_FRAMES = 3_000
+MAX_AUDIO_SAMPLES = 480_000  # media/audio.rs:19, 30 s at 16 kHz
 _BOUNDS = ("input_min", "input_max", "output_min", "output_max")
 
 
@@ -81,6 +85,13 @@ def _load():
         L.svl_audio_forward_device.argtypes = [vp, vp, vp, i32, vp, vp]
         L.svl_audio_embed_batch.argtypes = [vp, vp, vp, vp, i32, i64, vp]
         L.svl_audio_embed_device.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp]
+        L.svl_log_mel_layout.argtypes = [i64, vp, vp, vp]
+        L.svl_log_mel_create.argtypes = [vp, ctypes.POINTER(vp)]
+        L.svl_log_mel_destroy.argtypes = [vp]
+        L.svl_log_mel_batch.argtypes = [vp, vp, vp, i32, vp, vp]
+        L.svl_log_mel_device.argtypes = [vp, vp, vp, i32, vp, vp, vp]
+        L.svl_audio_embed_samples.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp]
+        L.svl_audio_embed_samples_device.argtypes = [vp, vp, vp, vp, vp, i32, i64, vp]
         L._audio_ready = True
     return L
 
@@ -275,11 +286,17 @@ class MelSpectrogram:
     """Row-major [frames, 128] log-mel features with the frame mask
     (audio_preprocess.rs:50-90)."""
 
-    def __init__(self, features, mask):
+    def __init__(self, features, mask, padded_samples=None):
         self.features = np.ascontiguousarray(features, np.float32).reshape(-1, FEATURE_SIZE)
         self.mask = np.ascontiguousarray(np.asarray(mask, bool).reshape(-1).astype(np.uint8))
         if self.mask.size != self.features.shape[0]:
             raise SvlError(7, "audio mel mask does not match the frame count")
+        self._padded = padded_samples
+
+    def padded_samples(self):
+        """16 kHz samples after right-padding to a multiple of 128 (None when
+        the spectrogram was not computed here)."""
+        return self._padded
 
     @property
     def frames(self):
@@ -296,6 +313,85 @@ class MelSpectrogram:
     def _c(self, with_features=True):
         return _Mel(self.features.ctypes.data if with_features else None, self.mask.ctypes.data,
                     self.frames)
+
+
+def _lengths(clips):
+    xs = [np.ascontiguousarray(np.asarray(c, np.float32).reshape(-1)) for c in clips]
+    lengths = np.array([x.size for x in xs], np.int64)
+    ptrs = (ctypes.c_void_p * max(len(xs), 1))(*[x.ctypes.data for x in xs])
+    return xs, lengths, ptrs
+
+
+def log_mel_layout(samples: int):
+    """(frames, padded_samples, valid_frames) of a clip of `samples` 16 kHz
+    samples (audio_preprocess.rs:94-131)."""
+    f, p, v = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    _check(_load().svl_log_mel_layout(int(samples), ctypes.byref(f), ctypes.byref(p),
+                                      ctypes.byref(v)))
+    return f.value, p.value, v.value
+
+
+class LogMel:
+    """The log-mel front end (audio_preprocess.rs:94-200) on one device."""
+
+    _cache = {}
+
+    def __init__(self, device: svl_amd.Device | None = None):
+        self.device = device or svl_amd.Device.get(0)
+        h = ctypes.c_void_p()
+        _check(_load().svl_log_mel_create(self.device.handle, ctypes.byref(h)))
+        self.handle = h
+
+    @classmethod
+    def get(cls, ordinal=0):
+        if ordinal not in cls._cache:
+            cls._cache[ordinal] = cls(svl_amd.Device.get(ordinal))
+        return cls._cache[ordinal]
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            _load().svl_log_mel_destroy(self.handle)
+            self.handle = None
+
+    def compute(self, samples) -> MelSpectrogram:
+        return self.compute_batch([samples])[0]
+
+    def compute_batch(self, clips) -> list:
+        xs, lengths, ptrs = _lengths(clips)
+        layouts = [log_mel_layout(n) if n > 0 else (0, 0, 0) for n in lengths]
+        total = sum(l[0] for l in layouts)
+        feats = np.empty((max(total, 1), FEATURE_SIZE), np.float32)
+        mask = np.empty(max(total, 1), np.uint8)
+        _check(_load().svl_log_mel_batch(self.handle, ptrs, ctypes.c_void_p(lengths.ctypes.data),
+                                         len(xs), ctypes.c_void_p(feats.ctypes.data),
+                                         ctypes.c_void_p(mask.ctypes.data)))
+        out, o = [], 0
+        for f, p, _ in layouts:
+            out.append(MelSpectrogram(feats[o:o + f].copy(), mask[o:o + f].astype(bool), p))
+            o += f
+        return out
+
+    def compute_device(self, samples_dev_ptr: int, lengths, features_dev_ptr: int, stream=None):
+        """Clips back to back in HBM -> features [sum frames, 128] in HBM;
+        returns the host frame masks, one array per clip."""
+        lengths = np.ascontiguousarray(lengths, np.int64)
+        layouts = [log_mel_layout(n) if n > 0 else (0, 0, 0) for n in lengths]
+        mask = np.empty(max(sum(l[0] for l in layouts), 1), np.uint8)
+        _check(_load().svl_log_mel_device(self.handle, ctypes.c_void_p(samples_dev_ptr),
+                                          ctypes.c_void_p(lengths.ctypes.data), len(lengths),
+                                          ctypes.c_void_p(features_dev_ptr),
+                                          ctypes.c_void_p(mask.ctypes.data),
+                                          ctypes.c_void_p(stream) if stream else None))
+        out, o = [], 0
+        for f, _, _ in layouts:
+            out.append(mask[o:o + f].astype(bool))
+            o += f
+        return out
+
+
+def log_mel(samples) -> MelSpectrogram:
+    """log_mel (audio_preprocess.rs:94-200) of 16 kHz mono samples on device 0."""
+    return LogMel.get(0).compute(samples)
 
 
 class AudioOutput:
@@ -414,6 +510,31 @@ class AudioEmbedder:
 
     def special_tokens(self):
         return self.tokens
+
+    def embed(self, samples, dimension: int):
+        """AudioEmbedder::embed (audio_embedder.rs:214-267) of 16 kHz mono
+        samples: log-mel, tower and text model on the device."""
+        return self.embed_samples_batch([samples], dimension)[0]
+
+    def embed_samples_batch(self, clips, dimension: int):
+        xs, lengths, ptrs = _lengths(clips)
+        out = np.empty((max(len(xs), 1), int(dimension)), np.float32)
+        tok = self.tokens._c()
+        _check(_load().svl_audio_embed_samples(self.audio.handle, self.model.handle,
+                                               ctypes.byref(tok), ptrs,
+                                               ctypes.c_void_p(lengths.ctypes.data), len(xs),
+                                               int(dimension), ctypes.c_void_p(out.ctypes.data)))
+        return out[: len(xs)]
+
+    def embed_samples_device(self, samples_dev_ptr: int, lengths, dimension: int):
+        lengths = np.ascontiguousarray(lengths, np.int64)
+        out = np.empty((max(len(lengths), 1), int(dimension)), np.float32)
+        tok = self.tokens._c()
+        _check(_load().svl_audio_embed_samples_device(
+            self.audio.handle, self.model.handle, ctypes.byref(tok),
+            ctypes.c_void_p(samples_dev_ptr), ctypes.c_void_p(lengths.ctypes.data), len(lengths),
+            int(dimension), ctypes.c_void_p(out.ctypes.data)))
+        return out[: len(lengths)]
 
     def embed_mel(self, mel: MelSpectrogram, dimension: int):
         return self.embed_batch([mel], dimension)[0]

@@ -101,3 +101,28 @@ def test_token_count_matches_the_oracle_masks(frames):
     m1 = [m0[2 * i] if 2 * i < f1 else False for i in range(f2)]
     assert mel.audio_tokens() == sum(m1)
     assert O._audio_lib().svlo_audio_subsampled_frames(frames) == f2
+
+
+@pytest.mark.parametrize("n", [129, 161, 320, 481, 1600, 2000, 16000, 479999, 480000, 480001,
+                               10_000_000])
+def test_log_mel_layout_matches_the_oracle(n):
+    """svl_log_mel_layout is host code: frames, padded length and valid
+    frames of audio_preprocess.rs:103-131 for clips around every boundary."""
+    try:
+        want = O.log_mel_layout(n)
+        if want[2] == 0:
+            raise O.OracleError(4)
+    except O.OracleError as e:
+        with pytest.raises(S.SvlError) as got:
+            A.log_mel_layout(n)
+        assert got.value.kind == "Corrupt" and e.status == 4
+        return
+    assert A.log_mel_layout(n) == want
+
+
+@pytest.mark.parametrize("n", [0, 1, 10, 128, 150, 160])
+def test_log_mel_layout_rejects_short_clips(n):
+    # audio_preprocess.rs:95-97, 115-120, 186-190: all Corrupt
+    with pytest.raises(S.SvlError) as e:
+        A.log_mel_layout(n)
+    assert e.value.kind == "Corrupt"
