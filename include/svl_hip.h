@@ -426,6 +426,68 @@ svl_status svl_audio_embed_samples_device(svl_audio_model *audio, svl_text_model
                                           const float *d_samples, const int64_t *lengths,
                                           int32_t clips, int64_t dimension, float *out);
 
+/* ---- tokenizer and text embedding from strings ---------------------------- */
+
+typedef struct svl_tokenizer svl_tokenizer;
+
+/* Tokenizer::from_json_str (src/model/tokenizer.rs:96-334): parses a
+ * tokenizer.json document (UTF-8, at most 64 MiB, the JSON limits of
+ * :569-578) and validates the BPE pipeline strictly: an inconsistent
+ * document -> CORRUPT, a pipeline other than the frozen model's ->
+ * UNSUPPORTED, a cap -> LIMIT. */
+svl_status svl_tokenizer_create(const char *json, size_t len, svl_tokenizer **out);
+svl_status svl_tokenizer_destroy(svl_tokenizer *tokenizer);
+
+/* Tokenizer::encode (tokenizer.rs:339-389) of `len` bytes of UTF-8 text
+ * (invalid UTF-8 -> CORRUPT). *count receives the number of ids; when it
+ * exceeds `capacity` the call returns USAGE and writes nothing. Input above
+ * 1 MiB or more than 262144 tokens -> LIMIT. */
+svl_status svl_tokenizer_encode(const svl_tokenizer *tokenizer, const char *text, size_t len,
+                                int add_special_tokens, uint32_t *ids, size_t capacity,
+                                size_t *count);
+/* encode for `n` texts on several host threads: text i's ids land in
+ * ids[offsets[i] .. offsets[i + 1]) (offsets [n + 1]). The first failing
+ * text, in order, gives the status. */
+svl_status svl_tokenizer_encode_batch(const svl_tokenizer *tokenizer, const char *const *texts,
+                                      const size_t *lens, int32_t n, int add_special_tokens,
+                                      uint32_t *ids, size_t capacity, int64_t *offsets);
+/* Tokenizer::decode (tokenizer.rs:391-425): an unknown id or invalid UTF-8
+ * output -> CORRUPT; *len as in encode. */
+svl_status svl_tokenizer_decode(const svl_tokenizer *tokenizer, const uint32_t *ids, size_t n,
+                                int skip_special_tokens, char *out, size_t capacity, size_t *len);
+/* tokenizer.rs:427-471 accessors; -1 / NULL where the reference returns
+ * None. svl_tokenizer_token's string lives as long as the tokenizer. */
+int64_t svl_tokenizer_token_id(const svl_tokenizer *tokenizer, const char *token, size_t len);
+const char *svl_tokenizer_token(const svl_tokenizer *tokenizer, uint32_t id, size_t *len);
+int64_t svl_tokenizer_vocab_size(const svl_tokenizer *tokenizer);
+int64_t svl_tokenizer_max_token_id(const svl_tokenizer *tokenizer);
+int64_t svl_tokenizer_bos_id(const svl_tokenizer *tokenizer);
+int64_t svl_tokenizer_eos_id(const svl_tokenizer *tokenizer);
+int64_t svl_tokenizer_unk_id(const svl_tokenizer *tokenizer);
+int64_t svl_tokenizer_pad_id(const svl_tokenizer *tokenizer);
+int svl_tokenizer_is_special_id(const svl_tokenizer *tokenizer, uint32_t id);
+
+/* Prompt roles of src/model/prompt.rs:38-55, in that order. */
+typedef enum {
+    SVL_PROMPT_SEARCH_QUERY = 0,
+    SVL_PROMPT_DOCUMENT = 1,
+    SVL_PROMPT_CLASSIFICATION = 2,
+    SVL_PROMPT_CLUSTERING = 3,
+    SVL_PROMPT_CODE_RETRIEVAL = 4,
+    SVL_PROMPT_FACT_CHECKING = 5,
+    SVL_PROMPT_SENTENCE_SIMILARITY = 6,
+    SVL_PROMPT_QUESTION_ANSWERING = 7
+} svl_prompt;
+
+/* TextEmbedder::embed (src/model/text.rs:610-626) for `n` texts: the
+ * prompt's prefix, encode with <bos>/<eos> (host threads), more than 8192
+ * tokens -> LIMIT, then one batched forward pass and
+ * ForwardOutput::embedding(dimension) (dimension outside 1..=embedding_dim
+ * -> INTERNAL). out [n, dimension]. */
+svl_status svl_text_embed_texts(svl_text_model *model, const svl_tokenizer *tokenizer,
+                                const char *const *texts, const size_t *lens, int32_t n,
+                                int32_t prompt, int64_t dimension, float *out);
+
 /* ---- deterministic synthetic data (benchmark and tests) ------------------ */
 /* Counter-based SplitMix64: element i of stream s under seed k is
  * u = (splitmix64(k ^ (s * 0x9E3779B97F4A7C15) + i) >> 40) / 2^24 in [0, 1),

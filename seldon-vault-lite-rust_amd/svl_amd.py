@@ -105,7 +105,12 @@ EXPORTED = [
     "svl_audio_forward_batch", "svl_audio_forward_device", "svl_audio_embed_batch",
     "svl_audio_embed_device", "svl_log_mel_layout", "svl_log_mel_create", "svl_log_mel_destroy",
     "svl_log_mel_batch", "svl_log_mel_device", "svl_audio_embed_samples",
-    "svl_audio_embed_samples_device",
+    "svl_audio_embed_samples_device", "svl_tokenizer_create", "svl_tokenizer_destroy",
+    "svl_tokenizer_encode", "svl_tokenizer_encode_batch", "svl_tokenizer_decode",
+    "svl_tokenizer_token_id", "svl_tokenizer_token", "svl_tokenizer_vocab_size",
+    "svl_tokenizer_max_token_id", "svl_tokenizer_bos_id", "svl_tokenizer_eos_id",
+    "svl_tokenizer_unk_id", "svl_tokenizer_pad_id", "svl_tokenizer_is_special_id",
+    "svl_text_embed_texts",
 ]
 
 _lib = None
