@@ -488,6 +488,47 @@ svl_status svl_text_embed_texts(svl_text_model *model, const svl_tokenizer *toke
                                 const char *const *texts, const size_t *lens, int32_t n,
                                 int32_t prompt, int64_t dimension, float *out);
 
+/* ---- exact vector search ---------------------------------------------------- */
+
+typedef struct svl_vector_index svl_vector_index;
+
+/* The vector view of Index::build (src/index/mod.rs:251-309): `n` chunk
+ * embeddings [n, dimension] (host, caller order) with their chunk ids,
+ * copied into HBM. An empty index has no dimension. dimension outside
+ * 1..=8192 (storage/model.rs:35) -> LIMIT. */
+svl_status svl_vector_index_create(svl_ctx *ctx, const float *embeddings,
+                                   const uint64_t *chunk_ids, int64_t n, int64_t dimension,
+                                   svl_vector_index **out);
+svl_status svl_vector_index_destroy(svl_vector_index *index);
+int64_t svl_vector_index_size(const svl_vector_index *index);
+int64_t svl_vector_index_dimension(const svl_vector_index *index);
+
+/* vector::rank (src/index/vector.rs:17-97) for `nq` queries [nq, query_dim]
+ * and the pagination slice of Index::search (mod.rs:347-359): entries
+ * [offset, offset + limit) of each query's ranking by descending cosine
+ * score (computed in double exactly as the reference computes it), ties by
+ * ascending chunk id. mask: NULL (no filter) or bytes in caller order, row
+ * q at mask + q * mask_stride (mask_stride 0: one row for every query);
+ * only chunks with a non-zero byte are ranked (Filters::matches).
+ *  out_index  [nq, limit] caller indices of the hits
+ *  out_score  [nq, limit] cosine scores
+ *  out_count  [nq] hits written for each query
+ * Validation per query in the reference's order: empty -> USAGE, more than
+ * 8192 dimensions -> LIMIT, a non-finite value or a zero norm -> USAGE, a
+ * dimension other than the index's -> USAGE; an admitted chunk with a zero
+ * or non-finite norm -> INTERNAL. */
+svl_status svl_vector_rank(svl_vector_index *index, const float *queries, int32_t nq,
+                           int64_t query_dim, const uint8_t *mask, int64_t mask_stride,
+                           int64_t offset, int64_t limit, int64_t *out_index, double *out_score,
+                           int64_t *out_count);
+/* The same with the queries already in HBM (d_queries [nq, query_dim], for
+ * example the text embedder's device output); their norms and checks run on
+ * `stream` (NULL = the index's stream). */
+svl_status svl_vector_rank_device(svl_vector_index *index, const float *d_queries, int32_t nq,
+                                  int64_t query_dim, const uint8_t *mask, int64_t mask_stride,
+                                  int64_t offset, int64_t limit, int64_t *out_index,
+                                  double *out_score, int64_t *out_count, void *stream);
+
 /* ---- deterministic synthetic data (benchmark and tests) ------------------ */
 /* Counter-based SplitMix64: element i of stream s under seed k is
  * u = (splitmix64(k ^ (s * 0x9E3779B97F4A7C15) + i) >> 40) / 2^24 in [0, 1),

@@ -684,3 +684,40 @@ def log_mel(samples):
                                    mask.ctypes.data_as(ctypes.POINTER(ctypes.c_ubyte)), msg, 256),
            msg.value.decode())
     return feats, mask.astype(bool), padded, valid
+
+
+# ---- index/vector.rs exact cosine ranking -------------------------------------------
+
+def vector_rank(query, embeddings, chunk_ids, mask=None, has_dim=None):
+    """vector::rank (vector.rs:17-97): the full ranking as (indices, scores)."""
+    L = lib()
+    if not getattr(L, "_search_ready", False):
+        sz = ctypes.c_size_t
+        L.svlo_vector_rank.argtypes = [ctypes.POINTER(ctypes.c_float), sz,
+                                       ctypes.POINTER(ctypes.c_float),
+                                       ctypes.POINTER(ctypes.c_uint64), sz, sz, ctypes.c_int,
+                                       ctypes.POINTER(ctypes.c_ubyte), ctypes.POINTER(sz),
+                                       ctypes.POINTER(ctypes.c_double), ctypes.POINTER(sz),
+                                       ctypes.c_char_p, sz]
+        L._search_ready = True
+    q = _f32(query).ravel()
+    e = _f32(embeddings)
+    n = e.shape[0] if e.ndim == 2 else 0
+    dim = e.shape[1] if e.ndim == 2 else 0
+    e = e.reshape(-1) if e.size else np.zeros(1, np.float32)
+    ids = np.ascontiguousarray(chunk_ids, np.uint64)
+    if ids.size == 0:
+        ids = np.zeros(1, np.uint64)
+    m = None if mask is None else np.ascontiguousarray(mask, np.uint8)
+    out_i = np.zeros(max(n, 1), np.uintp)
+    out_s = np.zeros(max(n, 1), np.float64)
+    cnt = ctypes.c_size_t()
+    msg = ctypes.create_string_buffer(256)
+    qq = q if q.size else np.zeros(1, np.float32)
+    _check(L.svlo_vector_rank(_fp(qq), q.size, _fp(e), ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)),
+                              n, dim, int(n > 0 if has_dim is None else has_dim),
+                              None if m is None else m.ctypes.data_as(ctypes.POINTER(ctypes.c_ubyte)),
+                              out_i.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)),
+                              out_s.ctypes.data_as(ctypes.POINTER(ctypes.c_double)),
+                              ctypes.byref(cnt), msg, 256), msg.value.decode())
+    return out_i[: cnt.value].astype(np.int64), out_s[: cnt.value]

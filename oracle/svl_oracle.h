@@ -237,6 +237,16 @@ int svlo_log_mel_layout(size_t samples, size_t *frames, size_t *padded_samples,
 int svlo_log_mel(const float *samples, size_t n_samples, float *features, unsigned char *mask,
                  char *msg, size_t msg_len);
 
+/* Exact vector search, src/index/vector.rs:17-97 (storage/model.rs:35 cap). */
+#define SVLO_MAX_EMBEDDING_DIMENSION 8192
+/* vector::rank over chunks emb [n, dim] with ids [n] (has_dim: the index has a
+ * dimension); mask NULL or [n] 0/1. out_index / out_score [n] receive the full
+ * ranking, *out_count its length. */
+int svlo_vector_rank(const float *query, size_t qlen, const float *emb, const uint64_t *ids,
+                     size_t n, size_t dim, int has_dim, const unsigned char *mask,
+                     size_t *out_index, double *out_score, size_t *out_count, char *msg,
+                     size_t msg_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,3 +6,4 @@
 #include "vision.hip"
 #include "audio.hip"
 #include "mel.hip"
+#include "search.hip"

@@ -225,4 +225,28 @@ struct MelTables {
 hipError_t launch_log_mel(const float *x, const MelClip *clips, int n_clips, int64_t total_frames,
                           const MelTables &t, float *out, int *flag, hipStream_t s);
 
+// ---- exact cosine search ---------------------------------------------------------
+// keys[q, c] = descending total-order key of dot(Q[q], V[c]) / (qnorm[q] *
+// cnorm[c]) accumulated in double in d order; all ones when mask (indexed
+// mask[q * mask_stride + perm[c]]) is given and zero.
+hipError_t launch_cosine_keys(const float *V, const double *cnorm, const float *Q,
+                              const double *qnorm, int nq, int64_t n, int D, const uint8_t *mask,
+                              int64_t mask_stride, const int64_t *perm, uint64_t *keys,
+                              hipStream_t s);
+// qnorm[q] = sqrt(sum Q[q, d]^2) in d order; flag bit 1: a non-finite value,
+// bit 2: a zero or non-finite norm (per query: flags[q]).
+hipError_t launch_query_norms(const float *Q, int nq, int D, double *qnorm, int *flags,
+                              hipStream_t s);
+// Stable ranking of all nq * n keys by (query, key, position). With tmp ==
+// nullptr only *tmp_bytes is computed. *sorted receives the buffer (idx or
+// idx_alt) that holds the flat pair indices q * n + c in ranked order.
+hipError_t rank_sort(const uint64_t *keys, uint64_t *keys_alt, uint32_t *idx, uint32_t *idx_alt,
+                     uint32_t *qkey, int nq, int64_t n, void *tmp, size_t *tmp_bytes,
+                     const uint32_t **sorted, hipStream_t s);
+// out_index / out_score [nq, limit]: ranked entries [offset, offset + take[q]).
+hipError_t launch_gather_hits(const uint64_t *keys, const uint32_t *sidx, int nq, int64_t n,
+                              const int64_t *perm, int64_t offset, int64_t limit,
+                              const int64_t *take, int64_t *out_index, double *out_score,
+                              hipStream_t s);
+
 }  // namespace svl

@@ -110,7 +110,9 @@ EXPORTED = [
     "svl_tokenizer_token_id", "svl_tokenizer_token", "svl_tokenizer_vocab_size",
     "svl_tokenizer_max_token_id", "svl_tokenizer_bos_id", "svl_tokenizer_eos_id",
     "svl_tokenizer_unk_id", "svl_tokenizer_pad_id", "svl_tokenizer_is_special_id",
-    "svl_text_embed_texts",
+    "svl_text_embed_texts", "svl_vector_index_create", "svl_vector_index_destroy",
+    "svl_vector_index_size", "svl_vector_index_dimension", "svl_vector_rank",
+    "svl_vector_rank_device",
 ]
 
 _lib = None
