@@ -14,7 +14,10 @@ two row groups on two streams), the roofline of the dominant kernel (the
 gate/up GEMM; its launches timed with HIP events on the stream they run on,
 in a second pass of the same steps on one stream so that each kernel's
 duration is its own), and the CPU oracle timed on this host's cores on a
-bounded sample.
+bounded sample. Secondary legs, each with its own workload string: image
+prompts (vision tower + text encoder), audio prompts (audio tower + text
+encoder, from log-mel frames and from 16 kHz samples through the log-mel
+front end), and exact cosine search over a 1M x 768 index.
 """
 import argparse
 import json
@@ -31,6 +34,7 @@ for p in (ROOT, os.path.join(ROOT, "seldon-vault-lite-rust_amd")):
 METRIC = "text embeddings/sec at batch 64×seq 512 FP32; % FP32-MFMA peak; p50 latency"
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X published dense FP32 matrix peak
 PEAK_HBM_GBS = 8000.0
+PEAK_FP64_TFLOPS = 78.6  # MI355X published FP64 peak
 BATCH, LEN_LO, LEN_HI = 64, 64, 512
 DIMS = [768, 512, 256, 128]
 
@@ -48,6 +52,8 @@ def parse():
                     help="timed batches of the image workload (0 skips it)")
     ap.add_argument("--audio-steps", type=int, default=5,
                     help="timed batches of the audio workload (0 skips it)")
+    ap.add_argument("--search-steps", type=int, default=5,
+                    help="timed batches of the vector-search workload (0 skips it)")
     ap.add_argument("--row-groups", type=int, default=3,
                     help="row groups (streams) the batch is split into")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -148,6 +154,25 @@ def image_leg(text_model, dev, steps):
     embed_ms = timed(embed)
     out = embed()
     assert np.isfinite(out).all()
+
+    # From 16 kHz samples: 4 x 30 s of U(-0.5, 0.5) noise (seed 4) in HBM.
+    # The log-mel front end alone, then samples -> embedding end to end.
+    rng = np.random.default_rng(4)
+    clips = [rng.uniform(-0.5, 0.5, 480000).astype(np.float32) for _ in range(n_clip)]
+    lengths = [c.size for c in clips]
+    samples = torch.from_numpy(np.concatenate(clips)).to("cuda:0")
+    mel_out = torch.empty((n_clip * frames, 128), device="cuda:0")
+    lm = svl_audio.LogMel(dev)
+    mel_ms = timed(lambda: lm.compute_device(samples.data_ptr(), lengths, mel_out.data_ptr()))
+    samples_ms = timed(lambda: emb.embed_samples_device(samples.data_ptr(), lengths, 768))
+    cpu_mel = None
+    if cpu_sample:
+        from oracle import oracle as O
+        a = time.perf_counter()
+        O.log_mel(clips[0])
+        cpu_mel_s = time.perf_counter() - a
+        cpu_mel = {"value": round(1.0 / cpu_mel_s, 3), "unit": "clips/s", "cores": 1,
+                   "kind": "port", "sample": "one 30 s clip through the C oracle log_mel"}
     P, H, I, L, hd, nh = grid * grid, 768, 3072, 16, 64, 12
     per_img = (2 * P * 768 * H + L * (2 * P * H * (3 * nh * hd + H + 3 * I) + 4 * hd * nh * P * P)
                + 2 * (P // 9) * H * 768)
@@ -161,16 +186,26 @@ def image_leg(text_model, dev, steps):
             "tower_tflops": round(flops / (tower_ms * 1e-3) / 1e12, 2),
             "tower_frac_of_fp32_mfma_peak": round(flops / (tower_ms * 1e-3) / 1e12
                                                   / PEAK_FP32_MFMA_TFLOPS, 4),
-            "tower_flops_per_batch": flops, "steps": steps}
+            "tower_flops_per_batch": flops, "steps": steps,
+            "log_mel": {"workload": "batch 4 clips of 30 s of 16 kHz samples in HBM -> "
+                                    "[4 x 2999, 128] log-mel features in HBM (f64 FFT, bit-exact "
+                                    "with the reference)",
+                        "clips_per_s": round(n_clip / (mel_ms * 1e-3), 2),
+                        "p50_ms_per_batch": round(mel_ms, 3),
+                        "frames_per_s": round(n_clip * frames / (mel_ms * 1e-3), 1),
+                        "cpu_baseline": cpu_mel},
+            "from_samples": {"clips_per_s": round(n_clip / (samples_ms * 1e-3), 2),
+                             "p50_ms_per_batch": round(samples_ms, 3)}}
 
 
-def audio_leg(text_model, dev, steps):
+def audio_leg(text_model, dev, steps, cpu_sample=True):
     """Audio workload: batch 4 clips of 30 s (2999 log-mel frames each, all
     valid; 750 audio tokens after subsampling) through the 12-layer audio
     tower (config AU, random-init weights seed 0) and the text encoder
-    (754-token prompts with the audio tokens substituted). The log-mel front
-    end is not part of the GPU path: the frames are synthetic log-mel values
-    U(-7, 2) (seed 3), resident in HBM."""
+    (754-token prompts with the audio tokens substituted), from synthetic
+    log-mel frames U(-7, 2) (seed 3) resident in HBM; then the log-mel front
+    end on 30 s of 16 kHz samples per clip, alone and feeding the same
+    embedding path."""
     import numpy as np
     import torch
 
@@ -227,6 +262,58 @@ def audio_leg(text_model, dev, steps):
             "tower_frac_of_fp32_mfma_peak": round(flops / (tower_ms * 1e-3) / 1e12
                                                   / PEAK_FP32_MFMA_TFLOPS, 4),
             "tower_flops_per_batch": flops, "steps": steps}
+
+
+def search_leg(dev, steps, cpu_sample=True):
+    """Exact cosine search: an index of 1,000,000 chunk embeddings of
+    dimension 768 (U(-1, 1), seed 5; chunk ids 1..n) resident in HBM; a batch
+    of 64 queries (seed 6) ranked in full and sliced to the top 10, and one
+    query alone. Scores are the reference's f64 sequential dot products; the
+    work is 2 * n * 768 FLOP (f64 FMA) per query."""
+    import numpy as np
+    import torch
+
+    import svl_amd
+    import svl_search
+
+    n, d, nq, k = 1_000_000, 768, 64, 10
+    emb = svl_amd.synth_uniform(5, 0, -1.0, 1.0, n * d).reshape(n, d)
+    ids = np.arange(1, n + 1, dtype=np.uint64)
+    ix = svl_search.VectorIndex(emb, ids, dev)
+    qs = svl_amd.synth_uniform(6, 0, -1.0, 1.0, nq * d).reshape(nq, d)
+    dq = torch.from_numpy(qs).to("cuda:0")
+    torch.cuda.synchronize()
+
+    def timed(f, reps):
+        f()
+        ms = []
+        for _ in range(reps):
+            a = time.perf_counter()
+            f()
+            ms.append((time.perf_counter() - a) * 1e3)
+        return float(np.median(ms))
+
+    batch_ms = timed(lambda: ix.rank_device(dq.data_ptr(), nq, d, limit=k), steps)
+    one_ms = timed(lambda: ix.rank_device(dq.data_ptr(), 1, d, limit=k), steps)
+    flops = 2.0 * n * d * nq
+    cpu = None
+    if cpu_sample:
+        from oracle import oracle as O
+        a = time.perf_counter()
+        O.vector_rank(qs[0], emb, ids)
+        cpu_s = time.perf_counter() - a
+        cpu = {"value": round(1.0 / cpu_s, 3), "unit": "queries/s", "cores": 1, "kind": "port",
+               "sample": "one query over the full 1M x 768 index through the C oracle "
+                         "vector_rank (f64 sequential dot products and the full sort)"}
+    del emb
+    return {"workload": "exact cosine ranking, 1,000,000 x 768 f32 chunk embeddings in HBM, "
+                        "64 queries in HBM, full ranking per query sliced to the top 10",
+            "queries_per_s": round(nq / (batch_ms * 1e-3), 1),
+            "p50_ms_per_batch": round(batch_ms, 3),
+            "one_query_p50_ms": round(one_ms, 3),
+            "f64_tflops_wall": round(flops / (batch_ms * 1e-3) / 1e12, 2),
+            "frac_of_fp64_peak_wall": round(flops / (batch_ms * 1e-3) / 1e12 / PEAK_FP64_TFLOPS, 4),
+            "cpu_baseline": cpu, "steps": steps}
 
 
 def main():
@@ -337,7 +424,10 @@ def main():
                 "launches": gu["launches"]}
 
     image = image_leg(model, dev, args.image_steps) if args.image_steps > 0 else None
-    audio = audio_leg(model, dev, args.audio_steps) if args.audio_steps > 0 else None
+    audio = (audio_leg(model, dev, args.audio_steps, args.cpu_sample_rows != 0)
+             if args.audio_steps > 0 else None)
+    search = (search_leg(dev, args.search_steps, args.cpu_sample_rows != 0)
+              if args.search_steps > 0 else None)
     cpu = cpu_baseline(cfg, weights, rows, args.cpu_sample_rows)
 
     breakdown = {k: {"ms_per_step": round(v["ms"] / args.steps, 3),
@@ -369,6 +459,7 @@ def main():
         "kernels": breakdown,
         "image": image,
         "audio": audio,
+        "search": search,
     }
     if cpu:
         line["speedup_vs_cpu_baseline"] = round(value / cpu["value"], 1)

@@ -44,12 +44,15 @@ struct svl_vector_index {
     DevBuf<int64_t> perm;           // chunk-id order -> caller index
     // per-call workspace
     DevBuf<float> Q;
-    DevBuf<double> qnorm;
+    DevBuf<double> qnorm, Qd;
     DevBuf<int> qflags;
     DevBuf<uint8_t> mask;
     DevBuf<uint64_t> keys, keys_alt;
     DevBuf<uint32_t> idx, idx_alt, qkey;
     DevBuf<unsigned char> tmp;
+    DevBuf<uint64_t> samples, samples_alt, cand_key, cand_key_alt;
+    DevBuf<uint32_t> cand_idx, cand_idx_alt;
+    DevBuf<unsigned int> cnt, seg_begin, seg_end, blk_count;
     DevBuf<int64_t> take, out_index;
     DevBuf<double> out_score;
     std::mutex mu;
@@ -57,8 +60,11 @@ struct svl_vector_index {
     ~svl_vector_index() {
         if (device >= 0) (void)hipSetDevice(device);
         V.release(); cnorm.release(); perm.release(); Q.release(); qnorm.release();
-        qflags.release(); mask.release(); keys.release(); keys_alt.release(); idx.release();
+        qflags.release(); Qd.release(); mask.release(); keys.release(); keys_alt.release(); idx.release();
         idx_alt.release(); qkey.release(); tmp.release(); take.release(); out_index.release();
+        samples.release(); samples_alt.release(); cand_key.release(); cand_key_alt.release();
+        cand_idx.release(); cand_idx_alt.release(); cnt.release(); seg_begin.release();
+        seg_end.release(); blk_count.release();
         out_score.release();
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -88,6 +94,73 @@ svl_status check_query(const float *q, int64_t len, int64_t index_dim, bool has_
     if (has_dim && len != index_dim)
         return fail(SVL_USAGE, "query %d: query embedding dimension %lld does not match the index dimension %lld",
                     which, (long long)len, (long long)index_dim);
+    return SVL_OK;
+}
+
+// Pages much smaller than the index (offset + limit <= n / 16): exact top-K
+// by threshold. S = 4096 evenly spaced keys per query are sorted; the sample
+// at a rank with margin above the expected (offset + limit) / n quantile is a
+// threshold, and every admitted key at or below it is a candidate (gathered
+// in position order without atomics). When each
+// query has at least min(offset + limit, admitted) candidates (and no more
+// than the buffer holds), its page lies among them, and sorting only the
+// candidates by (key, position) gives the ranking's exact entries; otherwise
+// `selected` stays false and the full sort runs.
+svl_status select_top(svl_vector_index *ix, int32_t nq, int64_t offset, int64_t limit,
+                      const std::vector<int64_t> &take, const std::vector<int64_t> &pass,
+                      int64_t *out_index, double *out_score, hipStream_t s, bool &selected) {
+    selected = false;
+    const int64_t n = ix->n, K = offset + limit;
+    constexpr int S = 4096;
+    if (n < 16 * S || K > n / 16) return SVL_OK;
+    const int64_t stride = n / S;
+    const double f = (double)K * S / (double)n;
+    const int rank = (int)std::min<double>(S - 1, std::ceil(1.5 * f + 4.0 * std::sqrt(f) + 8.0));
+    const int64_t cap = std::min<int64_t>(n, 2 * (int64_t)(rank + 1) * stride + 4096);
+    if ((int64_t)nq * cap > (int64_t)UINT32_MAX) return SVL_OK;
+    HIP_TRY(ix->samples.ensure((size_t)nq * S));
+    HIP_TRY(ix->samples_alt.ensure((size_t)nq * S));
+    HIP_TRY(ix->cand_key.ensure((size_t)(nq * cap)));
+    HIP_TRY(ix->cand_key_alt.ensure((size_t)(nq * cap)));
+    HIP_TRY(ix->cand_idx.ensure((size_t)(nq * cap)));
+    HIP_TRY(ix->cand_idx_alt.ensure((size_t)(nq * cap)));
+    HIP_TRY(ix->cnt.ensure((size_t)nq));
+    HIP_TRY(ix->seg_begin.ensure((size_t)nq));
+    HIP_TRY(ix->seg_end.ensure((size_t)nq));
+    HIP_TRY(ix->blk_count.ensure((size_t)nq * (size_t)candidate_blocks(n)));
+    size_t a = 0, b = 0;
+    HIP_TRY(sort_samples(ix->samples.p, ix->samples_alt.p, ix->seg_begin.p, ix->seg_end.p, nq, S,
+                         nullptr, &a, s));
+    HIP_TRY(sort_candidates(ix->cand_key.p, ix->cand_idx.p, ix->cand_key_alt.p,
+                            ix->cand_idx_alt.p, ix->cnt.p, ix->seg_begin.p, ix->seg_end.p, nq,
+                            cap, nullptr, &b, s));
+    HIP_TRY(ix->tmp.ensure(std::max<size_t>({a, b, 1})));
+    HIP_TRY(launch_sample_keys(ix->keys.p, nq, n, S, ix->samples.p, s));
+    HIP_TRY(sort_samples(ix->samples.p, ix->samples_alt.p, ix->seg_begin.p, ix->seg_end.p, nq, S,
+                         ix->tmp.p, &a, s));
+    HIP_TRY(launch_compact_keys(ix->keys.p, nq, n, ix->samples_alt.p, S, rank, cap,
+                                ix->blk_count.p, ix->cnt.p, ix->cand_key.p, ix->cand_idx.p, s));
+    std::vector<unsigned int> cnt((size_t)nq);
+    HIP_TRY(hipMemcpyAsync(cnt.data(), ix->cnt.p, (size_t)nq * sizeof(unsigned int),
+                           hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    for (int32_t q = 0; q < nq; ++q) {
+        const int64_t need = std::min(K, pass[(size_t)q]);
+        if ((int64_t)cnt[(size_t)q] < need || (int64_t)cnt[(size_t)q] > cap) return SVL_OK;
+    }
+    HIP_TRY(sort_candidates(ix->cand_key.p, ix->cand_idx.p, ix->cand_key_alt.p,
+                            ix->cand_idx_alt.p, ix->cnt.p, ix->seg_begin.p, ix->seg_end.p, nq,
+                            cap, ix->tmp.p, &b, s));
+    HIP_TRY(launch_gather_candidates(ix->cand_key_alt.p, ix->cand_idx_alt.p, nq, n, cap, ix->perm.p,
+                                     offset, limit, ix->take.p, ix->out_index.p,
+                                     ix->out_score.p, s));
+    HIP_TRY(hipMemcpyAsync(out_index, ix->out_index.p, (size_t)(nq * limit) * 8,
+                           hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipMemcpyAsync(out_score, ix->out_score.p, (size_t)(nq * limit) * 8,
+                           hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    (void)take;
+    selected = true;
     return SVL_OK;
 }
 
@@ -134,8 +207,14 @@ svl_status rank_loaded(svl_vector_index *ix, int32_t nq, const uint8_t *mask, in
         d_mask = ix->mask.p;
         d_stride = mask_stride == 0 ? 0 : n;
     }
+    const int qb = cosine_query_block(nq);
+    HIP_TRY(ix->Qd.ensure((size_t)(ix->D * ((nq + qb - 1) / qb * qb))));
     HIP_TRY(launch_cosine_keys(ix->V.p, ix->cnorm.p, ix->Q.p, ix->qnorm.p, nq, n, (int)ix->D,
-                               d_mask, d_stride, ix->perm.p, ix->keys.p, s));
+                               d_mask, d_stride, ix->perm.p, ix->Qd.p, ix->keys.p, s));
+    HIP_TRY(hipMemcpyAsync(ix->take.p, take.data(), (size_t)nq * 8, hipMemcpyHostToDevice, s));
+    bool selected = false;
+    ST_TRY(select_top(ix, nq, offset, limit, take, pass, out_index, out_score, s, selected));
+    if (selected) return SVL_OK;
     size_t tmp_bytes = 0;
     const uint32_t *sorted = nullptr;
     HIP_TRY(rank_sort(ix->keys.p, ix->keys_alt.p, ix->idx.p, ix->idx_alt.p, ix->qkey.p, nq, n,
@@ -143,7 +222,6 @@ svl_status rank_loaded(svl_vector_index *ix, int32_t nq, const uint8_t *mask, in
     HIP_TRY(ix->tmp.ensure(std::max<size_t>(tmp_bytes, 1)));
     HIP_TRY(rank_sort(ix->keys.p, ix->keys_alt.p, ix->idx.p, ix->idx_alt.p, ix->qkey.p, nq, n,
                       ix->tmp.p, &tmp_bytes, &sorted, s));
-    HIP_TRY(hipMemcpyAsync(ix->take.p, take.data(), (size_t)nq * 8, hipMemcpyHostToDevice, s));
     HIP_TRY(launch_gather_hits(ix->keys.p, sorted, nq, n, ix->perm.p, offset, limit, ix->take.p,
                                ix->out_index.p, ix->out_score.p, s));
     HIP_TRY(hipMemcpyAsync(out_index, ix->out_index.p, (size_t)(nq * limit) * 8,

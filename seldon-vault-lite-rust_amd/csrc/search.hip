@@ -9,16 +9,18 @@
 // computed in the reference's order on the host.
 //
 // Layout: the chunk matrix V [n, D] (rows in ascending chunk-id order) is
-// streamed once per block of QB queries. A workgroup owns 256 chunks (one
-// per lane) and QB queries; each step stages a 256 x 32 slice of V in LDS
-// (padded rows, conflict-free column reads) and the queries' 32 x QB slice
-// as doubles (broadcast reads), then every lane runs 32 x QB FMAs.
+// streamed once per block of QB queries. Each step stages a slice of 32
+// dimensions of the workgroup's chunks in LDS (padded rows, conflict-free
+// column reads); every lane then runs 32 FMAs per query it serves, whose
+// query operands are uniform loads from a d-major double copy of the queries
+// (scalar registers, no LDS traffic).
 //
 // Ranking: scores become 64-bit keys ordered like f64::total_cmp reversed
 // (ascending key = descending score); masked-out chunks get the largest key.
 // A stable device-wide radix sort by key, then a stable sort by query index,
 // yields each query's ranking with ties in ascending chunk-id order.
 #include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/device/device_segmented_radix_sort.hpp>
 
 #include "dev_common.hpp"
 #include "svl_internal.hpp"
@@ -35,49 +37,78 @@ __device__ __forceinline__ uint64_t descending_key(double s) {
     return ~asc;
 }
 
-template <int QB>
+// Queries as doubles, d-major: Qd[d * nq_pad + q] (zero padding), so that a
+// workgroup's QB query values at one d are one uniform (scalar) load.
+__global__ __launch_bounds__(256) void queries_f64_kernel(const float *Q, int nq, int D,
+                                                          int nq_pad, double *Qd) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)D * nq_pad) return;
+    const int d = (int)(i / nq_pad), q = (int)(i % nq_pad);
+    Qd[i] = q < nq ? (double)Q[(int64_t)q * D + d] : 0.0;
+}
+
+// The workgroup's QB queries are split over its waves, QW per wave: wave w
+// serves chunk group w / (QB / QW) (64 chunks, one per lane) and query
+// sub-block w % (QB / QW). A workgroup owns CH = 64 * 4 / (QB / QW) chunks,
+// so HBM traffic stays one pass over V per QB queries while each wave needs
+// only QW query values per step.
+template <int QB, int QW, bool VEC4>
 __global__ __launch_bounds__(256) void cosine_keys_kernel(
-    const float *__restrict__ V, const double *__restrict__ cnorm, const float *__restrict__ Q,
-    const double *__restrict__ qnorm, int nq, int64_t n, int D, const uint8_t *__restrict__ mask,
-    int64_t mask_stride, const int64_t *__restrict__ perm, uint64_t *__restrict__ keys) {
-    __shared__ float vt[SEARCH_CHUNKS][SEARCH_DK + 1];
-    __shared__ double qs[SEARCH_DK][QB];
+    const float *__restrict__ V, const double *__restrict__ cnorm,
+    const double *__restrict__ Qd, int nq_pad, const double *__restrict__ qnorm, int nq,
+    int64_t n, int D, const uint8_t *__restrict__ mask, int64_t mask_stride,
+    const int64_t *__restrict__ perm, uint64_t *__restrict__ keys) {
+    constexpr int SPLIT = QB / QW;
+    constexpr int CH = 64 * 4 / SPLIT;
+    __shared__ float vt[CH][SEARCH_DK + 1];
     const int t = threadIdx.x;
-    const int64_t c0 = (int64_t)blockIdx.x * SEARCH_CHUNKS;
-    const int q0 = blockIdx.y * QB;
-    double acc[QB];
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int lane = t & 63;
+    const int row = (wave / SPLIT) * 64 + lane;
+    const int64_t c0 = (int64_t)blockIdx.x * CH;
+    const int qs = blockIdx.y * QB + (wave % SPLIT) * QW;
+    double acc[QW];
 #pragma unroll
-    for (int j = 0; j < QB; ++j) acc[j] = 0.0;
+    for (int j = 0; j < QW; ++j) acc[j] = 0.0;
     for (int d0 = 0; d0 < D; d0 += SEARCH_DK) {
         const int dk = min(SEARCH_DK, D - d0);
-        // V slice: 256 rows x 32 columns, 16 consecutive threads per two rows
-        for (int i = t; i < SEARCH_CHUNKS * SEARCH_DK; i += 256) {
-            const int r = i / SEARCH_DK, k = i % SEARCH_DK;
-            float v = 0.0f;
-            if (c0 + r < n && k < dk) v = V[(c0 + r) * D + d0 + k];
-            vt[r][k] = v;
-        }
-        for (int i = t; i < SEARCH_DK * QB; i += 256) {
-            const int k = i / QB, j = i % QB;
-            double v = 0.0;
-            if (q0 + j < nq && k < dk) v = (double)Q[(int64_t)(q0 + j) * D + d0 + k];
-            qs[k][j] = v;
+        if (VEC4) {
+            // 8 lanes per row: 128 contiguous bytes of one chunk per 8 lanes
+            for (int i = t; i < CH * (SEARCH_DK / 4); i += 256) {
+                const int r = i / (SEARCH_DK / 4), k = 4 * (i % (SEARCH_DK / 4));
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (c0 + r < n && k < dk)
+                    v = *reinterpret_cast<const float4 *>(V + (c0 + r) * D + d0 + k);
+                vt[r][k] = v.x;
+                vt[r][k + 1] = v.y;
+                vt[r][k + 2] = v.z;
+                vt[r][k + 3] = v.w;
+            }
+        } else {
+            for (int i = t; i < CH * SEARCH_DK; i += 256) {
+                const int r = i / SEARCH_DK, k = i % SEARCH_DK;
+                float v = 0.0f;
+                if (c0 + r < n && k < dk) v = V[(c0 + r) * D + d0 + k];
+                vt[r][k] = v;
+            }
         }
         __syncthreads();
+        const double *qrow = Qd + (int64_t)d0 * nq_pad + qs;
         for (int k = 0; k < dk; ++k) {
-            const double v = (double)vt[t][k];
+            const double v = (double)vt[row][k];
+            const double *qk = qrow + (int64_t)k * nq_pad;
 #pragma unroll
-            for (int j = 0; j < QB; ++j) acc[j] = fma(qs[k][j], v, acc[j]);
+            for (int j = 0; j < QW; ++j) acc[j] = fma(qk[j], v, acc[j]);
         }
         __syncthreads();
     }
-    const int64_t c = c0 + t;
+    const int64_t c = c0 + row;
     if (c >= n) return;
     const double cn = cnorm[c];
     const int64_t orig = mask ? perm[c] : 0;
 #pragma unroll
-    for (int j = 0; j < QB; ++j) {
-        const int q = q0 + j;
+    for (int j = 0; j < QW; ++j) {
+        const int q = qs + j;
         if (q >= nq) break;
         uint64_t key = ~0ull;
         if (!mask || mask[(int64_t)q * mask_stride + orig])
@@ -86,15 +117,20 @@ __global__ __launch_bounds__(256) void cosine_keys_kernel(
     }
 }
 
-// One lane per query: the squared norm in d order (vector.rs:33-40).
-__global__ __launch_bounds__(64) void query_norm_kernel(const float *Q, int nq, int D,
-                                                        double *qnorm, int *flags) {
-    const int q = blockIdx.x * 64 + threadIdx.x;
+// One workgroup per query: the row is staged in LDS with coalesced loads,
+// then one lane accumulates the squared norm in d order (vector.rs:33-40).
+__global__ __launch_bounds__(256) void query_norm_kernel(const float *Q, int nq, int D,
+                                                         double *qnorm, int *flags) {
+    __shared__ float row[8192];
+    const int q = blockIdx.x;
     if (q >= nq) return;
+    for (int d = threadIdx.x; d < D; d += 256) row[d] = Q[(int64_t)q * D + d];
+    __syncthreads();
+    if (threadIdx.x != 0) return;
     double sum = 0.0;
     int f = 0;
     for (int d = 0; d < D; ++d) {
-        const float v = Q[(int64_t)q * D + d];
+        const float v = row[d];
         if (!isfinite(v)) f |= 1;
         sum = fma((double)v, (double)v, sum);
     }
@@ -106,8 +142,9 @@ __global__ __launch_bounds__(64) void query_norm_kernel(const float *Q, int nq, 
 hipError_t launch_query_norms(const float *Q, int nq, int D, double *qnorm, int *flags,
                               hipStream_t s) {
     if (nq <= 0) return hipSuccess;
-    hipLaunchKernelGGL(query_norm_kernel, dim3((unsigned)((nq + 63) / 64)), dim3(64), 0, s, Q, nq,
-                       D, qnorm, flags);
+    if (D > 8192) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(query_norm_kernel, dim3((unsigned)nq), dim3(256), 0, s, Q, nq, D, qnorm,
+                       flags);
     return hipGetLastError();
 }
 
@@ -140,22 +177,42 @@ __global__ __launch_bounds__(256) void gather_hits_kernel(const uint64_t *keys,
     out_score[(int64_t)q * limit + i] = __longlong_as_double((long long)b);
 }
 
+int cosine_query_block(int nq) {
+    return nq == 1 ? 1 : nq <= 4 ? 4 : nq <= 8 ? 8 : nq <= 16 ? 16 : 32;
+}
+
 hipError_t launch_cosine_keys(const float *V, const double *cnorm, const float *Q,
                               const double *qnorm, int nq, int64_t n, int D, const uint8_t *mask,
-                              int64_t mask_stride, const int64_t *perm, uint64_t *keys,
-                              hipStream_t s) {
+                              int64_t mask_stride, const int64_t *perm, double *Qd,
+                              uint64_t *keys, hipStream_t s) {
     if (nq <= 0 || n <= 0) return hipSuccess;
     if (D <= 0) return hipErrorInvalidValue;
-    const unsigned gx = (unsigned)((n + SEARCH_CHUNKS - 1) / SEARCH_CHUNKS);
-#define COS_LAUNCH(QB)                                                                        \
-    hipLaunchKernelGGL(cosine_keys_kernel<QB>, dim3(gx, (unsigned)((nq + QB - 1) / QB)),   \
-                       dim3(256), 0, s, V, cnorm, Q, qnorm, nq, n, D, mask, mask_stride, perm, \
-                       keys)
-    if (nq == 1) COS_LAUNCH(1);
-    else if (nq <= 4) COS_LAUNCH(4);
-    else if (nq <= 8) COS_LAUNCH(8);
-    else if (nq <= 16) COS_LAUNCH(16);
-    else COS_LAUNCH(32);
+    const int qb = cosine_query_block(nq);
+    const int nq_pad = (nq + qb - 1) / qb * qb;
+    const int64_t total = (int64_t)D * nq_pad;
+    hipLaunchKernelGGL(queries_f64_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       Q, nq, D, nq_pad, Qd);
+    const bool vec4 = D % 4 == 0;
+#define COS_LAUNCH(QB, QW)                                                                     \
+    do {                                                                                      \
+        constexpr int CH = 64 * 4 / (QB / QW);                                                \
+        const dim3 grid((unsigned)((n + CH - 1) / CH), (unsigned)(nq_pad / QB));              \
+        if (vec4)                                                                             \
+            hipLaunchKernelGGL((cosine_keys_kernel<QB, QW, true>), grid, dim3(256), 0, s, V, \
+                               cnorm, Qd, nq_pad, qnorm, nq, n, D, mask, mask_stride, perm,   \
+                               keys);                                                         \
+        else                                                                                  \
+            hipLaunchKernelGGL((cosine_keys_kernel<QB, QW, false>), grid, dim3(256), 0, s,   \
+                               V, cnorm, Qd, nq_pad, qnorm, nq, n, D, mask, mask_stride,      \
+                               perm, keys);                                                   \
+    } while (0)
+    switch (qb) {
+        case 1: COS_LAUNCH(1, 1); break;
+        case 4: COS_LAUNCH(4, 4); break;
+        case 8: COS_LAUNCH(8, 8); break;
+        case 16: COS_LAUNCH(16, 8); break;
+        default: COS_LAUNCH(32, 8); break;
+    }
 #undef COS_LAUNCH
     return hipGetLastError();
 }
@@ -192,6 +249,194 @@ hipError_t rank_sort(const uint64_t *keys, uint64_t *keys_alt, uint32_t *idx, ui
                                   0, qbits, s);
     *sorted = idx;
     return e;
+}
+
+// ---- top-K selection (offset + limit much smaller than the index) ---------------
+// Every stride-th key of each query, S of them: samples[q * S + i].
+__global__ __launch_bounds__(256) void sample_keys_kernel(const uint64_t *keys, int nq, int64_t n,
+                                                          int S, int64_t stride,
+                                                          uint64_t *samples) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int q = blockIdx.y;
+    if (i < S && q < nq) samples[(int64_t)q * S + i] = keys[(int64_t)q * n + (int64_t)i * stride];
+}
+
+// Candidates of query q: every admitted key <= sorted sample `rank`, in
+// position order. Pass 1 counts them per block of COMPACT_ITEMS keys; a
+// per-query scan gives each block its offset (and cnt[q] the total); pass 2
+// writes them at cand[q * cap + offset], keeping the first cap.
+constexpr int COMPACT_ITEMS = 4096;  // keys per block: 256 lanes x 16
+
+__device__ __forceinline__ bool is_candidate(uint64_t k, uint64_t thresh) {
+    return k != ~0ull && k <= thresh;
+}
+
+__global__ __launch_bounds__(256) void count_candidates_kernel(const uint64_t *keys, int64_t n,
+                                                               const uint64_t *sorted_samples,
+                                                               int S, int rank, int nblk,
+                                                               unsigned int *blk_count) {
+    __shared__ unsigned int wave_total[4];
+    const int q = blockIdx.y;
+    const uint64_t thresh = sorted_samples[(int64_t)q * S + rank];
+    const int64_t base = (int64_t)blockIdx.x * COMPACT_ITEMS;
+    unsigned int c = 0;
+    for (int i = threadIdx.x; i < COMPACT_ITEMS; i += 256) {
+        const int64_t pos = base + i;
+        if (pos < n && is_candidate(keys[(int64_t)q * n + pos], thresh)) ++c;
+    }
+    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+    if ((threadIdx.x & 63) == 0) wave_total[threadIdx.x >> 6] = c;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        blk_count[(int64_t)q * nblk + blockIdx.x] =
+            wave_total[0] + wave_total[1] + wave_total[2] + wave_total[3];
+}
+
+// One lane per query: exclusive scan of its block counts (in place) and the
+// total.
+__global__ __launch_bounds__(64) void scan_candidates_kernel(unsigned int *blk_count, int nq,
+                                                             int nblk, unsigned int *cnt) {
+    const int q = blockIdx.x * 64 + threadIdx.x;
+    if (q >= nq) return;
+    unsigned int run = 0;
+    for (int b = 0; b < nblk; ++b) {
+        const unsigned int c = blk_count[(int64_t)q * nblk + b];
+        blk_count[(int64_t)q * nblk + b] = run;
+        run += c;
+    }
+    cnt[q] = run;
+}
+
+__global__ __launch_bounds__(256) void write_candidates_kernel(
+    const uint64_t *keys, int64_t n, const uint64_t *sorted_samples, int S, int rank, int nblk,
+    const unsigned int *blk_offset, int64_t cap, uint64_t *cand_key, uint32_t *cand_idx) {
+    __shared__ unsigned int wave_count[4];
+    const int q = blockIdx.y;
+    const uint64_t thresh = sorted_samples[(int64_t)q * S + rank];
+    const int64_t base = (int64_t)blockIdx.x * COMPACT_ITEMS;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    unsigned int offset = blk_offset[(int64_t)q * nblk + blockIdx.x];
+    // rounds of 256 consecutive keys, in position order within the block
+    for (int r = 0; r < COMPACT_ITEMS; r += 256) {
+        const int64_t pos = base + r + threadIdx.x;
+        uint64_t k = 0;
+        const bool hit = pos < n && is_candidate(k = keys[(int64_t)q * n + pos], thresh);
+        const uint64_t ballot = __ballot(hit);
+        if (lane == 0) wave_count[wave] = (unsigned int)__popcll(ballot);
+        __syncthreads();
+        unsigned int before = 0;
+        for (int w = 0; w < wave; ++w) before += wave_count[w];
+        const unsigned int below = (unsigned int)__popcll(ballot & ((1ull << lane) - 1));
+        if (hit) {
+            const int64_t slot = (int64_t)offset + before + below;
+            if (slot < cap) {
+                cand_key[(int64_t)q * cap + slot] = k;
+                cand_idx[(int64_t)q * cap + slot] = (uint32_t)((int64_t)q * n + pos);
+            }
+        }
+        offset += wave_count[0] + wave_count[1] + wave_count[2] + wave_count[3];
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void segment_bounds_kernel(const unsigned int *cnt, int nq,
+                                                             int64_t cap, unsigned int *begin,
+                                                             unsigned int *end) {
+    const int q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= nq) return;
+    begin[q] = (unsigned int)(q * cap);
+    end[q] = (unsigned int)(q * cap + min((int64_t)cnt[q], cap));
+}
+
+hipError_t launch_sample_keys(const uint64_t *keys, int nq, int64_t n, int S, uint64_t *samples,
+                              hipStream_t s) {
+    hipLaunchKernelGGL(sample_keys_kernel, dim3((unsigned)((S + 255) / 256), (unsigned)nq),
+                       dim3(256), 0, s, keys, nq, n, S, n / S, samples);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void uniform_bounds_kernel(int nq, int S, unsigned int *begin,
+                                                             unsigned int *end) {
+    const int q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= nq) return;
+    begin[q] = (unsigned int)(q * S);
+    end[q] = (unsigned int)((q + 1) * S);
+}
+
+hipError_t sort_samples(uint64_t *samples, uint64_t *samples_alt, unsigned int *begin,
+                        unsigned int *end, int nq, int S, void *tmp, size_t *tmp_bytes,
+                        hipStream_t s) {
+    if (tmp)
+        hipLaunchKernelGGL(uniform_bounds_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256),
+                           0, s, nq, S, begin, end);
+    return rocprim::segmented_radix_sort_keys(tmp, *tmp_bytes, samples, samples_alt,
+                                              (unsigned int)(nq * S), (unsigned int)nq, begin,
+                                              end, 0, 64, s);
+}
+
+int candidate_blocks(int64_t n) { return (int)((n + COMPACT_ITEMS - 1) / COMPACT_ITEMS); }
+
+hipError_t launch_compact_keys(const uint64_t *keys, int nq, int64_t n,
+                               const uint64_t *sorted_samples, int S, int rank, int64_t cap,
+                               unsigned int *blk_count, unsigned int *cnt, uint64_t *cand_key,
+                               uint32_t *cand_idx, hipStream_t s) {
+    const int nblk = candidate_blocks(n);
+    const dim3 grid((unsigned)nblk, (unsigned)nq);
+    hipLaunchKernelGGL(count_candidates_kernel, grid, dim3(256), 0, s, keys, n, sorted_samples, S,
+                       rank, nblk, blk_count);
+    hipLaunchKernelGGL(scan_candidates_kernel, dim3((unsigned)((nq + 63) / 64)), dim3(64), 0, s,
+                       blk_count, nq, nblk, cnt);
+    hipLaunchKernelGGL(write_candidates_kernel, grid, dim3(256), 0, s, keys, n, sorted_samples, S,
+                       rank, nblk, blk_count, cap, cand_key, cand_idx);
+    return hipGetLastError();
+}
+
+// Candidates of each query in (key, position) order: they are written in
+// position order, so one stable segmented sort by key suffices. Results in
+// key_alt / idx_alt.
+hipError_t sort_candidates(const uint64_t *cand_key, const uint32_t *cand_idx, uint64_t *key_alt,
+                           uint32_t *idx_alt, const unsigned int *cnt, unsigned int *begin,
+                           unsigned int *end, int nq, int64_t cap, void *tmp, size_t *tmp_bytes,
+                           hipStream_t s) {
+    const unsigned int total = (unsigned int)(nq * cap);
+    if (tmp)
+        hipLaunchKernelGGL(segment_bounds_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256),
+                           0, s, cnt, nq, cap, begin, end);
+    return rocprim::segmented_radix_sort_pairs(tmp, *tmp_bytes, cand_key, key_alt, cand_idx,
+                                               idx_alt, total, (unsigned int)nq, begin, end, 0, 64,
+                                               s);
+}
+
+// Hits from the sorted candidates: entries [offset, offset + take[q]) of
+// segment q.
+__global__ __launch_bounds__(256) void gather_candidates_kernel(const uint64_t *cand_key,
+                                                                const uint32_t *cand_idx, int nq,
+                                                                int64_t n, int64_t cap,
+                                                                const int64_t *perm,
+                                                                int64_t offset, int64_t limit,
+                                                                const int64_t *take,
+                                                                int64_t *out_index,
+                                                                double *out_score) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int q = blockIdx.y;
+    if (q >= nq || i >= take[q]) return;
+    const int64_t src = (int64_t)q * cap + offset + i;
+    const uint64_t asc = ~cand_key[src];
+    const uint64_t b = (asc >> 63) ? (asc & 0x7FFFFFFFFFFFFFFFull) : ~asc;
+    out_index[(int64_t)q * limit + i] = perm[cand_idx[src] % (uint64_t)n];
+    out_score[(int64_t)q * limit + i] = __longlong_as_double((long long)b);
+}
+
+hipError_t launch_gather_candidates(const uint64_t *cand_key, const uint32_t *cand_idx, int nq,
+                                    int64_t n, int64_t cap, const int64_t *perm, int64_t offset,
+                                    int64_t limit, const int64_t *take, int64_t *out_index,
+                                    double *out_score, hipStream_t s) {
+    if (nq <= 0 || limit <= 0) return hipSuccess;
+    hipLaunchKernelGGL(gather_candidates_kernel,
+                       dim3((unsigned)((limit + 255) / 256), (unsigned)nq), dim3(256), 0, s,
+                       cand_key, cand_idx, nq, n, cap, perm, offset, limit, take, out_index,
+                       out_score);
+    return hipGetLastError();
 }
 
 hipError_t launch_gather_hits(const uint64_t *keys, const uint32_t *sidx, int nq, int64_t n,

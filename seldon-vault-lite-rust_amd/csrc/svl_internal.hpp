@@ -229,10 +229,12 @@ hipError_t launch_log_mel(const float *x, const MelClip *clips, int n_clips, int
 // keys[q, c] = descending total-order key of dot(Q[q], V[c]) / (qnorm[q] *
 // cnorm[c]) accumulated in double in d order; all ones when mask (indexed
 // mask[q * mask_stride + perm[c]]) is given and zero.
+// Qd: scratch of D * round_up(nq, cosine_query_block(nq)) doubles.
+int cosine_query_block(int nq);
 hipError_t launch_cosine_keys(const float *V, const double *cnorm, const float *Q,
                               const double *qnorm, int nq, int64_t n, int D, const uint8_t *mask,
-                              int64_t mask_stride, const int64_t *perm, uint64_t *keys,
-                              hipStream_t s);
+                              int64_t mask_stride, const int64_t *perm, double *Qd,
+                              uint64_t *keys, hipStream_t s);
 // qnorm[q] = sqrt(sum Q[q, d]^2) in d order; flag bit 1: a non-finite value,
 // bit 2: a zero or non-finite norm (per query: flags[q]).
 hipError_t launch_query_norms(const float *Q, int nq, int D, double *qnorm, int *flags,
@@ -243,6 +245,31 @@ hipError_t launch_query_norms(const float *Q, int nq, int D, double *qnorm, int 
 hipError_t rank_sort(const uint64_t *keys, uint64_t *keys_alt, uint32_t *idx, uint32_t *idx_alt,
                      uint32_t *qkey, int nq, int64_t n, void *tmp, size_t *tmp_bytes,
                      const uint32_t **sorted, hipStream_t s);
+// Top-K selection for pages far smaller than the index: S samples per query
+// (every (n / S)-th key), sorted per query; candidates are the admitted keys
+// <= sorted sample `rank`, in position order (at most cap stored per query,
+// cnt[q] counts all); the candidates sorted by (key, position); and the page
+// gathered.
+hipError_t launch_sample_keys(const uint64_t *keys, int nq, int64_t n, int S, uint64_t *samples,
+                              hipStream_t s);
+hipError_t sort_samples(uint64_t *samples, uint64_t *samples_alt, unsigned int *begin,
+                        unsigned int *end, int nq, int S, void *tmp, size_t *tmp_bytes,
+                        hipStream_t s);
+// blk_count: candidate_blocks(n) * nq counters.
+int candidate_blocks(int64_t n);
+hipError_t launch_compact_keys(const uint64_t *keys, int nq, int64_t n,
+                               const uint64_t *sorted_samples, int S, int rank, int64_t cap,
+                               unsigned int *blk_count, unsigned int *cnt, uint64_t *cand_key,
+                               uint32_t *cand_idx, hipStream_t s);
+// Stable sort of each query's candidates by key into key_alt / idx_alt.
+hipError_t sort_candidates(const uint64_t *cand_key, const uint32_t *cand_idx, uint64_t *key_alt,
+                           uint32_t *idx_alt, const unsigned int *cnt, unsigned int *begin,
+                           unsigned int *end, int nq, int64_t cap, void *tmp, size_t *tmp_bytes,
+                           hipStream_t s);
+hipError_t launch_gather_candidates(const uint64_t *cand_key, const uint32_t *cand_idx, int nq,
+                                    int64_t n, int64_t cap, const int64_t *perm, int64_t offset,
+                                    int64_t limit, const int64_t *take, int64_t *out_index,
+                                    double *out_score, hipStream_t s);
 // out_index / out_score [nq, limit]: ranked entries [offset, offset + take[q]).
 hipError_t launch_gather_hits(const uint64_t *keys, const uint32_t *sidx, int nq, int64_t n,
                               const int64_t *perm, int64_t offset, int64_t limit,

@@ -124,3 +124,25 @@ def test_error_taxonomy():
     with pytest.raises(S.SvlError) as e:       # SearchRequest::validate
         ix.search(np.array([1.0, 0.0], np.float32), limit=0)
     assert e.value.kind == "Usage"
+
+
+def test_top_k_selection_path():
+    """Pages far smaller than the index take the threshold selection; ties
+    at the top (400 identical chunks), sparse filters and a query with fewer
+    admitted chunks than the page must still give the exact ranking."""
+    n, d = 80_000, 64
+    emb, ids = corpus(n, d, seed=21, ties=False)
+    emb[1000:1400] = emb[7]
+    ix = V.VectorIndex(emb, ids)
+    rng = np.random.default_rng(22)
+    qs = rng.standard_normal((6, d)).astype(np.float32)
+    qs[1] = emb[7]
+    masks = np.ones((6, n), np.uint8)
+    masks[2] = rng.random(n) > 0.97
+    masks[3] = 0
+    masks[3, rng.choice(n, 5, replace=False)] = 1          # 5 admitted < page
+    for offset, limit in ((0, 10), (3, 50), (100, 1000)):
+        got = ix.rank(qs, masks=masks, offset=offset, limit=limit)
+        for q in range(6):
+            check_query(ix, emb, ids, qs[q], got[q], mask=masks[q], offset=offset, limit=limit,
+                        label=f"query {q} page ({offset}, {limit})")
