@@ -11,9 +11,9 @@
 //    block built from v_mfma_f32_32x32x2_f32 tiles (32 FMA/clk/SIMD, the FP32
 //    matrix peak).
 //  * K advances in BK-wide slices that go straight from HBM/L2 into LDS with
-//    buffer_load_dwordx4 ... lds (no register staging), double buffered: the
-//    DMA of slice k+1 is in flight while the MFMAs consume slice k, with one
-//    barrier per slice. Buffer resources bound each operand to its valid
+//    buffer_load_dwordx4 ... lds (no register staging) through 2-4 LDS
+//    stages: the DMAs of the next slices are in flight while the MFMAs
+//    consume slice k, with one barrier per slice. Buffer resources bound each operand to its valid
 //    rows, so the ragged M tail (and N tail) reads zeros without branches.
 //  * LDS rows are unpadded; 16-byte chunks are XOR-swizzled by row
 //    (chunk ^ (row / rows_per_bank_line) % chunks_per_row) on the way in, so
@@ -226,8 +226,9 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Direct-to-LDS variant; requires K % BK == 0 and 16-byte aligned rows.
-template <int BM, int BN, int BK, int EPI, int MINB>
+// Direct-to-LDS variant; requires K % BK == 0 and 16-byte aligned rows. NS
+// LDS stages: NS - 1 slices are in flight while one is consumed.
+template <int BM, int BN, int BK, int EPI, int MINB, int NS>
 __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m, int tiles_n) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int TM = BM / 64, TN = BN / 64;   // 32x32 tiles per wave
@@ -238,8 +239,9 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     constexpr int W_CH = BN / RPK / 4;
     static_assert(BM % 64 == 0 && BN % 64 == 0 && A_CH >= 1 && W_CH >= 1, "tile shape");
     static_assert(!paired_epi<EPI>() || TN % 2 == 0, "paired epilogues take 32-column tile pairs");
-    __shared__ float As[2][BM * BK];
-    __shared__ float Ws[2][BN * BK];
+    static_assert(NS >= 2 && (NS - 2) * (A_CH + W_CH) < 64, "pipeline depth");
+    __shared__ float As[NS][BM * BK];
+    __shared__ float Ws[NS][BN * BK];
 
     const int ntiles = tiles_m * tiles_n;
     const int bid = blockIdx.x;
@@ -303,12 +305,17 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
 
     const int sw = (l32 / RPL) % CPR;
     const int nk = p.K / BK;
-    issue(0, 0);
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st)
+        if (st < nk) issue(st, st * BK);
     for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        wait_vmcnt<0>();   // this wave's DMA of slice kt has landed
+        const int cur = kt % NS;
+        // this wave's DMA of slice kt has landed: only the NS - 2 later
+        // slices (A_CH + W_CH instructions each) may still be in flight
+        if (kt + NS - 2 < nk) wait_vmcnt<(NS - 2) * (A_CH + W_CH)>();
+        else wait_vmcnt<0>();
         __syncthreads();   // ... and every wave's; slice kt-1 is no longer read
-        if (kt + 1 < nk) issue(cur ^ 1, (kt + 1) * BK);
+        if (kt + NS - 1 < nk) issue((kt + NS - 1) % NS, (kt + NS - 1) * BK);
         const float *as = &As[cur][(wm * (BM / 2) + l32) * BK];
         const float *ws = &Ws[cur][(wn * (BN / 2) + l32) * BK];
 #pragma unroll
@@ -386,11 +393,11 @@ __global__ __launch_bounds__(256) void gemm_nt_simple(GemmArgs p) {
     }
 }
 
-template <int BM, int BN, int BK, int EPI, int MINB>
+template <int BM, int BN, int BK, int EPI, int MINB, int NS>
 static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
     const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
-    hipLaunchKernelGGL((gemm_nt_dma<BM, BN, BK, EPI, MINB>), dim3(tm * tn), dim3(256), 0, s, a, tm,
-                       tn);
+    hipLaunchKernelGGL((gemm_nt_dma<BM, BN, BK, EPI, MINB, NS>), dim3(tm * tn), dim3(256), 0, s, a,
+                       tm, tn);
     return hipGetLastError();
 }
 
@@ -406,19 +413,44 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 //    path's row groups): measured best is 64x64 for N <= 256, 128x64 below
 //    1024 tiles of 128x128, else 128x128; the other streams' work fills the
 //    partial rounds that the cost model above optimises for.
-//  * Paired epilogues need 32-column tile pairs, so they always take 128x128.
+//  * Paired epilogues need 32-column tile pairs: 128x128, or 64x128 when the
+//    grid of 128x128 tiles would not cover the GPU once.
+//  * Stages: grids of at least two workgroups per CU keep two stages (their
+//    co-resident workgroups hide each other's DMA latency, and a deeper
+//    pipeline measured slower there); short grids, whose few workgroups run
+//    the K loop alone, take as many stages as the LDS budget allows.
+//    Grids that do not fill the GPU once (fewer tiles than CUs) also take
+//    64-wide K slices, so each barrier is amortised over four times more
+//    MFMAs (the k order, set by the 8-k steps, is the same for any slice
+//    width).
+template <int BM, int BN, int BK, int EPI, int MINB, int NS_DEEP>
+static hipError_t launch_dma_staged(const GemmArgs &a, hipStream_t s) {
+    // workgroups per CU that the deep pipeline's LDS allows (160 KB per CU)
+    constexpr int FIT = 160 * 1024 / (NS_DEEP * (BM + BN) * BK * 4);
+    constexpr int MINB_DEEP = FIT < MINB ? FIT : MINB;
+    const int64_t t = (int64_t)((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    if constexpr (BM * BN <= 64 * 128)
+        if (t < 256 && a.K % 64 == 0) return launch_dma<BM, BN, 64, EPI, 1, 3>(a, s);
+    if (t < 2 * 256) return launch_dma<BM, BN, BK, EPI, MINB_DEEP, NS_DEEP>(a, s);
+    return launch_dma<BM, BN, BK, EPI, MINB, 2>(a, s);
+}
+
 template <int EPI>
 static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
+    auto tiles = [&](int bm, int bn) {
+        return (int64_t)((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn);
+    };
     if constexpr (paired_epi<EPI>()) {
-        return launch_dma<128, 128, 16, EPI, 3>(a, s);
+        if (tiles(128, 128) < 256) {
+            if (tiles(64, 128) < 256 && a.K % 64 == 0) return launch_dma<64, 128, 64, EPI, 1, 3>(a, s);
+            return launch_dma<64, 128, 16, EPI, 3, 4>(a, s);
+        }
+        return launch_dma_staged<128, 128, 16, EPI, 3, 3>(a, s);
     } else {
-        auto tiles = [&](int bm, int bn) {
-            return (int64_t)((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn);
-        };
         if (a.cus > 0) {
-            if (a.N <= 256 && a.K % 32 == 0) return launch_dma<64, 64, 32, EPI, 4>(a, s);
-            if (tiles(128, 128) < 4 * 256) return launch_dma<128, 64, 16, EPI, 4>(a, s);
-            return launch_dma<128, 128, 16, EPI, 3>(a, s);
+            if (a.N <= 256 && a.K % 32 == 0) return launch_dma<64, 64, 32, EPI, 4, 2>(a, s);
+            if (tiles(128, 128) < 4 * 256) return launch_dma_staged<128, 64, 16, EPI, 4, 3>(a, s);
+            return launch_dma_staged<128, 128, 16, EPI, 3, 3>(a, s);
         }
         auto per_cu = [&](int bm, int bn) { return (double)((tiles(bm, bn) + 255) / 256); };
         const double c128 = per_cu(128, 128) * (128.0 * 128.0);
@@ -426,11 +458,11 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
         const double c64 = per_cu(64, 64) * (64.0 * 64.0) / 0.90;
         if (c64 < c128 && c64 < c12864) {
             if (a.K % 32 == 0 && (a.K >= 1024 || a.N <= 256))
-                return launch_dma<64, 64, 32, EPI, 4>(a, s);
-            return launch_dma<64, 64, 16, EPI, 4>(a, s);
+                return launch_dma_staged<64, 64, 32, EPI, 4, 3>(a, s);
+            return launch_dma_staged<64, 64, 16, EPI, 4, 4>(a, s);
         }
-        if (c12864 < c128) return launch_dma<128, 64, 16, EPI, 4>(a, s);
-        return launch_dma<128, 128, 16, EPI, 3>(a, s);
+        if (c12864 < c128) return launch_dma_staged<128, 64, 16, EPI, 4, 3>(a, s);
+        return launch_dma_staged<128, 128, 16, EPI, 3, 3>(a, s);
     }
 }
 
