@@ -33,6 +33,7 @@
 //  * Epilogues fuse the elementwise op that follows each projection in
 //    text.rs (PLE scale, GeGLU, GELU-gate x per-layer input).
 #include <algorithm>
+#include <type_traits>
 
 #include "dev_common.hpp"
 #include "svl_internal.hpp"
@@ -239,9 +240,26 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     constexpr int W_CH = BN / RPK / 4;
     static_assert(BM % 64 == 0 && BN % 64 == 0 && A_CH >= 1 && W_CH >= 1, "tile shape");
     static_assert(!paired_epi<EPI>() || TN % 2 == 0, "paired epilogues take 32-column tile pairs");
-    static_assert(NS >= 2 && (NS - 2) * (A_CH + W_CH) < 64, "pipeline depth");
-    __shared__ float As[NS][BM * BK];
-    __shared__ float Ws[NS][BN * BK];
+    static_assert(NS >= 2 && NS <= 4 && (NS - 2) * (A_CH + W_CH) < 64, "pipeline depth");
+    // One LDS object per stage, addressed with compile-time stage indices, so
+    // the compiler can see that the DMA filling one stage never aliases the
+    // fragment reads of another and need not drain the DMA before reading.
+    __shared__ float As0[BM * BK], As1[BM * BK], As2[NS > 2 ? BM * BK : 4], As3[NS > 3 ? BM * BK : 4];
+    __shared__ float Ws0[BN * BK], Ws1[BN * BK], Ws2[NS > 2 ? BN * BK : 4], Ws3[NS > 3 ? BN * BK : 4];
+    auto stage_a = [&](auto st) -> float * {
+        constexpr int i = decltype(st)::value;
+        if constexpr (i == 0) return As0;
+        else if constexpr (i == 1) return As1;
+        else if constexpr (i == 2) return As2;
+        else return As3;
+    };
+    auto stage_w = [&](auto st) -> float * {
+        constexpr int i = decltype(st)::value;
+        if constexpr (i == 0) return Ws0;
+        else if constexpr (i == 1) return Ws1;
+        else if constexpr (i == 2) return Ws2;
+        else return Ws3;
+    };
 
     const int ntiles = tiles_m * tiles_n;
     const int bid = blockIdx.x;
@@ -282,16 +300,18 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
         const int c = (lane % CPR) ^ ((row / RPL) % CPR);
         w_off[q] = (row * (int)p.ldw + 4 * c) * 4;
     }
-    auto issue = [&](int buf, int k0) {
+    auto issue = [&](auto st, int k0) {
+        float *as = stage_a(st);
+        float *ws = stage_w(st);
 #pragma unroll
         for (int q = 0; q < A_CH; ++q)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ra, (__attribute__((address_space(3))) void *)&As[buf][(wave * A_CH + q) * 256], 16,
+                ra, (__attribute__((address_space(3))) void *)&as[(wave * A_CH + q) * 256], 16,
                 a_off[q], k0 * 4, 0, 0);
 #pragma unroll
         for (int q = 0; q < W_CH; ++q)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rw, (__attribute__((address_space(3))) void *)&Ws[buf][(wave * W_CH + q) * 256], 16,
+                rw, (__attribute__((address_space(3))) void *)&ws[(wave * W_CH + q) * 256], 16,
                 w_off[q], k0 * 4, 0, 0);
     };
 
@@ -305,19 +325,26 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
 
     const int sw = (l32 / RPL) % CPR;
     const int nk = p.K / BK;
-#pragma unroll
-    for (int st = 0; st < NS - 1; ++st)
-        if (st < nk) issue(st, st * BK);
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt % NS;
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+    if (0 < nk) issue(S0{}, 0);
+    if constexpr (NS > 2) if (1 < nk) issue(S1{}, BK);
+    if constexpr (NS > 3) if (2 < nk) issue(S2{}, 2 * BK);
+    // slice kt lives in stage kt % NS; the loop below is unrolled NS times so
+    // every stage index is a constant
+    auto step = [&](int kt, auto st) {
+        constexpr int cur = decltype(st)::value;
         // this wave's DMA of slice kt has landed: only the NS - 2 later
         // slices (A_CH + W_CH instructions each) may still be in flight
         if (kt + NS - 2 < nk) wait_vmcnt<(NS - 2) * (A_CH + W_CH)>();
         else wait_vmcnt<0>();
         __syncthreads();   // ... and every wave's; slice kt-1 is no longer read
-        if (kt + NS - 1 < nk) issue((kt + NS - 1) % NS, (kt + NS - 1) * BK);
-        const float *as = &As[cur][(wm * (BM / 2) + l32) * BK];
-        const float *ws = &Ws[cur][(wn * (BN / 2) + l32) * BK];
+        if (kt + NS - 1 < nk)
+            issue(std::integral_constant<int, (cur + NS - 1) % NS>{}, (kt + NS - 1) * BK);
+        const float *as = stage_a(st) + (wm * (BM / 2) + l32) * BK;
+        const float *ws = stage_w(st) + (wn * (BN / 2) + l32) * BK;
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 8) {
             const int pos = ((kk >> 2) + hh) ^ sw;
@@ -338,6 +365,12 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
                                                                          acc[i][j], 0, 0, 0);
         }
+    };
+    for (int kt = 0; kt < nk; kt += NS) {
+        step(kt, S0{});
+        if (kt + 1 < nk) step(kt + 1, S1{});
+        if constexpr (NS > 2) if (kt + 2 < nk) step(kt + 2, S2{});
+        if constexpr (NS > 3) if (kt + 3 < nk) step(kt + 3, S3{});
     }
     gemm_epilogue<TM, TN, EPI>(p, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2), l32, hh, seg);
 #endif
