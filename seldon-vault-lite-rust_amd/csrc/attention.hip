@@ -28,6 +28,8 @@
 // p-weighted value rows in key order).
 #include <algorithm>
 
+#include <type_traits>
+
 #include "dev_common.hpp"
 #include "svl_internal.hpp"
 
@@ -204,8 +206,11 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
     constexpr int NQ = HD / 8;   // float4 query fragments per lane
     constexpr int NT = HD / 32;  // output tiles
     constexpr int ROWS_PER_WAVE = KT / WAVES;
-    __shared__ float Ks[2][KT * HD];
-    __shared__ float Vs[2][KT * HD];
+    // One LDS object per stage, addressed with compile-time stage indices:
+    // the compiler can then see that the DMA filling one stage does not alias
+    // the reads of the other and need not drain it before reading.
+    __shared__ float Ks0[KT * HD], Ks1[KT * HD];
+    __shared__ float Vs0[KT * HD], Vs1[KT * HD];
 
     const AttnTile tile = p.tiles[blockIdx.x];
     const int G = p.nh / p.nkv;
@@ -259,18 +264,22 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
         koff[q] = (r * ldk + 4 * (lane ^ (r & 15))) * 4;
         voff[q] = (r * ldv + 4 * lane) * 4;
     }
-    auto issue = [&](int buf, int k0) {
+    auto issue = [&](auto st, int k0) {
+        float *kd = decltype(st)::value == 0 ? Ks0 : Ks1;
+        float *vd = decltype(st)::value == 0 ? Vs0 : Vs1;
 #pragma unroll
         for (int q = 0; q < ROWS_PER_WAVE; ++q) {
             const int r = wave * ROWS_PER_WAVE + q;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rk, (__attribute__((address_space(3))) void *)&Ks[buf][r * HD], 16, koff[q],
+                rk, (__attribute__((address_space(3))) void *)&kd[r * HD], 16, koff[q],
                 k0 * ldk * 4, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rv, (__attribute__((address_space(3))) void *)&Vs[buf][r * HD], 16, voff[q],
+                rv, (__attribute__((address_space(3))) void *)&vd[r * HD], 16, voff[q],
                 k0 * ldv * 4, 0, 0);
         }
     };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
     // K fragment c (chunk 2c + hh of key row l32) sits at chunk
     // (2c + hh) ^ (l32 % 16) = 16 (c / 8) + 2 ((c % 8) ^ (sw / 2)) + (hh ^ (sw % 2)).
     const int sw = l32 & 15;
@@ -278,18 +287,20 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
 #pragma unroll
     for (int b = 0; b < 8; ++b) kcol[b] = l32 * HD + 4 * (2 * (b ^ (sw >> 1)) + (hh ^ (sw & 1)));
 
-    issue(0, k_first);
-    for (int it = 0; it < n_tiles; ++it) {
+    issue(S0{}, k_first);
+    // key tile it lives in stage it % 2; the loop is unrolled twice so the
+    // stage index is a constant
+    auto step = [&](int it, auto st) {
+        constexpr int cur = decltype(st)::value;
         const int k0 = k_first + it * KT;
-        const int cur = it & 1;
         __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
         __syncthreads();
-        if (it + 1 < n_tiles) issue(cur ^ 1, k0 + KT);
+        if (it + 1 < n_tiles) issue(std::integral_constant<int, cur ^ 1>{}, k0 + KT);
 
         f32x16 s0;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s0[r] = 0.f;
-        const float *kb = Ks[cur];
+        const float *kb = cur == 0 ? Ks0 : Ks1;
 #pragma unroll
         for (int c = 0; c < NQ; ++c) {
             const f32x4 a0 = *(const f32x4 *)(kb + kcol[c & 7] + 64 * (c >> 3));
@@ -342,7 +353,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
         psum += __shfl_xor(psum, 32, 64);
         l_run += psum;
 
-        const float *vb = Vs[cur] + 4 * hh * HD + 4 * l32;
+        const float *vb = (cur == 0 ? Vs0 : Vs1) + 4 * hh * HD + 4 * l32;
 #pragma unroll
         for (int si = 0; si < 16; ++si) {
             const float *vp = vb + (8 * (si >> 2) + (si & 3)) * HD;
@@ -354,6 +365,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
                 o[4 + t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vc[t], pr[si], o[4 + t], 0, 0, 0);
             }
         }
+    };
+    for (int it = 0; it < n_tiles; it += 2) {
+        step(it, S0{});
+        if (it + 1 < n_tiles) step(it + 1, S1{});
     }
 
     if (vvalid) {
