@@ -181,6 +181,191 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_mfma_kernel(AttnArgs p) {
     }
 }
 
+// head_dim 64 / 128 variant with the K/V tiles streamed by DMA (the vision
+// tower's heads). Same scheme as the head_dim 256 kernel below: K and V
+// tiles of 32 keys go from HBM/L2 into LDS with buffer_load ... lds, double
+// buffered in separate per-stage LDS objects; one DMA instruction moves
+// 1 KB = 1024 / (4 HD) key rows. K rows keep their 16-byte chunks
+// XOR-swizzled by (key % 16) so the 32 rows read at one chunk by S^T hit
+// distinct banks; V rows stay row-contiguous (lane l reads head dims
+// l * HD/32 .. + HD/32 of a row). Online softmax in log2 units with a lazily
+// moved reference max, as below.
+template <int HD, int WAVES>
+__global__ __launch_bounds__(64 * WAVES, 1) void attn_dma_kernel(AttnArgs p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    static_assert(HD == 64 || HD == 128, "head dims of this kernel");
+    constexpr int KT = 32;
+    constexpr int NQ = HD / 8;           // float4 query fragments per lane
+    constexpr int NT = HD / 32;          // output tiles
+    constexpr int CPR = HD / 4;          // 16-byte chunks per key row
+    constexpr int RPI = 64 / CPR;        // key rows per 1 KB DMA instruction
+    constexpr int IPW = KT / RPI / WAVES;  // DMA instructions per wave per operand
+    static_assert(IPW >= 1, "tile split");
+    __shared__ float Ks0[KT * HD], Ks1[KT * HD];
+    __shared__ float Vs0[KT * HD], Vs1[KT * HD];
+
+    const AttnTile tile = p.tiles[blockIdx.x];
+    const int G = p.nh / p.nkv;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, hh = lane >> 5;
+    const int nvec = tile.len * G;
+    const int v = tile.qv0 + wave * 32 + l32;
+    const bool vvalid = v < nvec;
+    const int vq = vvalid ? v : nvec - 1;
+    const int qpos = vq / G;
+    const int qhead = tile.kvh * G + (vq - qpos * G);
+    const float *qrow = p.q + (int64_t)(tile.tok0 + qpos) * p.ldq + qhead * HD;
+
+    // Query fragments pre-scaled by scale * log2(e): S^T comes out in log2 units.
+    const float scale2 = p.scale * 1.4426950408889634f;
+    f32x4 qf[NQ];
+#pragma unroll
+    for (int c = 0; c < NQ; ++c) qf[c] = *(const f32x4 *)(qrow + 8 * c + 4 * hh) * scale2;
+
+    f32x16 o[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+    float m_ref = -INFINITY, l_run = 0.f;
+
+    const int v_last = min(tile.qv0 + 32 * WAVES, nvec) - 1;
+    const int p_lo = tile.qv0 / G, p_hi = v_last / G;
+    int k_lo = 0, k_hi = tile.len - 1;
+    if (p.window >= 0) {
+        k_lo = max(0, p_lo - p.window);
+        k_hi = min(tile.len - 1, p_hi + p.window);
+    }
+    const int k_first = (k_lo / KT) * KT;
+    const int n_tiles = (k_hi - k_first) / KT + 1;
+
+    const int ldk = (int)p.ldk, ldv = (int)p.ldv;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.k + (int64_t)tile.tok0 * p.ldk + tile.kvh * HD), (short)0,
+        ((tile.len - 1) * ldk + HD) * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.v + (int64_t)tile.tok0 * p.ldv + tile.kvh * HD), (short)0,
+        ((tile.len - 1) * ldv + HD) * 4, 0x00020000);
+    // instruction q of this wave fills LDS floats [(wave * IPW + q) * 256, +256):
+    // lane l writes slot l % CPR of row (wave * IPW + q) * RPI + l / CPR
+    int koff[IPW], voff[IPW];
+#pragma unroll
+    for (int q = 0; q < IPW; ++q) {
+        const int r = (wave * IPW + q) * RPI + lane / CPR;
+        const int slot = lane % CPR;
+        koff[q] = (r * ldk + 4 * (slot ^ (r & 15))) * 4;
+        voff[q] = (r * ldv + 4 * slot) * 4;
+    }
+    auto issue = [&](auto st, int k0) {
+        float *kd = decltype(st)::value == 0 ? Ks0 : Ks1;
+        float *vd = decltype(st)::value == 0 ? Vs0 : Vs1;
+#pragma unroll
+        for (int q = 0; q < IPW; ++q) {
+            const int base = (wave * IPW + q) * 256;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rk, (__attribute__((address_space(3))) void *)&kd[base], 16, koff[q],
+                k0 * ldk * 4, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rv, (__attribute__((address_space(3))) void *)&vd[base], 16, voff[q],
+                k0 * ldv * 4, 0, 0);
+        }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    // K fragment c of key row l32: global chunk 2c + hh, stored at slot
+    // (2c + hh) ^ (l32 % 16)
+    const int ksw = l32 & 15;
+
+    issue(S0{}, k_first);
+    auto step = [&](int it, auto st) {
+        constexpr int cur = decltype(st)::value;
+        const int k0 = k_first + it * KT;
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+        __syncthreads();
+        if (it + 1 < n_tiles) issue(std::integral_constant<int, cur ^ 1>{}, k0 + KT);
+
+        const float *kb = (cur == 0 ? Ks0 : Ks1) + l32 * HD;
+        f32x16 s0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s0[r] = 0.f;
+#pragma unroll
+        for (int c = 0; c < NQ; ++c) {
+            const f32x4 a0 = *(const f32x4 *)(kb + 4 * ((2 * c + hh) ^ ksw));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], qf[c][j], s0, 0, 0, 0);
+        }
+
+        float pr[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pr[r] = s0[r];
+        const bool tail = k0 + KT > tile.len;
+        const bool edge = p.window >= 0 && (k0 < p_hi - p.window || k0 + KT - 1 > p_lo + p.window);
+        if (tail || edge) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                const int dist = qpos > key ? qpos - key : key - qpos;
+                const bool ok = (key < tile.len) & ((p.window < 0) | (dist <= p.window));
+                pr[r] = ok ? pr[r] : -INFINITY;
+            }
+        }
+        float tmax = pr[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, pr[r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const bool grow = tmax > m_ref + RESCALE_LOG2;
+        if (__ballot(grow)) {
+            const float m_new = grow ? tmax : m_ref;
+            const float alpha = m_ref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) o[t] = o[t] * alpha;
+            m_ref = m_new;
+        }
+        float psum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            pr[r] = pr[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pr[r] - m_ref);
+            psum += pr[r];
+        }
+        psum += __shfl_xor(psum, 32, 64);
+        l_run += psum;
+
+        const float *vb = (cur == 0 ? Vs0 : Vs1) + 4 * hh * HD + l32 * NT;
+#pragma unroll
+        for (int si = 0; si < 16; ++si) {
+            float va[NT];
+            load_n<NT>(vb + (8 * (si >> 2) + (si & 3)) * HD, va);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[t], pr[si], o[t], 0, 0, 0);
+        }
+    };
+    for (int it = 0; it < n_tiles; it += 2) {
+        step(it, S0{});
+        if (it + 1 < n_tiles) step(it + 1, S1{});
+    }
+
+    if (vvalid) {
+        const float inv = 1.0f / l_run;
+        float *orow = p.out + (int64_t)(tile.tok0 + qpos) * p.ldo + qhead * HD;
+        bool ok = isfinite(inv);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = 8 * (r >> 2) + 4 * hh + (r & 3);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float y = o[t][r] * inv;
+                ok = ok && isfinite(y);
+                orow[i * NT + t] = y;
+            }
+        }
+        if (!ok) raise_flag(p.flag, FLAG_NONFINITE);
+    }
+#endif
+}
+
 // head_dim 256 variant with the K/V tiles streamed by DMA.
 //  * K and V tiles (32 keys x 1 KB) go from HBM/L2 straight into LDS with
 //    buffer_load_dwordx4 ... lds, double buffered (2 x 64 KB): tile t+1 is in
@@ -456,11 +641,19 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
     const dim3 block(64 * ATTN_WAVES);
     switch (a.hd) {
         case 64:
-            hipLaunchKernelGGL((attn_mfma_kernel<64, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s, a);
+            if (a.tokens * std::max(std::max(a.ldk, a.ldv), (int64_t)64) * 4 < INT32_MAX)
+                hipLaunchKernelGGL((attn_dma_kernel<64, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s, a);
+            else
+                hipLaunchKernelGGL((attn_mfma_kernel<64, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
+                                   a);
             return hipGetLastError();
         case 128:
-            hipLaunchKernelGGL((attn_mfma_kernel<128, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
-                               a);
+            if (a.tokens * std::max(std::max(a.ldk, a.ldv), (int64_t)128) * 4 < INT32_MAX)
+                hipLaunchKernelGGL((attn_dma_kernel<128, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
+                                   a);
+            else
+                hipLaunchKernelGGL((attn_mfma_kernel<128, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
+                                   a);
             return hipGetLastError();
         case 256:
             if (a.tokens * std::max(std::max(a.ldk, a.ldv), (int64_t)256) * 4 < INT32_MAX)
