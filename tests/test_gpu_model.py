@@ -126,6 +126,31 @@ def test_shape_a_full_depth_t1_matches_oracle():
     _shape_parity(cfg, [128])
 
 
+def test_long_context_rows_match_oracle():
+    # BASELINE T3's row length: two 2048-token rows through a sliding layer
+    # (window 512: every query's window is cut on both sides) and a full one
+    # (the 2048 x 2048 score matrix).
+    cfg = svl_synth.config_a(layers=2, vocab=4096)
+    _shape_parity(cfg, [2048, 2047])
+
+
+def test_long_context_t3_shape_is_batch_invariant():
+    # The full T3 shape (8 x 2048 tokens, 24 layers): every row of the batch
+    # equals the same row run alone, bit for bit, and is a finite unit vector.
+    cfg = svl_synth.config_a(layers=24, vocab=262144)
+    w = svl_synth.weights(cfg, seed=0)
+    m = model(cfg, w)
+    del w
+    rows = svl_synth.token_rows(cfg["vocab_size"], [2048] * 8, seed=4)
+    batch = m.forward_batch(rows)
+    for i in (0, 5):
+        one = m.forward_batch([rows[i]])[0]
+        assert np.array_equal(one.normalized(), batch[i].normalized()), f"row {i}"
+    for b in batch:
+        e = b.normalized()
+        assert np.isfinite(e).all() and abs(float(e.astype(np.float64) @ e) - 1.0) < 1e-5
+
+
 def test_shape_b_manifest_shape_matches_oracle():
     # 2 KV heads on sliding layers, 1 KV head of head_dim 512 on the full layer.
     cfg = svl_synth.config_b(layers=6, vocab=4096)
