@@ -220,6 +220,22 @@ def audio_weights(config: dict, text_hidden: int, seed: int = 0) -> dict:
     return out
 
 
+def sine_clips(n_clip: int, seed: int = 3, seconds: float = 30.0, rate: int = 16000):
+    """Synthetic 16 kHz mono clips: per clip, three sines of amplitude 0.3 at
+    frequencies uniform in [100, 4000) Hz plus Gaussian noise of sigma 0.05,
+    drawn from numpy default_rng(seed) clip by clip (3 frequencies, then the
+    noise)."""
+    rng = np.random.default_rng(seed)
+    t = np.arange(int(seconds * rate), dtype=np.float64) / rate
+    clips = []
+    for _ in range(n_clip):
+        f = rng.uniform(100.0, 4000.0, 3)
+        x = 0.3 * np.sin(2 * np.pi * f[:, None] * t[None, :]).sum(axis=0)
+        x += rng.normal(0.0, 0.05, t.size)
+        clips.append(x.astype(np.float32))
+    return clips
+
+
 def mel_clips(frames, seed: int = 3, masks=None):
     """Synthetic log-mel spectrograms, one per entry of `frames`."""
     import svl_audio

@@ -8,9 +8,10 @@ reference's double-precision FFT, magnitudes and mel sums in the same order
 with the same twiddles and filter weights. Cases: the six official WAV
 fixtures (and their first values at tests/audio.rs:87-93's 1e-5), the tiny
 audio fixture's 12 frames (tests/audio_tiny.rs:95-110), full 30 s clips of
-noise, a 35 s clip (truncated), a ragged batch with every layout boundary,
-the device-resident variant, the error taxonomy, and the embedding of the
-tiny fixture's samples against its golden embedding."""
+noise, a batch of 30 s clips of sines plus noise, a 35 s clip (truncated), a
+ragged batch with every layout boundary, the device-resident variant, the
+error taxonomy, and the embedding of the tiny fixture's samples against its
+golden embedding."""
 import json
 import os
 
@@ -81,6 +82,16 @@ def test_full_and_truncated_clips(lm):
         mel = lm.compute(x)
         assert mel.frames == 2999
         assert_bit_exact(mel, x, label)
+
+
+def test_sine_and_noise_batch(lm):
+    # The audio throughput workload: 4 x 30 s of three sines (100-4000 Hz)
+    # plus N(0, 0.05^2) noise, computed as one batch.
+    clips = svl_synth.sine_clips(4, seed=3)
+    mels = lm.compute_batch(clips)
+    for i, (x, mel) in enumerate(zip(clips, mels)):
+        assert mel.frames == 2999 and mel.valid_frames() == 2999
+        assert_bit_exact(mel, x, f"sine clip {i}")
 
 
 def test_ragged_batch_and_device_path(lm):
