@@ -447,7 +447,8 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 //    1024 tiles of 128x128, else 128x128; the other streams' work fills the
 //    partial rounds that the cost model above optimises for.
 //  * Paired epilogues need 32-column tile pairs: 128x128, or 64x128 when the
-//    grid of 128x128 tiles would not cover the GPU once.
+//    grid of 128x128 tiles would not cover the GPU twice (the audio tower's
+//    M = 3000 GLU: 384 tiles of 128x128 at 77 TFLOP/s, 752 of 64x128 at 97).
 //  * Stages: grids of at least two workgroups per CU keep two stages (their
 //    co-resident workgroups hide each other's DMA latency, and a deeper
 //    pipeline measured slower there); short grids, whose few workgroups run
@@ -474,7 +475,7 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
         return (int64_t)((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn);
     };
     if constexpr (paired_epi<EPI>()) {
-        if (tiles(128, 128) < 256) {
+        if (tiles(128, 128) < 2 * 256) {
             if (tiles(64, 128) < 256 && a.K % 64 == 0) return launch_dma<64, 128, 64, EPI, 1, 3>(a, s);
             return launch_dma<64, 128, 16, EPI, 3, 4>(a, s);
         }
