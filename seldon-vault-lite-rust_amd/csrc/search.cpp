@@ -50,7 +50,7 @@ struct svl_vector_index {
     DevBuf<uint64_t> keys, keys_alt;
     DevBuf<uint32_t> idx, idx_alt, qkey;
     DevBuf<unsigned char> tmp;
-    DevBuf<uint64_t> samples, samples_alt, cand_key, cand_key_alt;
+    DevBuf<uint64_t> samples, cand_key, cand_key_alt;
     DevBuf<uint32_t> cand_idx, cand_idx_alt;
     DevBuf<unsigned int> cnt, seg_begin, seg_end, blk_count;
     DevBuf<int64_t> take, out_index;
@@ -62,7 +62,7 @@ struct svl_vector_index {
         V.release(); cnorm.release(); perm.release(); Q.release(); qnorm.release();
         qflags.release(); Qd.release(); mask.release(); keys.release(); keys_alt.release(); idx.release();
         idx_alt.release(); qkey.release(); tmp.release(); take.release(); out_index.release();
-        samples.release(); samples_alt.release(); cand_key.release(); cand_key_alt.release();
+        samples.release(); cand_key.release(); cand_key_alt.release();
         cand_idx.release(); cand_idx_alt.release(); cnt.release(); seg_begin.release();
         seg_end.release(); blk_count.release();
         out_score.release();
@@ -111,7 +111,7 @@ svl_status select_top(svl_vector_index *ix, int32_t nq, int64_t offset, int64_t 
                       int64_t *out_index, double *out_score, hipStream_t s, bool &selected) {
     selected = false;
     const int64_t n = ix->n, K = offset + limit;
-    constexpr int S = 4096;
+    constexpr int S = SAMPLE_COUNT;
     if (n < 16 * S || K > n / 16) return SVL_OK;
     const int64_t stride = n / S;
     const double f = (double)K * S / (double)n;
@@ -119,38 +119,40 @@ svl_status select_top(svl_vector_index *ix, int32_t nq, int64_t offset, int64_t 
     const int64_t cap = std::min<int64_t>(n, 2 * (int64_t)(rank + 1) * stride + 4096);
     if ((int64_t)nq * cap > (int64_t)UINT32_MAX) return SVL_OK;
     HIP_TRY(ix->samples.ensure((size_t)nq * S));
-    HIP_TRY(ix->samples_alt.ensure((size_t)nq * S));
     HIP_TRY(ix->cand_key.ensure((size_t)(nq * cap)));
     HIP_TRY(ix->cand_key_alt.ensure((size_t)(nq * cap)));
     HIP_TRY(ix->cand_idx.ensure((size_t)(nq * cap)));
     HIP_TRY(ix->cand_idx_alt.ensure((size_t)(nq * cap)));
     HIP_TRY(ix->cnt.ensure((size_t)nq));
-    HIP_TRY(ix->seg_begin.ensure((size_t)nq));
-    HIP_TRY(ix->seg_end.ensure((size_t)nq));
     HIP_TRY(ix->blk_count.ensure((size_t)nq * (size_t)candidate_blocks(n)));
-    size_t a = 0, b = 0;
-    HIP_TRY(sort_samples(ix->samples.p, ix->samples_alt.p, ix->seg_begin.p, ix->seg_end.p, nq, S,
-                         nullptr, &a, s));
-    HIP_TRY(sort_candidates(ix->cand_key.p, ix->cand_idx.p, ix->cand_key_alt.p,
-                            ix->cand_idx_alt.p, ix->cnt.p, ix->seg_begin.p, ix->seg_end.p, nq,
-                            cap, nullptr, &b, s));
-    HIP_TRY(ix->tmp.ensure(std::max<size_t>({a, b, 1})));
-    HIP_TRY(launch_sample_keys(ix->keys.p, nq, n, S, ix->samples.p, s));
-    HIP_TRY(sort_samples(ix->samples.p, ix->samples_alt.p, ix->seg_begin.p, ix->seg_end.p, nq, S,
-                         ix->tmp.p, &a, s));
-    HIP_TRY(launch_compact_keys(ix->keys.p, nq, n, ix->samples_alt.p, S, rank, cap,
-                                ix->blk_count.p, ix->cnt.p, ix->cand_key.p, ix->cand_idx.p, s));
+    HIP_TRY(sort_samples(ix->keys.p, nq, n, ix->samples.p, s));
+    HIP_TRY(launch_compact_keys(ix->keys.p, nq, n, ix->samples.p, S, rank, cap, ix->blk_count.p,
+                                ix->cnt.p, ix->cand_key.p, ix->cand_idx.p, s));
     std::vector<unsigned int> cnt((size_t)nq);
     HIP_TRY(hipMemcpyAsync(cnt.data(), ix->cnt.p, (size_t)nq * sizeof(unsigned int),
                            hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
+    int64_t most = 0;
     for (int32_t q = 0; q < nq; ++q) {
         const int64_t need = std::min(K, pass[(size_t)q]);
         if ((int64_t)cnt[(size_t)q] < need || (int64_t)cnt[(size_t)q] > cap) return SVL_OK;
+        most = std::max<int64_t>(most, cnt[(size_t)q]);
     }
-    HIP_TRY(sort_candidates(ix->cand_key.p, ix->cand_idx.p, ix->cand_key_alt.p,
-                            ix->cand_idx_alt.p, ix->cnt.p, ix->seg_begin.p, ix->seg_end.p, nq,
-                            cap, ix->tmp.p, &b, s));
+    if (most <= CAND_LDS) {
+        HIP_TRY(sort_candidates_lds(ix->cand_key.p, ix->cand_idx.p, ix->cand_key_alt.p,
+                                    ix->cand_idx_alt.p, ix->cnt.p, nq, cap, s));
+    } else {
+        HIP_TRY(ix->seg_begin.ensure((size_t)nq));
+        HIP_TRY(ix->seg_end.ensure((size_t)nq));
+        size_t b = 0;
+        HIP_TRY(sort_candidates(ix->cand_key.p, ix->cand_idx.p, ix->cand_key_alt.p,
+                                ix->cand_idx_alt.p, ix->cnt.p, ix->seg_begin.p, ix->seg_end.p, nq,
+                                cap, nullptr, &b, s));
+        HIP_TRY(ix->tmp.ensure(std::max<size_t>(b, 1)));
+        HIP_TRY(sort_candidates(ix->cand_key.p, ix->cand_idx.p, ix->cand_key_alt.p,
+                                ix->cand_idx_alt.p, ix->cnt.p, ix->seg_begin.p, ix->seg_end.p, nq,
+                                cap, ix->tmp.p, &b, s));
+    }
     HIP_TRY(launch_gather_candidates(ix->cand_key_alt.p, ix->cand_idx_alt.p, nq, n, cap, ix->perm.p,
                                      offset, limit, ix->take.p, ix->out_index.p,
                                      ix->out_score.p, s));

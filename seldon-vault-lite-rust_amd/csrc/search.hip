@@ -252,13 +252,53 @@ hipError_t rank_sort(const uint64_t *keys, uint64_t *keys_alt, uint32_t *idx, ui
 }
 
 // ---- top-K selection (offset + limit much smaller than the index) ---------------
-// Every stride-th key of each query, S of them: samples[q * S + i].
-__global__ __launch_bounds__(256) void sample_keys_kernel(const uint64_t *keys, int nq, int64_t n,
-                                                          int S, int64_t stride,
-                                                          uint64_t *samples) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const int q = blockIdx.y;
-    if (i < S && q < nq) samples[(int64_t)q * S + i] = keys[(int64_t)q * n + (int64_t)i * stride];
+// Ascending bitonic sort of P keys (P a power of two, P / 2 a multiple of the
+// block size or smaller) held in LDS, by the whole block. With an index
+// array the order is (key, index) lexicographic, a total order when the
+// indices are distinct.
+template <int NT, bool WITH_IDX>
+__device__ void bitonic_lds(uint64_t *k, uint32_t *ix, int P) {
+    for (int size = 2; size <= P; size <<= 1) {
+        for (int j = size >> 1; j > 0; j >>= 1) {
+            for (int t = threadIdx.x; t < P / 2; t += NT) {
+                const int i = 2 * j * (t / j) + (t % j);
+                const int l = i + j;
+                const bool up = (i & size) == 0;
+                const uint64_t a = k[i], b = k[l];
+                bool gt;
+                if constexpr (WITH_IDX)
+                    gt = a > b || (a == b && ix[i] > ix[l]);
+                else
+                    gt = a > b;
+                if (gt == up) {
+                    k[i] = b;
+                    k[l] = a;
+                    if constexpr (WITH_IDX) {
+                        const uint32_t x = ix[i];
+                        ix[i] = ix[l];
+                        ix[l] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// One block per query: its SAMPLE_COUNT samples, every stride-th key
+// (stride = n / SAMPLE_COUNT, so every sample position is below n), sorted
+// ascending into sorted[q * SAMPLE_COUNT ...].
+
+__global__ __launch_bounds__(1024) void sort_samples_kernel(const uint64_t *keys, int64_t n,
+                                                            int64_t stride, uint64_t *sorted) {
+    __shared__ uint64_t sk[SAMPLE_COUNT];
+    const int q = blockIdx.x;
+    for (int i = threadIdx.x; i < SAMPLE_COUNT; i += 1024)
+        sk[i] = keys[(int64_t)q * n + (int64_t)i * stride];
+    __syncthreads();
+    bitonic_lds<1024, false>(sk, nullptr, SAMPLE_COUNT);
+    for (int i = threadIdx.x; i < SAMPLE_COUNT; i += 1024)
+        sorted[(int64_t)q * SAMPLE_COUNT + i] = sk[i];
 }
 
 // Candidates of query q: every admitted key <= sorted sample `rank`, in
@@ -292,19 +332,32 @@ __global__ __launch_bounds__(256) void count_candidates_kernel(const uint64_t *k
             wave_total[0] + wave_total[1] + wave_total[2] + wave_total[3];
 }
 
-// One lane per query: exclusive scan of its block counts (in place) and the
-// total.
-__global__ __launch_bounds__(64) void scan_candidates_kernel(unsigned int *blk_count, int nq,
-                                                             int nblk, unsigned int *cnt) {
-    const int q = blockIdx.x * 64 + threadIdx.x;
-    if (q >= nq) return;
+// One block per query: exclusive scan of its block counts (in place) and the
+// total, 256 counts at a time.
+__global__ __launch_bounds__(256) void scan_candidates_kernel(unsigned int *blk_count, int nblk,
+                                                              unsigned int *cnt) {
+    __shared__ unsigned int wave_total[4];
+    const int q = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    unsigned int *c = blk_count + (int64_t)q * nblk;
     unsigned int run = 0;
-    for (int b = 0; b < nblk; ++b) {
-        const unsigned int c = blk_count[(int64_t)q * nblk + b];
-        blk_count[(int64_t)q * nblk + b] = run;
-        run += c;
+    for (int b0 = 0; b0 < nblk; b0 += 256) {
+        const int b = b0 + threadIdx.x;
+        const unsigned int v = b < nblk ? c[b] : 0u;
+        unsigned int incl = v;
+        for (int o = 1; o < 64; o <<= 1) {
+            const unsigned int up = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += up;
+        }
+        if (lane == 63) wave_total[wave] = incl;
+        __syncthreads();
+        unsigned int before = run;
+        for (int w = 0; w < wave; ++w) before += wave_total[w];
+        if (b < nblk) c[b] = before + incl - v;
+        run += wave_total[0] + wave_total[1] + wave_total[2] + wave_total[3];
+        __syncthreads();
     }
-    cnt[q] = run;
+    if (threadIdx.x == 0) cnt[q] = run;
 }
 
 __global__ __launch_bounds__(256) void write_candidates_kernel(
@@ -348,30 +401,12 @@ __global__ __launch_bounds__(256) void segment_bounds_kernel(const unsigned int 
     end[q] = (unsigned int)(q * cap + min((int64_t)cnt[q], cap));
 }
 
-hipError_t launch_sample_keys(const uint64_t *keys, int nq, int64_t n, int S, uint64_t *samples,
-                              hipStream_t s) {
-    hipLaunchKernelGGL(sample_keys_kernel, dim3((unsigned)((S + 255) / 256), (unsigned)nq),
-                       dim3(256), 0, s, keys, nq, n, S, n / S, samples);
-    return hipGetLastError();
-}
-
-__global__ __launch_bounds__(256) void uniform_bounds_kernel(int nq, int S, unsigned int *begin,
-                                                             unsigned int *end) {
-    const int q = blockIdx.x * 256 + threadIdx.x;
-    if (q >= nq) return;
-    begin[q] = (unsigned int)(q * S);
-    end[q] = (unsigned int)((q + 1) * S);
-}
-
-hipError_t sort_samples(uint64_t *samples, uint64_t *samples_alt, unsigned int *begin,
-                        unsigned int *end, int nq, int S, void *tmp, size_t *tmp_bytes,
+hipError_t sort_samples(const uint64_t *keys, int nq, int64_t n, uint64_t *sorted,
                         hipStream_t s) {
-    if (tmp)
-        hipLaunchKernelGGL(uniform_bounds_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256),
-                           0, s, nq, S, begin, end);
-    return rocprim::segmented_radix_sort_keys(tmp, *tmp_bytes, samples, samples_alt,
-                                              (unsigned int)(nq * S), (unsigned int)nq, begin,
-                                              end, 0, 64, s);
+    if (nq <= 0) return hipSuccess;
+    hipLaunchKernelGGL(sort_samples_kernel, dim3((unsigned)nq), dim3(1024), 0, s, keys, n,
+                       n / SAMPLE_COUNT, sorted);
+    return hipGetLastError();
 }
 
 int candidate_blocks(int64_t n) { return (int)((n + COMPACT_ITEMS - 1) / COMPACT_ITEMS); }
@@ -384,8 +419,8 @@ hipError_t launch_compact_keys(const uint64_t *keys, int nq, int64_t n,
     const dim3 grid((unsigned)nblk, (unsigned)nq);
     hipLaunchKernelGGL(count_candidates_kernel, grid, dim3(256), 0, s, keys, n, sorted_samples, S,
                        rank, nblk, blk_count);
-    hipLaunchKernelGGL(scan_candidates_kernel, dim3((unsigned)((nq + 63) / 64)), dim3(64), 0, s,
-                       blk_count, nq, nblk, cnt);
+    hipLaunchKernelGGL(scan_candidates_kernel, dim3((unsigned)nq), dim3(256), 0, s, blk_count,
+                       nblk, cnt);
     hipLaunchKernelGGL(write_candidates_kernel, grid, dim3(256), 0, s, keys, n, sorted_samples, S,
                        rank, nblk, blk_count, cap, cand_key, cand_idx);
     return hipGetLastError();
@@ -405,6 +440,40 @@ hipError_t sort_candidates(const uint64_t *cand_key, const uint32_t *cand_idx, u
     return rocprim::segmented_radix_sort_pairs(tmp, *tmp_bytes, cand_key, key_alt, cand_idx,
                                                idx_alt, total, (unsigned int)nq, begin, end, 0, 64,
                                                s);
+}
+
+// Candidate lists of at most CAND_LDS entries: one block per query sorts
+// (key, position) pairs in LDS; positions are distinct, so this is the
+// order the stable key sort gives to candidates stored in position order.
+__global__ __launch_bounds__(1024) void sort_candidates_lds_kernel(
+    const uint64_t *cand_key, const uint32_t *cand_idx, const unsigned int *cnt, int64_t cap,
+    uint64_t *key_alt, uint32_t *idx_alt) {
+    __shared__ uint64_t sk[CAND_LDS];
+    __shared__ uint32_t si[CAND_LDS];
+    const int q = blockIdx.x;
+    const int c = (int)min<int64_t>(min<int64_t>((int64_t)cnt[q], cap), CAND_LDS);
+    int P = 2;
+    while (P < c) P <<= 1;
+    const int64_t base = (int64_t)q * cap;
+    for (int i = threadIdx.x; i < P; i += 1024) {
+        sk[i] = i < c ? cand_key[base + i] : ~0ull;
+        si[i] = i < c ? cand_idx[base + i] : ~0u;
+    }
+    __syncthreads();
+    bitonic_lds<1024, true>(sk, si, P);
+    for (int i = threadIdx.x; i < c; i += 1024) {
+        key_alt[base + i] = sk[i];
+        idx_alt[base + i] = si[i];
+    }
+}
+
+hipError_t sort_candidates_lds(const uint64_t *cand_key, const uint32_t *cand_idx,
+                               uint64_t *key_alt, uint32_t *idx_alt, const unsigned int *cnt,
+                               int nq, int64_t cap, hipStream_t s) {
+    if (nq <= 0) return hipSuccess;
+    hipLaunchKernelGGL(sort_candidates_lds_kernel, dim3((unsigned)nq), dim3(1024), 0, s, cand_key,
+                       cand_idx, cnt, cap, key_alt, idx_alt);
+    return hipGetLastError();
 }
 
 // Hits from the sorted candidates: entries [offset, offset + take[q]) of

@@ -245,15 +245,14 @@ hipError_t launch_query_norms(const float *Q, int nq, int D, double *qnorm, int 
 hipError_t rank_sort(const uint64_t *keys, uint64_t *keys_alt, uint32_t *idx, uint32_t *idx_alt,
                      uint32_t *qkey, int nq, int64_t n, void *tmp, size_t *tmp_bytes,
                      const uint32_t **sorted, hipStream_t s);
-// Top-K selection for pages far smaller than the index: S samples per query
-// (every (n / S)-th key), sorted per query; candidates are the admitted keys
+// Top-K selection for pages far smaller than the index: SAMPLE_COUNT samples
+// per query (every (n / SAMPLE_COUNT)-th key, n >= SAMPLE_COUNT), sorted per
+// query into sorted[q * SAMPLE_COUNT ...]; candidates are the admitted keys
 // <= sorted sample `rank`, in position order (at most cap stored per query,
 // cnt[q] counts all); the candidates sorted by (key, position); and the page
 // gathered.
-hipError_t launch_sample_keys(const uint64_t *keys, int nq, int64_t n, int S, uint64_t *samples,
-                              hipStream_t s);
-hipError_t sort_samples(uint64_t *samples, uint64_t *samples_alt, unsigned int *begin,
-                        unsigned int *end, int nq, int S, void *tmp, size_t *tmp_bytes,
+constexpr int SAMPLE_COUNT = 4096;
+hipError_t sort_samples(const uint64_t *keys, int nq, int64_t n, uint64_t *sorted,
                         hipStream_t s);
 // blk_count: candidate_blocks(n) * nq counters.
 int candidate_blocks(int64_t n);
@@ -261,6 +260,12 @@ hipError_t launch_compact_keys(const uint64_t *keys, int nq, int64_t n,
                                const uint64_t *sorted_samples, int S, int rank, int64_t cap,
                                unsigned int *blk_count, unsigned int *cnt, uint64_t *cand_key,
                                uint32_t *cand_idx, hipStream_t s);
+// Candidates sorted in LDS when every query has at most CAND_LDS of them
+// (cnt[q] <= min(cap, CAND_LDS)), into key_alt / idx_alt.
+constexpr int CAND_LDS = 8192;
+hipError_t sort_candidates_lds(const uint64_t *cand_key, const uint32_t *cand_idx,
+                               uint64_t *key_alt, uint32_t *idx_alt, const unsigned int *cnt,
+                               int nq, int64_t cap, hipStream_t s);
 // Stable sort of each query's candidates by key into key_alt / idx_alt.
 hipError_t sort_candidates(const uint64_t *cand_key, const uint32_t *cand_idx, uint64_t *key_alt,
                            uint32_t *idx_alt, const unsigned int *cnt, unsigned int *begin,
