@@ -48,28 +48,32 @@ __global__ __launch_bounds__(256) void queries_f64_kernel(const float *Q, int nq
 }
 
 // The workgroup's QB queries are split over its waves, QW per wave: wave w
-// serves chunk group w / (QB / QW) (64 chunks, one per lane) and query
-// sub-block w % (QB / QW). A workgroup owns CH = 64 * 4 / (QB / QW) chunks,
-// so HBM traffic stays one pass over V per QB queries while each wave needs
-// only QW query values per step.
-template <int QB, int QW, bool VEC4>
+// serves chunk group w / (QB / QW) (64 * CPL chunks, CPL per lane) and query
+// sub-block w % (QB / QW). A workgroup owns CH = 64 * CPL * 4 / (QB / QW)
+// chunks, so HBM traffic stays one pass over V per QB queries while each
+// wave needs only QW query values per step, each reused for CPL chunks
+// (the uniform query loads, not the FMAs, bound the rate when CPL = 1).
+template <int QB, int QW, int CPL, bool VEC4>
 __global__ __launch_bounds__(256) void cosine_keys_kernel(
     const float *__restrict__ V, const double *__restrict__ cnorm,
     const double *__restrict__ Qd, int nq_pad, const double *__restrict__ qnorm, int nq,
     int64_t n, int D, const uint8_t *__restrict__ mask, int64_t mask_stride,
     const int64_t *__restrict__ perm, uint64_t *__restrict__ keys) {
     constexpr int SPLIT = QB / QW;
-    constexpr int CH = 64 * 4 / SPLIT;
+    static_assert(QB % QW == 0 && 4 % SPLIT == 0, "query sub-blocks must tile the 4 waves");
+    constexpr int CH = 64 * CPL * 4 / SPLIT;
     __shared__ float vt[CH][SEARCH_DK + 1];
     const int t = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int lane = t & 63;
-    const int row = (wave / SPLIT) * 64 + lane;
+    const int row0 = (wave / SPLIT) * 64 * CPL + lane;   // rows row0 + 64 * i
     const int64_t c0 = (int64_t)blockIdx.x * CH;
     const int qs = blockIdx.y * QB + (wave % SPLIT) * QW;
-    double acc[QW];
+    double acc[CPL][QW];
 #pragma unroll
-    for (int j = 0; j < QW; ++j) acc[j] = 0.0;
+    for (int i = 0; i < CPL; ++i)
+#pragma unroll
+        for (int j = 0; j < QW; ++j) acc[i][j] = 0.0;
     for (int d0 = 0; d0 < D; d0 += SEARCH_DK) {
         const int dk = min(SEARCH_DK, D - d0);
         if (VEC4) {
@@ -95,25 +99,31 @@ __global__ __launch_bounds__(256) void cosine_keys_kernel(
         __syncthreads();
         const double *qrow = Qd + (int64_t)d0 * nq_pad + qs;
         for (int k = 0; k < dk; ++k) {
-            const double v = (double)vt[row][k];
             const double *qk = qrow + (int64_t)k * nq_pad;
 #pragma unroll
-            for (int j = 0; j < QW; ++j) acc[j] = fma(qk[j], v, acc[j]);
+            for (int i = 0; i < CPL; ++i) {
+                const double v = (double)vt[row0 + 64 * i][k];
+#pragma unroll
+                for (int j = 0; j < QW; ++j) acc[i][j] = fma(qk[j], v, acc[i][j]);
+            }
         }
         __syncthreads();
     }
-    const int64_t c = c0 + row;
-    if (c >= n) return;
-    const double cn = cnorm[c];
-    const int64_t orig = mask ? perm[c] : 0;
 #pragma unroll
-    for (int j = 0; j < QW; ++j) {
-        const int q = qs + j;
-        if (q >= nq) break;
-        uint64_t key = ~0ull;
-        if (!mask || mask[(int64_t)q * mask_stride + orig])
-            key = descending_key(acc[j] / (qnorm[q] * cn));
-        keys[(int64_t)q * n + c] = key;
+    for (int i = 0; i < CPL; ++i) {
+        const int64_t c = c0 + row0 + 64 * i;
+        if (c >= n) break;
+        const double cn = cnorm[c];
+        const int64_t orig = mask ? perm[c] : 0;
+#pragma unroll
+        for (int j = 0; j < QW; ++j) {
+            const int q = qs + j;
+            if (q >= nq) break;
+            uint64_t key = ~0ull;
+            if (!mask || mask[(int64_t)q * mask_stride + orig])
+                key = descending_key(acc[i][j] / (qnorm[q] * cn));
+            keys[(int64_t)q * n + c] = key;
+        }
     }
 }
 
@@ -178,7 +188,7 @@ __global__ __launch_bounds__(256) void gather_hits_kernel(const uint64_t *keys,
 }
 
 int cosine_query_block(int nq) {
-    return nq == 1 ? 1 : nq <= 4 ? 4 : nq <= 8 ? 8 : nq <= 16 ? 16 : 32;
+    return nq == 1 ? 1 : nq <= 4 ? 4 : nq <= 8 ? 8 : nq <= 16 ? 16 : nq <= 32 ? 32 : 64;
 }
 
 hipError_t launch_cosine_keys(const float *V, const double *cnorm, const float *Q,
@@ -193,25 +203,29 @@ hipError_t launch_cosine_keys(const float *V, const double *cnorm, const float *
     hipLaunchKernelGGL(queries_f64_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                        Q, nq, D, nq_pad, Qd);
     const bool vec4 = D % 4 == 0;
-#define COS_LAUNCH(QB, QW)                                                                     \
+#define COS_LAUNCH(QB, QW, CPL)                                                                \
     do {                                                                                      \
-        constexpr int CH = 64 * 4 / (QB / QW);                                                \
+        constexpr int CH = 64 * CPL * 4 / (QB / QW);                                          \
         const dim3 grid((unsigned)((n + CH - 1) / CH), (unsigned)(nq_pad / QB));              \
         if (vec4)                                                                             \
-            hipLaunchKernelGGL((cosine_keys_kernel<QB, QW, true>), grid, dim3(256), 0, s, V, \
-                               cnorm, Qd, nq_pad, qnorm, nq, n, D, mask, mask_stride, perm,   \
-                               keys);                                                         \
+            hipLaunchKernelGGL((cosine_keys_kernel<QB, QW, CPL, true>), grid, dim3(256), 0, \
+                               s, V, cnorm, Qd, nq_pad, qnorm, nq, n, D, mask, mask_stride,   \
+                               perm, keys);                                                   \
         else                                                                                  \
-            hipLaunchKernelGGL((cosine_keys_kernel<QB, QW, false>), grid, dim3(256), 0, s,   \
-                               V, cnorm, Qd, nq_pad, qnorm, nq, n, D, mask, mask_stride,      \
+            hipLaunchKernelGGL((cosine_keys_kernel<QB, QW, CPL, false>), grid, dim3(256), 0, \
+                               s, V, cnorm, Qd, nq_pad, qnorm, nq, n, D, mask, mask_stride,   \
                                perm, keys);                                                   \
     } while (0)
+    // (QB, QW, CPL) measured best at 1M x 768 per query count: up to 16
+    // queries the pass over V (one per QB queries) bounds the rate; from 32
+    // on, CPL = 2 halves the uniform query loads per FMA.
     switch (qb) {
-        case 1: COS_LAUNCH(1, 1); break;
-        case 4: COS_LAUNCH(4, 4); break;
-        case 8: COS_LAUNCH(8, 8); break;
-        case 16: COS_LAUNCH(16, 8); break;
-        default: COS_LAUNCH(32, 8); break;
+        case 1: COS_LAUNCH(1, 1, 1); break;
+        case 4: COS_LAUNCH(4, 4, 1); break;
+        case 8: COS_LAUNCH(8, 2, 2); break;
+        case 16: COS_LAUNCH(16, 4, 2); break;
+        case 32: COS_LAUNCH(32, 8, 2); break;
+        default: COS_LAUNCH(64, 16, 2); break;
     }
 #undef COS_LAUNCH
     return hipGetLastError();

@@ -7,7 +7,8 @@ reference's sequential double accumulation.
 Cases: the reference's unit tests; a ragged dimension (not a multiple of the
 32-wide slice) and a chunk count that is not a multiple of the 256-chunk
 tile; exact score ties broken by chunk id; per-query and shared filters;
-every query-block width (1, 4, 8, 16, 32 and a tail); pagination slices and
+every query-block width (1, 4, 8, 16, 32, 64 and tails), dimensions that are
+and are not a multiple of 4 (vector and scalar staging); pagination slices and
 the full ranking; queries already in HBM; a 200k x 768 index; the error
 taxonomy."""
 import math
@@ -56,9 +57,10 @@ def test_reference_unit_cases():
     assert [(h.index, h.chunk_id, h.vector_rank) for h in hits] == [(2, 3, 2), (1, 2, 3)]
 
 
-@pytest.mark.parametrize("nq", [1, 3, 8, 16, 33])
-def test_batches_match_oracle_bit_for_bit(nq):
-    n, d = 1000 + 37, 100                      # ragged tile and slice
+@pytest.mark.parametrize("nq,d", [(1, 100), (3, 100), (8, 100), (16, 100), (33, 100), (64, 100),
+                                  (65, 100), (40, 99), (12, 99)])
+def test_batches_match_oracle_bit_for_bit(nq, d):
+    n = 1000 + 37                              # ragged tile; d ragged against the 32-wide slice
     emb, ids = corpus(n, d, seed=nq)
     ix = V.VectorIndex(emb, ids)
     rng = np.random.default_rng(100 + nq)
