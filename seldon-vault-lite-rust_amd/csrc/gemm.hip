@@ -7,26 +7,31 @@
 // so both operands are K-contiguous and no transpose is ever materialised.
 //
 // Design (gfx950):
-//  * 256 threads = 4 wave64s in a 2x2 grid; each wave owns a (BM/2)x(BN/2)
-//    block built from v_mfma_f32_32x32x2_f32 tiles (32 FMA/clk/SIMD, the FP32
-//    matrix peak).
+//  * 256 threads = 4 wave64s; WMW waves along M and 4 / WMW along N (2 x 2
+//    unless a tile is only 16 rows per wave); each wave owns a block of
+//    v_mfma_f32_16x16x4_f32 tiles (16 FMA/clk/SIMD per instruction, the FP32
+//    matrix peak). 16 x 16 output tiles keep one wave's dependent MFMA chain
+//    at K / 4 instructions, so small-M launches (one short row) split the
+//    output into many short chains instead of a few long ones.
 //  * K advances in BK-wide slices that go straight from HBM/L2 into LDS with
 //    buffer_load_dwordx4 ... lds (no register staging) through 2-4 LDS
 //    stages: the DMAs of the next slices are in flight while the MFMAs
-//    consume slice k, with one barrier per slice. Buffer resources bound each operand to its valid
-//    rows, so the ragged M tail (and N tail) reads zeros without branches.
+//    consume slice k, with one barrier per slice. Buffer resources bound
+//    each operand to its valid rows, so the ragged M tail (and N tail) reads
+//    zeros without branches.
 //  * LDS rows are unpadded; 16-byte chunks are XOR-swizzled by row
 //    (chunk ^ (row / rows_per_bank_line) % chunks_per_row) on the way in, so
-//    the row-parallel ds_read_b128 fragment loads hit distinct banks.
-//  * Each lane reads float4 = 4 consecutive k of its row and feeds them to 4
-//    MFMAs; lanes 0-31 carry k..k+3 and lanes 32-63 k+4..k+7 of the same 8-k
-//    step, a k-permutation applied identically to A and W, so the sum over
-//    k is unchanged. Every output element sees the same MFMA sequence over k
-//    whatever the tile shape, so results do not depend on the tile chosen
-//    or on a row's position in the batch.
+//    the 16-row fragment loads (one ds_read_b128 per lane) hit distinct banks.
+//  * Lane l reads float4 = k0 + 4 (l / 16) .. + 3 of row l % 16 and feeds
+//    element s to MFMA s, so MFMA s of a 16-k group sums k0 + s, k0 + 4 + s,
+//    k0 + 8 + s, k0 + 12 + s; A and W use the same permutation, so the sum
+//    over k is unchanged. Every output element sees the same MFMA sequence
+//    over k whatever the tile shape, so results do not depend on the tile
+//    chosen or on a row's position in the batch.
 //  * The tile shape is chosen per launch from the grid's per-CU work:
 //    128x128 (3 workgroups per CU) for large grids, 128x64 or 64x64 (4 per
-//    CU) when bigger tiles would leave CUs idle or unevenly loaded.
+//    CU) when bigger tiles would leave CUs idle or unevenly loaded, 32x32
+//    when even 64x64 tiles would not cover the GPU once.
 //  * Tiles are numbered M-major with N fastest and remapped so consecutive
 //    tiles land on the same XCD: the N tiles that share an A block hit that
 //    XCD's L2 instead of HBM.
@@ -42,19 +47,17 @@ namespace svl {
 
 template <int BM, int BN>
 struct GemmShape {
-    static_assert(BM % 64 == 0 && BN % 64 == 0, "2x2 waves of 32x32 MFMA tiles");
+    static_assert(BM % 64 == 0 && BN % 64 == 0, "2x2 waves of 16x16 MFMA tiles");
     static constexpr int BK = 32;
     static constexpr int LDS = BK + 4;
     static constexpr int WM = BM / 2;
     static constexpr int WN = BN / 2;
-    static constexpr int TM = WM / 32;
-    static constexpr int TN = WN / 32;
+    static constexpr int TM = WM / 16;
+    static constexpr int TN = WN / 16;
     static constexpr int A_F4 = BM * BK / 4 / 256;
     static constexpr int W_F4 = BN * BK / 4 / 256;
 };
 
-// Epilogue shared by the GEMM kernels. Accumulator register r of a 32x32
-// tile holds row 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.
 // True for the epilogues whose W rows come in interleaved 32-row pairs.
 template <int EPI>
 constexpr bool paired_epi() {
@@ -72,48 +75,73 @@ __device__ __forceinline__ int clip_segment(const GemmArgs &p, int n0) {
     return p.clip_cols > 0 ? n0 / p.clip_cols : 0;
 }
 
-// Epilogue shared by the GEMM kernels. Accumulator register r of a 32x32
-// tile holds row 8*(r/4) + 4*(lane/32) + r%4 and column lane%32.
+// Epilogue shared by the GEMM kernels. The MFMAs take the W fragment as
+// their first operand, so a 16x16 accumulator tile is C transposed: lane l
+// holds row l % 16 of the tile and its four consecutive columns
+// 4 (l / 16) .. + 3, stored as one float4. Paired epilogues take the
+// 64-column groups of W (32 first-operand rows, then 32 second-operand rows):
+// tiles j and j + 2 of each group of four.
+__device__ __forceinline__ void store_cols4(float *crow, int n0, int limit, bool vec,
+                                            const f32x4 &v) {
+    if (vec && n0 + 3 < limit) {
+        *(f32x4 *)(crow + n0) = v;
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (n0 + r < limit) crow[n0 + r] = v[r];
+    }
+}
+
 template <int TM, int TN, int EPI>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x16 (&acc)[TM][TN],
-                                              int mw, int nw, int l32, int hh, int seg) {
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x4 (&acc)[TM][TN],
+                                              int mw, int nw, int l16, int g, int seg) {
     float olo = 0.f, ohi = 0.f;
     if constexpr (clipped_epi<EPI>()) {
         olo = p.clip[seg][2];
         ohi = p.clip[seg][3];
     }
+    const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)p.C & 15) == 0;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+        const int m = mw + i * 16 + l16;
+        if (m >= p.M) continue;
+        float *crow = p.C + (int64_t)m * p.ldc;
+        if constexpr (paired_epi<EPI>()) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int m = mw + i * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-            if (m >= p.M) continue;
-            float *crow = p.C + (int64_t)m * p.ldc;
-            if constexpr (paired_epi<EPI>()) {
+            for (int j = 0; j < TN; j += 4) {
 #pragma unroll
-                for (int j = 0; j < TN; j += 2) {
-                    const int oc = nw / 2 + (j / 2) * 32 + l32;
-                    if (oc >= p.n_out) continue;
-                    if constexpr (EPI == EPI_GEGLU)
-                        crow[oc] = gelu_tanh(acc[i][j][r]) * acc[i][j + 1][r];
-                    else
-                        crow[oc] = clamp_ref(acc[i][j][r], olo, ohi) *
-                                   sigmoid_ref(clamp_ref(acc[i][j + 1][r], olo, ohi));
+                for (int u = 0; u < 2; ++u) {
+                    const int oc = (nw + j * 16) / 2 + 16 * u + 4 * g;
+                    f32x4 v;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float x = acc[i][j + u][r], y = acc[i][j + 2 + u][r];
+                        if constexpr (EPI == EPI_GEGLU)
+                            v[r] = gelu_tanh(x) * y;
+                        else
+                            v[r] = clamp_ref(x, olo, ohi) * sigmoid_ref(clamp_ref(y, olo, ohi));
+                    }
+                    store_cols4(crow, oc, p.n_out, vec, v);
                 }
-            } else {
+            }
+        } else {
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const int n = nw + j * 32 + l32;
-                    if (n >= p.N) continue;
-                    float v = acc[i][j][r];
-                    if constexpr (EPI == EPI_SCALE) v = v * p.alpha;
+            for (int j = 0; j < TN; ++j) {
+                const int n0 = nw + j * 16 + 4 * g;
+                f32x4 v;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int n = n0 + r;
+                    float x = acc[i][j][r];
+                    if constexpr (EPI == EPI_SCALE) x = x * p.alpha;
                     if constexpr (EPI == EPI_GELU_MUL)
-                        v = gelu_tanh(v) * p.aux[(int64_t)m * p.ldaux + n];
-                    if constexpr (EPI == EPI_BIAS) v = v + p.aux[n];
-                    if constexpr (EPI == EPI_CLIP_STORE) v = clamp_ref(v, olo, ohi);
-                    if constexpr (EPI == EPI_CLIP_SILU) v = silu_ref(clamp_ref(v, olo, ohi));
-                    crow[n] = v;
+                        x = gelu_tanh(x) * (n < p.N ? p.aux[(int64_t)m * p.ldaux + n] : 0.f);
+                    if constexpr (EPI == EPI_BIAS) x = x + (n < p.N ? p.aux[n] : 0.f);
+                    if constexpr (EPI == EPI_CLIP_STORE) x = clamp_ref(x, olo, ohi);
+                    if constexpr (EPI == EPI_CLIP_SILU) x = silu_ref(clamp_ref(x, olo, ohi));
+                    v[r] = x;
                 }
+                store_cols4(crow, n0, p.N, vec, v);
             }
         }
     }
@@ -136,7 +164,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int l32 = lane & 31, hh = lane >> 5;
+    const int l16 = lane & 15, g = lane >> 4;
     const int M = p.M, N = p.N, K = p.K;
     const int seg = clip_segment(p, n0);
     float alo = 0.f, ahi = 0.f;
@@ -145,13 +173,11 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
         ahi = p.clip[seg][1];
     }
 
-    f32x16 acc[S::TM][S::TN];
+    f32x4 acc[S::TM][S::TN];
 #pragma unroll
     for (int i = 0; i < S::TM; ++i)
 #pragma unroll
-        for (int j = 0; j < S::TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        for (int j = 0; j < S::TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     f32x4 ra[S::A_F4], rw[S::W_F4];
     auto load_global = [&](int k0) {
@@ -192,32 +218,32 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         if (kt + 1 < nk) load_global((kt + 1) * S::BK);
-        const float *as = &As[cur][(wm * S::WM + l32) * S::LDS + 4 * hh];
-        const float *ws = &Ws[cur][(wn * S::WN + l32) * S::LDS + 4 * hh];
+        const float *as = &As[cur][(wm * S::WM + l16) * S::LDS + 4 * g];
+        const float *ws = &Ws[cur][(wn * S::WN + l16) * S::LDS + 4 * g];
 #pragma unroll
-        for (int kk = 0; kk < S::BK; kk += 8) {
+        for (int kk = 0; kk < S::BK; kk += 16) {
             f32x4 a[S::TM], b[S::TN];
 #pragma unroll
             for (int i = 0; i < S::TM; ++i) {
-                a[i] = *(const f32x4 *)(as + i * 32 * S::LDS + kk);
+                a[i] = *(const f32x4 *)(as + i * 16 * S::LDS + kk);
                 if constexpr (clipped_epi<EPI>()) a[i] = clamp4(a[i], alo, ahi);
             }
 #pragma unroll
-            for (int j = 0; j < S::TN; ++j) b[j] = *(const f32x4 *)(ws + j * 32 * S::LDS + kk);
+            for (int j = 0; j < S::TN; ++j) b[j] = *(const f32x4 *)(ws + j * 16 * S::LDS + kk);
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
                 for (int i = 0; i < S::TM; ++i)
 #pragma unroll
                     for (int j = 0; j < S::TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[j][s], a[i][s],
                                                                          acc[i][j], 0, 0, 0);
         }
         if (kt + 1 < nk) store_lds(cur ^ 1);
         __syncthreads();
     }
 
-    gemm_epilogue<S::TM, S::TN, EPI>(p, acc, m0 + wm * S::WM, n0 + wn * S::WN, l32, hh, seg);
+    gemm_epilogue<S::TM, S::TN, EPI>(p, acc, m0 + wm * S::WM, n0 + wn * S::WN, l16, g, seg);
 }
 
 // s_waitcnt vmcnt(N): at most N vector-memory operations of this wave in flight.
@@ -228,18 +254,23 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // Direct-to-LDS variant; requires K % BK == 0 and 16-byte aligned rows. NS
-// LDS stages: NS - 1 slices are in flight while one is consumed.
-template <int BM, int BN, int BK, int EPI, int MINB, int NS>
+// LDS stages: NS - 1 slices are in flight while one is consumed. WMW waves
+// along M, 4 / WMW along N.
+template <int BM, int BN, int BK, int EPI, int MINB, int NS, int WMW>
 __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m, int tiles_n) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int TM = BM / 64, TN = BN / 64;   // 32x32 tiles per wave
+    constexpr int WNW = 4 / WMW;                // waves along N
+    constexpr int WTM = BM / WMW, WTN = BN / WNW;
+    constexpr int TM = WTM / 16, TN = WTN / 16;  // 16x16 tiles per wave
     constexpr int CPR = BK / 4;                 // 16-byte chunks per row
     constexpr int RPK = 64 / CPR;               // rows per 1 KB DMA instruction
     constexpr int RPL = 64 / BK;                // rows per 64-bank LDS line
     constexpr int A_CH = BM / RPK / 4;          // DMA instructions per wave per slice
     constexpr int W_CH = BN / RPK / 4;
-    static_assert(BM % 64 == 0 && BN % 64 == 0 && A_CH >= 1 && W_CH >= 1, "tile shape");
-    static_assert(!paired_epi<EPI>() || TN % 2 == 0, "paired epilogues take 32-column tile pairs");
+    static_assert(WMW == 1 || WMW == 2 || WMW == 4, "wave layout");
+    static_assert(BK % 16 == 0 && WTM % 16 == 0 && WTN % 16 == 0 && A_CH >= 1 && W_CH >= 1,
+                  "tile shape");
+    static_assert(!paired_epi<EPI>() || TN % 4 == 0, "paired epilogues take 64-column wave tiles");
     static_assert(NS >= 2 && NS <= 4 && (NS - 2) * (A_CH + W_CH) < 64, "pipeline depth");
     // One LDS object per stage, addressed with compile-time stage indices, so
     // the compiler can see that the DMA filling one stage never aliases the
@@ -269,8 +300,8 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
     const int m0 = tm * BM, n0 = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int l32 = lane & 31, hh = lane >> 5;
+    const int wm = wave / WNW, wn = wave % WNW;
+    const int l16 = lane & 15, g = lane >> 4;
     const int M = p.M, N = p.N;
     const int seg = clip_segment(p, n0);
     float alo = 0.f, ahi = 0.f;
@@ -315,15 +346,15 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
                 w_off[q], k0 * 4, 0, 0);
     };
 
-    f32x16 acc[TM][TN];
+    f32x4 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int sw = (l32 / RPL) % CPR;
+    // 16-row fragment blocks start at multiples of 16, so a row's swizzle
+    // depends on l16 only
+    const int sw = (l16 / RPL) % CPR;
     const int nk = p.K / BK;
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
@@ -343,26 +374,26 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
         __syncthreads();   // ... and every wave's; slice kt-1 is no longer read
         if (kt + NS - 1 < nk)
             issue(std::integral_constant<int, (cur + NS - 1) % NS>{}, (kt + NS - 1) * BK);
-        const float *as = stage_a(st) + (wm * (BM / 2) + l32) * BK;
-        const float *ws = stage_w(st) + (wn * (BN / 2) + l32) * BK;
+        const float *as = stage_a(st) + (wm * WTM + l16) * BK;
+        const float *ws = stage_w(st) + (wn * WTN + l16) * BK;
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 8) {
-            const int pos = ((kk >> 2) + hh) ^ sw;
+        for (int kk = 0; kk < BK; kk += 16) {
+            const int pos = ((kk >> 2) + g) ^ sw;
             f32x4 a[TM], b[TN];
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
-                a[i] = *(const f32x4 *)(as + i * 32 * BK + 4 * pos);
+                a[i] = *(const f32x4 *)(as + i * 16 * BK + 4 * pos);
                 if constexpr (clipped_epi<EPI>()) a[i] = clamp4(a[i], alo, ahi);
             }
 #pragma unroll
-            for (int j = 0; j < TN; ++j) b[j] = *(const f32x4 *)(ws + j * 32 * BK + 4 * pos);
+            for (int j = 0; j < TN; ++j) b[j] = *(const f32x4 *)(ws + j * 16 * BK + 4 * pos);
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[j][s], a[i][s],
                                                                          acc[i][j], 0, 0, 0);
         }
     };
@@ -372,7 +403,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
         if constexpr (NS > 2) if (kt + 2 < nk) step(kt + 2, S2{});
         if constexpr (NS > 3) if (kt + 3 < nk) step(kt + 3, S3{});
     }
-    gemm_epilogue<TM, TN, EPI>(p, acc, m0 + wm * (BM / 2), n0 + wn * (BN / 2), l32, hh, seg);
+    gemm_epilogue<TM, TN, EPI>(p, acc, m0 + wm * WTM, n0 + wn * WTN, l16, g, seg);
 #endif
 }
 
@@ -426,11 +457,11 @@ __global__ __launch_bounds__(256) void gemm_nt_simple(GemmArgs p) {
     }
 }
 
-template <int BM, int BN, int BK, int EPI, int MINB, int NS>
+template <int BM, int BN, int BK, int EPI, int MINB, int NS, int WMW = 2>
 static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
     const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
-    hipLaunchKernelGGL((gemm_nt_dma<BM, BN, BK, EPI, MINB, NS>), dim3(tm * tn), dim3(256), 0, s, a,
-                       tm, tn);
+    hipLaunchKernelGGL((gemm_nt_dma<BM, BN, BK, EPI, MINB, NS, WMW>), dim3(tm * tn), dim3(256), 0,
+                       s, a, tm, tn);
     return hipGetLastError();
 }
 
@@ -438,24 +469,30 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 //  * A launch with the whole GPU: workgroups are spread round-robin over the
 //    256 CUs, so it takes about ceil(tiles / 256) tile-times on its busiest
 //    CU; the cost of a tile shape is that count times the tile's MAC count
-//    over the shape's measured efficiency (128x128 at 3 per CU: 1.0; 128x64
-//    and 64x64 at 4 per CU: 0.95 and 0.90). Small grids therefore take
-//    smaller tiles (64x64 for the audio tower's M = 3000 projections), large
-//    ones 128x128. 64x64 uses BK 32 when K is long or N narrow.
+//    over the shape's measured efficiency (128x128 at 3 per CU and 64x64 at
+//    4 per CU: 1.0; 128x64 at 4 per CU: 0.95), ties going to 64x64. With
+//    16x16 fragments 64x64 tiles keep up with larger ones (the 18688-token
+//    O projection: 168 us against 202 us for 128x64 tiles), and their finer
+//    grid wastes less of the last round.
 //  * A launch that shares the GPU with other streams (a.cus > 0, the text
-//    path's row groups): measured best is 64x64 for N <= 256, 128x64 below
-//    1024 tiles of 128x128, else 128x128; the other streams' work fills the
-//    partial rounds that the cost model above optimises for.
-//  * Paired epilogues need 32-column tile pairs: 128x128, or 64x128 when the
-//    grid of 128x128 tiles would not cover the GPU twice (the audio tower's
-//    M = 3000 GLU: 384 tiles of 128x128 at 77 TFLOP/s, 752 of 64x128 at 97).
+//    path's row groups): 64x64 (O and down per group: 65 and 93 us against
+//    75 and 110 us for 128x64); the other streams' work fills the partial
+//    rounds that the cost model above optimises for.
+//  * Grids that 64x64 tiles would not cover once (one short row, 128 tokens:
+//    QKV at 6.9 us against 15.9 us for 64x64 tiles): 32x32 tiles, one 16x16
+//    block per wave; paired epilogues 64x64 tiles with the four waves
+//    stacked along M (one 16x64 block each).
+//  * Paired epilogues need the 32 + 32 columns of a pair in one wave:
+//    128x128, or 64x128 when the grid of 128x128 tiles would not cover the
+//    GPU twice (the audio tower's M = 3000 GLU: 384 tiles of 128x128 at 77
+//    TFLOP/s, 752 of 64x128 at 97).
 //  * Stages: grids of at least two workgroups per CU keep two stages (their
 //    co-resident workgroups hide each other's DMA latency, and a deeper
 //    pipeline measured slower there); short grids, whose few workgroups run
 //    the K loop alone, take as many stages as the LDS budget allows.
 //    Grids that do not fill the GPU once (fewer tiles than CUs) also take
 //    64-wide K slices, so each barrier is amortised over four times more
-//    MFMAs (the k order, set by the 8-k steps, is the same for any slice
+//    MFMAs (the k order, set by the 16-k groups, is the same for any slice
 //    width).
 template <int BM, int BN, int BK, int EPI, int MINB, int NS_DEEP>
 static hipError_t launch_dma_staged(const GemmArgs &a, hipStream_t s) {
@@ -474,25 +511,36 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
     auto tiles = [&](int bm, int bn) {
         return (int64_t)((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn);
     };
+    // Grids that 64x64 tiles would not cover once (a few short rows): the
+    // smallest tiles, one 16x16 (or, paired, 16x64) block per wave, so each
+    // wave's MFMA chain is K / 4 (or 4 x K / 4) instructions long.
+    const bool tiny = tiles(64, 64) < 256 && a.K % 32 == 0;
     if constexpr (paired_epi<EPI>()) {
+        if (tiny) {
+            if (a.K % 64 == 0) return launch_dma<64, 64, 64, EPI, 1, 3, 4>(a, s);
+            return launch_dma<64, 64, 32, EPI, 1, 4, 4>(a, s);
+        }
         if (tiles(128, 128) < 2 * 256) {
             if (tiles(64, 128) < 256 && a.K % 64 == 0) return launch_dma<64, 128, 64, EPI, 1, 3>(a, s);
             return launch_dma<64, 128, 16, EPI, 3, 4>(a, s);
         }
         return launch_dma_staged<128, 128, 16, EPI, 3, 3>(a, s);
     } else {
+        if (tiny) {
+            if (a.K % 64 == 0) return launch_dma<32, 32, 64, EPI, 1, 3>(a, s);
+            return launch_dma<32, 32, 32, EPI, 1, 4>(a, s);
+        }
         if (a.cus > 0) {
-            if (a.N <= 256 && a.K % 32 == 0) return launch_dma<64, 64, 32, EPI, 4, 2>(a, s);
+            if (a.K % 32 == 0) return launch_dma<64, 64, 32, EPI, 4, 2>(a, s);
             if (tiles(128, 128) < 4 * 256) return launch_dma_staged<128, 64, 16, EPI, 4, 3>(a, s);
             return launch_dma_staged<128, 128, 16, EPI, 3, 3>(a, s);
         }
         auto per_cu = [&](int bm, int bn) { return (double)((tiles(bm, bn) + 255) / 256); };
         const double c128 = per_cu(128, 128) * (128.0 * 128.0);
         const double c12864 = per_cu(128, 64) * (128.0 * 64.0) / 0.95;
-        const double c64 = per_cu(64, 64) * (64.0 * 64.0) / 0.90;
-        if (c64 < c128 && c64 < c12864) {
-            if (a.K % 32 == 0 && (a.K >= 1024 || a.N <= 256))
-                return launch_dma_staged<64, 64, 32, EPI, 4, 3>(a, s);
+        const double c64 = per_cu(64, 64) * (64.0 * 64.0);
+        if (c64 <= c128 && c64 < c12864) {
+            if (a.K % 32 == 0) return launch_dma_staged<64, 64, 32, EPI, 4, 3>(a, s);
             return launch_dma_staged<64, 64, 16, EPI, 4, 4>(a, s);
         }
         if (c12864 < c128) return launch_dma_staged<128, 64, 16, EPI, 4, 3>(a, s);
