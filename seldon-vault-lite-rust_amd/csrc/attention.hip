@@ -388,42 +388,43 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int HD = 256;
     constexpr int KT = 32;
-    constexpr int NQ = HD / 8;   // float4 query fragments per lane
-    constexpr int NT = HD / 32;  // output tiles
+    constexpr int SPLIT = 8 / WAVES;     // workgroups per 128-vector work item
     constexpr int ROWS_PER_WAVE = KT / WAVES;
+    static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4 || WAVES == 8, "waves");
     // One LDS object per stage, addressed with compile-time stage indices:
     // the compiler can then see that the DMA filling one stage does not alias
     // the reads of the other and need not drain it before reading.
     __shared__ float Ks0[KT * HD], Ks1[KT * HD];
     __shared__ float Vs0[KT * HD], Vs1[KT * HD];
 
-    const AttnTile tile = p.tiles[blockIdx.x];
+    const AttnTile tile = p.tiles[blockIdx.x / SPLIT];
     const int G = p.nh / p.nkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int l32 = lane & 31, hh = lane >> 5;
+    const int l16 = lane & 15, g = lane >> 4;
     const int nvec = tile.len * G;
-    const int v = tile.qv0 + wave * 32 + l32;
+    const int vbase = tile.qv0 + (blockIdx.x % SPLIT) * 16 * WAVES;
+    if (vbase >= nvec) return;   // the whole workgroup: a part past the row's vectors
+    const int v = vbase + wave * 16 + l16;
     const bool vvalid = v < nvec;
     const int vq = vvalid ? v : nvec - 1;
     const int qpos = vq / G;
     const int qhead = tile.kvh * G + (vq - qpos * G);
     const float *qrow = p.q + (int64_t)(tile.tok0 + qpos) * p.ldq + qhead * HD;
 
-    // Query fragments pre-scaled by scale * log2(e): S^T comes out in log2 units.
+    // Query fragments pre-scaled by scale * log2(e): S^T comes out in log2
+    // units. Fragment c holds dims 16 c + 4 (lane / 16) .. + 3.
     const float scale2 = p.scale * 1.4426950408889634f;
-    f32x4 qf[NQ];
+    f32x4 qf[HD / 16];
 #pragma unroll
-    for (int c = 0; c < NQ; ++c) qf[c] = *(const f32x4 *)(qrow + 8 * c + 4 * hh) * scale2;
+    for (int c = 0; c < HD / 16; ++c) qf[c] = *(const f32x4 *)(qrow + 16 * c + 4 * g) * scale2;
 
-    f32x16 o[NT];
+    f32x4 o[HD / 16];
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
+    for (int t = 0; t < HD / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_ref = -INFINITY, l_run = 0.f;
 
-    const int v_last = min(tile.qv0 + 32 * WAVES, nvec) - 1;
-    const int p_lo = tile.qv0 / G, p_hi = v_last / G;
+    const int v_last = min(vbase + 16 * WAVES, nvec) - 1;
+    const int p_lo = vbase / G, p_hi = v_last / G;
     int k_lo = 0, k_hi = tile.len - 1;
     if (p.window >= 0) {
         k_lo = max(0, p_lo - p.window);
@@ -465,12 +466,6 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
-    // K fragment c (chunk 2c + hh of key row l32) sits at chunk
-    // (2c + hh) ^ (l32 % 16) = 16 (c / 8) + 2 ((c % 8) ^ (sw / 2)) + (hh ^ (sw % 2)).
-    const int sw = l32 & 15;
-    int kcol[8];
-#pragma unroll
-    for (int b = 0; b < 8; ++b) kcol[b] = l32 * HD + 4 * (2 * (b ^ (sw >> 1)) + (hh ^ (sw & 1)));
 
     issue(S0{}, k_first);
     // key tile it lives in stage it % 2; the loop is unrolled twice so the
@@ -482,43 +477,55 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
         __syncthreads();
         if (it + 1 < n_tiles) issue(std::integral_constant<int, cur ^ 1>{}, k0 + KT);
 
-        f32x16 s0;
+        // S^T for keys kb * 16 + 4 (lane / 16) + r (register r of block kb)
+        // and query vector lane % 16. K row kb * 16 + l16 holds dim chunk
+        // 4 c + g at slot (4 c + g) ^ l16.
+        const float *kb0 = (cur == 0 ? Ks0 : Ks1) + l16 * HD;
+        f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s0[r] = 0.f;
-        const float *kb = cur == 0 ? Ks0 : Ks1;
+        for (int c = 0; c < HD / 16; ++c) {
+            const int slot = (4 * c + g) ^ l16;
 #pragma unroll
-        for (int c = 0; c < NQ; ++c) {
-            const f32x4 a0 = *(const f32x4 *)(kb + kcol[c & 7] + 64 * (c >> 3));
+            for (int kb = 0; kb < 2; ++kb) {
+                const f32x4 kf = *(const f32x4 *)(kb0 + kb * 16 * HD + 4 * slot);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], qf[c][j], s0, 0, 0, 0);
+                for (int j = 0; j < 4; ++j)
+                    s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[j], qf[c][j], s[kb], 0, 0, 0);
+            }
         }
 
         // Scores in log2 units; masks only on the row-tail tile and on tiles
         // that cross a sliding-window edge of some query of the block.
         // Lanes of invalid query vectors are never stored and need no mask.
-        float pr[16];
+        float pr[2][4];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) pr[r] = s0[r];
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pr[kb][r] = s[kb][r];
         const bool tail = k0 + KT > tile.len;
         const bool edge = p.window >= 0 && (k0 < p_hi - p.window || k0 + KT - 1 > p_lo + p.window);
         if (tail || edge) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = k0 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                const int dist = qpos > key ? qpos - key : key - qpos;
-                const bool ok = (key < tile.len) & ((p.window < 0) | (dist <= p.window));
-                pr[r] = ok ? pr[r] : -INFINITY;
-            }
-        }
-        float tmax = pr[0];
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, pr[r]);
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + kb * 16 + 4 * g + r;
+                    const int dist = qpos > key ? qpos - key : key - qpos;
+                    const bool ok = (key < tile.len) & ((p.window < 0) | (dist <= p.window));
+                    pr[kb][r] = ok ? pr[kb][r] : -INFINITY;
+                }
+        }
+        float tmax = pr[0][0];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, pr[kb][r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
         // Lazy rescale: the reference max m_ref only moves when a query's
         // max grows by more than RESCALE_LOG2 (probabilities then stay below
         // 2^RESCALE_LOG2). O and l are divided out at the end, so the result
-        // is the same softmax; the 128 accumulator registers are rescaled
+        // is the same softmax; the 64 accumulator registers are rescaled
         // only on the (rare, wave-uniform) tiles where some max jumped.
         const bool grow = tmax > m_ref + RESCALE_LOG2;
         if (__ballot(grow)) {
@@ -526,30 +533,37 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
             const float alpha = m_ref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - m_new);
             l_run *= alpha;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) o[t] = o[t] * alpha;
+            for (int t = 0; t < HD / 16; ++t) o[t] = o[t] * alpha;
             m_ref = m_new;
         }
         float psum = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            pr[r] = pr[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pr[r] - m_ref);
-            psum += pr[r];
-        }
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pr[kb][r] = pr[kb][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pr[kb][r] - m_ref);
+                psum += pr[kb][r];
+            }
+        psum += __shfl_xor(psum, 16, 64);
         psum += __shfl_xor(psum, 32, 64);
         l_run += psum;
 
-        const float *vb = (cur == 0 ? Vs0 : Vs1) + 4 * hh * HD + 4 * l32;
+        // O^T += V^T P^T, keys 4 (lane / 16) + r of block kb in MFMA r: lane
+        // l supplies V row kb * 16 + 4 (l / 16) + r, dims 64 c + 4 (l % 16)
+        // .. + 3, one per output tile 4 c + t (tile row i = dim 64 c + 4 i + t).
+        const float *vb = (cur == 0 ? Vs0 : Vs1) + 4 * g * HD + 4 * l16;
 #pragma unroll
-        for (int si = 0; si < 16; ++si) {
-            const float *vp = vb + (8 * (si >> 2) + (si & 3)) * HD;
-            const f32x4 va = *(const f32x4 *)(vp);
-            const f32x4 vc = *(const f32x4 *)(vp + 128);
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[t], pr[si], o[t], 0, 0, 0);
-                o[4 + t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vc[t], pr[si], o[4 + t], 0, 0, 0);
-            }
-        }
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < HD / 64; ++c) {
+                    const f32x4 va = *(const f32x4 *)(vb + (kb * 16 + r) * HD + 64 * c);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        o[4 * c + t] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[t], pr[kb][r],
+                                                                          o[4 * c + t], 0, 0, 0);
+                }
     };
     for (int it = 0; it < n_tiles; it += 2) {
         step(it, S0{});
@@ -557,22 +571,21 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
     }
 
     if (vvalid) {
+        // lane l holds, for its query vector, dims 64 c + 16 (l / 16) + 4 r
+        // + t in register r of tile 4 c + t
         const float inv = 1.0f / l_run;
         float *orow = p.out + (int64_t)(tile.tok0 + qpos) * p.ldo + qhead * HD;
         bool ok = isfinite(inv);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 8 * (r >> 2) + 4 * hh + (r & 3);
-            f32x4 lo, hi;
+        for (int c = 0; c < HD / 64; ++c)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                lo[t] = o[t][r] * inv;
-                hi[t] = o[4 + t][r] * inv;
+            for (int r = 0; r < 4; ++r) {
+                f32x4 d;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) d[t] = o[4 * c + t][r] * inv;
+                ok = ok && finite4(d);
+                *(f32x4 *)(orow + 64 * c + 16 * g + 4 * r) = d;
             }
-            ok = ok && finite4(lo) && finite4(hi);
-            *(f32x4 *)(orow + 4 * i) = lo;
-            *(f32x4 *)(orow + 128 + 4 * i) = hi;
-        }
         if (!ok) raise_flag(p.flag, FLAG_NONFINITE);
     }
 #endif
@@ -655,13 +668,32 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
                 hipLaunchKernelGGL((attn_mfma_kernel<128, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
                                    a);
             return hipGetLastError();
-        case 256:
-            if (a.tokens * std::max(std::max(a.ldk, a.ldv), (int64_t)256) * 4 < INT32_MAX)
-                hipLaunchKernelGGL((attn_dma256_kernel<ATTN_WAVES>), dim3(a.n_tiles), block, 0, s, a);
-            else
+        case 256: {
+            // Buffer windows are per row: the longest row bounds the offsets.
+            const int64_t rows = a.max_len > 0 ? a.max_len : a.tokens;
+            if (rows * std::max(std::max(a.ldk, a.ldv), (int64_t)256) * 4 >= INT32_MAX) {
                 hipLaunchKernelGGL((attn_mfma_kernel<256, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
                                    a);
+                return hipGetLastError();
+            }
+            // 8 waves (two per SIMD) per 128-vector work item on grids that
+            // cover the GPU; smaller grids split each item over 2, 4 or 8
+            // workgroups of 16 vectors per wave, which shortens the per-CU
+            // chain without changing any vector's arithmetic.
+            const int64_t t = a.n_tiles;
+            if (t >= 256)
+                hipLaunchKernelGGL((attn_dma256_kernel<8>), dim3((unsigned)t), dim3(512), 0, s, a);
+            else if (2 * t >= 256)
+                hipLaunchKernelGGL((attn_dma256_kernel<4>), dim3((unsigned)(2 * t)), dim3(256), 0, s,
+                                   a);
+            else if (4 * t >= 256)
+                hipLaunchKernelGGL((attn_dma256_kernel<2>), dim3((unsigned)(4 * t)), dim3(128), 0, s,
+                                   a);
+            else
+                hipLaunchKernelGGL((attn_dma256_kernel<1>), dim3((unsigned)(8 * t)), dim3(64), 0, s,
+                                   a);
             return hipGetLastError();
+        }
         default:
             if (!a.pos || !a.rowlen) return hipErrorInvalidValue;
             hipLaunchKernelGGL(attn_simple_kernel, dim3((unsigned)(a.tokens * a.nh)), dim3(64), 0,

@@ -535,6 +535,7 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
             a.rowlen = rowlen;
             a.tokens = T;
             a.flag = flag;
+            a.max_len = std::min<int64_t>(T, MAX_TEXT_TOKENS);  // validate_row caps every row
             Timer tm(m, s, KC_ATTENTION, grp.attn_flops[ly.full]);
             HIP_TRY(launch_attention(a, s));
         }
@@ -1276,6 +1277,7 @@ svl_status svl_bidirectional_attention(const float *d_q, const float *d_k, const
     a.pos = dp;
     a.rowlen = dl;
     a.tokens = seq_len;
+    a.max_len = seq_len;
     a.flag = flag;
     svl_status st = SVL_OK;
     if ((!tiles.empty() && hipMemcpyAsync(dt, tiles.data(), tiles.size() * sizeof(AttnTile),

@@ -104,6 +104,7 @@ struct AttnArgs {
     const int32_t *rowlen;  // per token: length of its row (simple kernel)
     int64_t tokens;
     int *flag;
+    int64_t max_len = 0;    // longest row (0: unknown, bounded by tokens)
 };
 // Query vectors per work item of the MFMA kernel (0 if hd has no MFMA kernel).
 int attn_block_vectors(int hd);
