@@ -10,8 +10,9 @@
 // workgroup takes 32 * WAVES query vectors of one row and one KV head and
 // streams that row's keys through LDS in tiles of 32, so one K/V tile feeds
 // all G heads (the single shared KV head of EmbeddingGemma).
-//  * S^T = K . Q^T with v_mfma_f32_32x32x2_f32: A = K tile from LDS, B = the
-//    wave's 32 query vectors held in registers for the whole pass. In the
+//  * S^T = K . Q^T with v_mfma_f32_32x32x2_f32 (head_dim 256: 16x16x4, see
+//    below): A = K tile from LDS, B = the wave's 32 query vectors held in
+//    registers for the whole pass. In the
 //    transposed score tile each lane owns one query column, so the running
 //    max / sum of the online softmax and the rescale of the output are
 //    lane-local (one cross-half shuffle per tile).
@@ -366,23 +367,30 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma_kernel(AttnArgs p) {
 #endif
 }
 
-// head_dim 256 variant with the K/V tiles streamed by DMA.
+// head_dim 256 variant with the K/V tiles streamed by DMA, on
+// v_mfma_f32_16x16x4_f32 fragments: each wave owns 16 query vectors, so its
+// Q fragments and O^T accumulators take 64 + 64 registers and a 128-vector
+// work item runs as 8 waves, two per SIMD, that hide each other's softmax
+// and barrier stalls. Small grids split a work item over 2, 4 or 8
+// workgroups (fewer waves each); a vector's arithmetic is the same either
+// way, so results do not depend on the batch.
 //  * K and V tiles (32 keys x 1 KB) go from HBM/L2 straight into LDS with
 //    buffer_load_dwordx4 ... lds, double buffered (2 x 64 KB): tile t+1 is in
 //    flight while tile t is consumed; one barrier per tile. Keys past the row
 //    end fall outside the buffer window and read as zero.
-//  * K rows are stored with their 16-byte chunks XOR-swizzled by (key % 16):
-//    S^T reads 32 key rows at the same chunk, which then hit 16 distinct
-//    bank groups per phase. V rows are read row-contiguously by each half
-//    wave and stay unswizzled.
-//  * Output row i of O^T tile t holds head dims (t / 4) * 128 + 4 i + t % 4:
-//    lane l reads chunks l and 32 + l of a V row, contiguous across lanes.
+//  * S^T = K . Q^T per 16-key block: K rows are stored with their 16-byte
+//    chunks XOR-swizzled by (key % 16), so the 16 key rows read at one chunk
+//    hit 16 distinct bank groups. Lane l holds keys 4 (l / 16) + r of each
+//    block for query vector l % 16; max and sum reduce over the four lanes
+//    of a query.
+//  * O^T += V^T . P^T: MFMA r of a key block sums keys 4 g + r (g = lane /
+//    16), exactly the probabilities lane g holds in register r; lane l reads
+//    V row 4 g + r at dims 64 c + 4 (l % 16) .. + 3, one dim for each of the
+//    four output tiles 4 c + t (tile row i = head dim 64 c + 4 i + t). V rows
+//    are read contiguously by each 16-lane group and stay unswizzled.
 //  * Online softmax in log2 units (v_exp_f32) with a lazily moved reference
-//    max, so the 128 output accumulators are rescaled only when a query's
-//    running max grows by more than 2^8.
-//  * The per-tile advance of the DMA source goes in the scalar offset, and
-//    the swizzled K-read offsets are 8 per-lane values, which keeps the
-//    kernel within 512 registers without spills.
+//    max, so the output accumulators are rescaled only when a query's running
+//    max grows by more than 2^8.
 template <int WAVES>
 __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) {
 #if defined(__HIP_DEVICE_COMPILE__)
