@@ -474,10 +474,11 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 //    256 CUs, so it takes about ceil(tiles / 256) tile-times on its busiest
 //    CU; the cost of a tile shape is that count times the tile's MAC count
 //    over the shape's measured efficiency (128x128 at 3 per CU and 64x64 at
-//    4 per CU: 1.0; 128x64 at 4 per CU: 0.95), ties going to 64x64. With
-//    16x16 fragments 64x64 tiles keep up with larger ones (the 18688-token
-//    O projection: 168 us against 202 us for 128x64 tiles), and their finer
-//    grid wastes less of the last round.
+//    4 per CU: 1.0; 128x64 at 4 per CU: 0.95), ties going to the larger
+//    tile (the audio tower's M = 3000 x 4096 projection: 250 us at 128x128,
+//    275 us at 64x64). With 16x16 fragments 64x64 tiles keep up with larger
+//    ones (the 18688-token O projection: 168 us against 202 us for 128x64
+//    tiles), and their finer grid wastes less of the last round.
 //  * A launch that shares the GPU with other streams (a.cus > 0, the text
 //    path's row groups): 64x64 (O and down per group: 65 and 93 us against
 //    75 and 110 us for 128x64); the other streams' work fills the partial
@@ -546,7 +547,7 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
         const double c128 = per_cu(128, 128) * (128.0 * 128.0);
         const double c12864 = per_cu(128, 64) * (128.0 * 64.0) / 0.95;
         const double c64 = per_cu(64, 64) * (64.0 * 64.0);
-        if (c64 <= c128 && c64 < c12864) {
+        if (c64 < c128 && c64 < c12864) {
             if (a.K % 32 == 0) return launch_dma_staged<64, 64, 32, EPI, 4, 3>(a, s);
             return launch_dma_staged<64, 64, 16, EPI, 4, 4>(a, s);
         }
