@@ -488,18 +488,29 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
         // S^T for keys kb * 16 + 4 (lane / 16) + r (register r of block kb)
         // and query vector lane % 16. K row kb * 16 + l16 holds dim chunk
         // 4 c + g at slot (4 c + g) ^ l16.
+        // The fragments of chunk c + 1 are read while chunk c's MFMAs run,
+        // and the two key blocks' chains alternate.
         const float *kb0 = (cur == 0 ? Ks0 : Ks1) + l16 * HD;
         f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        f32x4 kf0 = *(const f32x4 *)(kb0 + 4 * (g ^ l16));
+        f32x4 kf1 = *(const f32x4 *)(kb0 + 16 * HD + 4 * (g ^ l16));
 #pragma unroll
         for (int c = 0; c < HD / 16; ++c) {
-            const int slot = (4 * c + g) ^ l16;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const f32x4 kf = *(const f32x4 *)(kb0 + kb * 16 * HD + 4 * slot);
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[j], qf[c][j], s[kb], 0, 0, 0);
+            f32x4 nf0 = kf0, nf1 = kf1;
+            if (c + 1 < HD / 16) {
+                const int slot = (4 * (c + 1) + g) ^ l16;
+                nf0 = *(const f32x4 *)(kb0 + 4 * slot);
+                nf1 = *(const f32x4 *)(kb0 + 16 * HD + 4 * slot);
             }
+            // keep the reads of chunk c + 1 ahead of chunk c's MFMAs
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                s[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf0[j], qf[c][j], s[0], 0, 0, 0);
+                s[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf1[j], qf[c][j], s[1], 0, 0, 0);
+            }
+            kf0 = nf0;
+            kf1 = nf1;
         }
 
         // Scores in log2 units; masks only on the row-tail tile and on tiles
