@@ -369,15 +369,19 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma_kernel(AttnArgs p) {
 
 // head_dim 256 variant with the K/V tiles streamed by DMA, on
 // v_mfma_f32_16x16x4_f32 fragments: each wave owns 16 query vectors, so its
-// Q fragments and O^T accumulators take 64 + 64 registers and a 128-vector
-// work item runs as 8 waves, two per SIMD, that hide each other's softmax
-// and barrier stalls. Small grids split a work item over 2, 4 or 8
-// workgroups (fewer waves each); a vector's arithmetic is the same either
-// way, so results do not depend on the batch.
-//  * K and V tiles (32 keys x 1 KB) go from HBM/L2 straight into LDS with
-//    buffer_load_dwordx4 ... lds, double buffered (2 x 64 KB): tile t+1 is in
-//    flight while tile t is consumed; one barrier per tile. Keys past the row
-//    end fall outside the buffer window and read as zero.
+// Q fragments and O^T accumulators take 64 + 64 registers. Keys stream in
+// 16-key tiles double buffered in 64 KB, so two workgroups of four waves
+// share a CU (two waves per SIMD from independent workgroups: one's barrier
+// and softmax stalls overlap the other's MFMAs), and the small LDS footprint
+// leaves room for the GEMM workgroups of concurrent streams. A 128-vector
+// work item is split over 2 workgroups, or 4 or 8 of fewer waves on small
+// grids; a vector's arithmetic is the same either way, so results do not
+// depend on the batch. (With 32-key tiles and one 8-wave workgroup per CU the
+// text batch of 64 rows ran 2.5 % slower.)
+//  * K and V tiles go from HBM/L2 straight into LDS with
+//    buffer_load_dwordx4 ... lds, double buffered: tile t+1 is in flight
+//    while tile t is consumed; one barrier per tile. Keys past the row end
+//    fall outside the buffer window and read as zero.
 //  * S^T = K . Q^T per 16-key block: K rows are stored with their 16-byte
 //    chunks XOR-swizzled by (key % 16), so the 16 key rows read at one chunk
 //    hit 16 distinct bank groups. Lane l holds keys 4 (l / 16) + r of each
@@ -391,14 +395,16 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma_kernel(AttnArgs p) {
 //  * Online softmax in log2 units (v_exp_f32) with a lazily moved reference
 //    max, so the output accumulators are rescaled only when a query's running
 //    max grows by more than 2^8.
-template <int WAVES>
-__global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) {
+template <int WAVES, int KT>
+__global__ __launch_bounds__(64 * WAVES, (KT == 16 && WAVES == 4) ? 2 : 1) void attn_dma256_kernel(
+    AttnArgs p) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int HD = 256;
-    constexpr int KT = 32;
+    constexpr int NKB = KT / 16;         // 16-key blocks per tile
     constexpr int SPLIT = 8 / WAVES;     // workgroups per 128-vector work item
     constexpr int ROWS_PER_WAVE = KT / WAVES;
     static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4 || WAVES == 8, "waves");
+    static_assert((KT == 16 || KT == 32) && ROWS_PER_WAVE >= 1, "key tile");
     // One LDS object per stage, addressed with compile-time stage indices:
     // the compiler can then see that the DMA filling one stage does not alias
     // the reads of the other and need not drain it before reading.
@@ -491,41 +497,45 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
         // The fragments of chunk c + 1 are read while chunk c's MFMAs run,
         // and the two key blocks' chains alternate.
         const float *kb0 = (cur == 0 ? Ks0 : Ks1) + l16 * HD;
-        f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-        f32x4 kf0 = *(const f32x4 *)(kb0 + 4 * (g ^ l16));
-        f32x4 kf1 = *(const f32x4 *)(kb0 + 16 * HD + 4 * (g ^ l16));
+        f32x4 s[NKB], kf[NKB];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+            s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            kf[kb] = *(const f32x4 *)(kb0 + kb * 16 * HD + 4 * (g ^ l16));
+        }
 #pragma unroll
         for (int c = 0; c < HD / 16; ++c) {
-            f32x4 nf0 = kf0, nf1 = kf1;
-            if (c + 1 < HD / 16) {
-                const int slot = (4 * (c + 1) + g) ^ l16;
-                nf0 = *(const f32x4 *)(kb0 + 4 * slot);
-                nf1 = *(const f32x4 *)(kb0 + 16 * HD + 4 * slot);
+            f32x4 nf[NKB];
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                nf[kb] = kf[kb];
+                if (c + 1 < HD / 16)
+                    nf[kb] = *(const f32x4 *)(kb0 + kb * 16 * HD + 4 * ((4 * (c + 1) + g) ^ l16));
             }
             // keep the reads of chunk c + 1 ahead of chunk c's MFMAs
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                s[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf0[j], qf[c][j], s[0], 0, 0, 0);
-                s[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf1[j], qf[c][j], s[1], 0, 0, 0);
-            }
-            kf0 = nf0;
-            kf1 = nf1;
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+                    s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kb][j], qf[c][j], s[kb], 0, 0, 0);
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) kf[kb] = nf[kb];
         }
 
         // Scores in log2 units; masks only on the row-tail tile and on tiles
         // that cross a sliding-window edge of some query of the block.
         // Lanes of invalid query vectors are never stored and need no mask.
-        float pr[2][4];
+        float pr[NKB][4];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) pr[kb][r] = s[kb][r];
         const bool tail = k0 + KT > tile.len;
         const bool edge = p.window >= 0 && (k0 < p_hi - p.window || k0 + KT - 1 > p_lo + p.window);
         if (tail || edge) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int key = k0 + kb * 16 + 4 * g + r;
@@ -536,7 +546,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
         }
         float tmax = pr[0][0];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, pr[kb][r]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
@@ -557,7 +567,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
         }
         float psum = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 pr[kb][r] = pr[kb][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pr[kb][r] - m_ref);
@@ -572,7 +582,7 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma256_kernel(AttnArgs p) 
         // .. + 3, one per output tile 4 c + t (tile row i = dim 64 c + 4 i + t).
         const float *vb = (cur == 0 ? Vs0 : Vs1) + 4 * g * HD + 4 * l16;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -695,22 +705,21 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
                                    a);
                 return hipGetLastError();
             }
-            // 8 waves (two per SIMD) per 128-vector work item on grids that
-            // cover the GPU; smaller grids split each item over 2, 4 or 8
-            // workgroups of 16 vectors per wave, which shortens the per-CU
-            // chain without changing any vector's arithmetic.
+            // 16-key tiles double buffered in 64 KB: two workgroups of four
+            // waves (64 query vectors each) share a CU, so one's barrier and
+            // softmax stalls overlap the other's MFMAs. Smaller grids split a
+            // 128-vector work item over 4 or 8 workgroups of fewer waves; a
+            // vector's arithmetic is the same in every variant.
             const int64_t t = a.n_tiles;
-            if (t >= 256)
-                hipLaunchKernelGGL((attn_dma256_kernel<8>), dim3((unsigned)t), dim3(512), 0, s, a);
-            else if (2 * t >= 256)
-                hipLaunchKernelGGL((attn_dma256_kernel<4>), dim3((unsigned)(2 * t)), dim3(256), 0, s,
-                                   a);
+            if (2 * t >= 256)
+                hipLaunchKernelGGL((attn_dma256_kernel<4, 16>), dim3((unsigned)(2 * t)), dim3(256),
+                                   0, s, a);
             else if (4 * t >= 256)
-                hipLaunchKernelGGL((attn_dma256_kernel<2>), dim3((unsigned)(4 * t)), dim3(128), 0, s,
-                                   a);
+                hipLaunchKernelGGL((attn_dma256_kernel<2, 16>), dim3((unsigned)(4 * t)), dim3(128),
+                                   0, s, a);
             else
-                hipLaunchKernelGGL((attn_dma256_kernel<1>), dim3((unsigned)(8 * t)), dim3(64), 0, s,
-                                   a);
+                hipLaunchKernelGGL((attn_dma256_kernel<1, 16>), dim3((unsigned)(8 * t)), dim3(64),
+                                   0, s, a);
             return hipGetLastError();
         }
         default:
