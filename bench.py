@@ -410,7 +410,7 @@ def main():
             lat.append((time.perf_counter() - a) * 1e3)
 
     traffic = gemm_traffic()
-    roofline = {"kernel": "gemm_nt_dma<128,128,16,EPI_GEGLU,3,2,2> (gate/up projection + GeGLU)",
+    roofline = {"kernel": "gemm_nt_dma<64,128,16,EPI_GEGLU,4,2,2> (gate/up projection + GeGLU)",
                 "bound": "mfma", "achieved": round(gu_tflops, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(gu_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
                 "traffic": traffic,

@@ -487,10 +487,11 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 //    QKV at 6.9 us against 15.9 us for 64x64 tiles): 32x32 tiles, one 16x16
 //    block per wave; paired epilogues 64x64 tiles with the four waves
 //    stacked along M (one 16x64 block each).
-//  * Paired epilogues need the 32 + 32 columns of a pair in one wave:
-//    128x128, or 64x128 when the grid of 128x128 tiles would not cover the
-//    GPU twice (the audio tower's M = 3000 GLU: 384 tiles of 128x128 at 77
-//    TFLOP/s, 752 of 64x128 at 97).
+//  * Paired epilogues need the 32 + 32 columns of a pair in one wave: 64x128
+//    tiles (4 per CU; the 18688-token gate/up: 481 us against 502 us for
+//    128x128; per row group, with 32-wide K slices: 168 us against 185 us),
+//    deeper pipelines below two rounds of 128x128 tiles, or 64x64 with the
+//    four waves stacked along M on one-row grids.
 //  * Stages: grids of at least two workgroups per CU keep two stages (their
 //    co-resident workgroups hide each other's DMA latency, and a deeper
 //    pipeline measured slower there); short grids, whose few workgroups run
@@ -525,11 +526,12 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
             if (a.K % 64 == 0) return launch_dma<64, 64, 64, EPI, 1, 3, 4>(a, s);
             return launch_dma<64, 64, 32, EPI, 1, 4, 4>(a, s);
         }
+        if (a.cus > 0 && a.K % 32 == 0) return launch_dma<64, 128, 32, EPI, 3, 2>(a, s);
         if (tiles(128, 128) < 2 * 256) {
             if (tiles(64, 128) < 256 && a.K % 64 == 0) return launch_dma<64, 128, 64, EPI, 1, 3>(a, s);
             return launch_dma<64, 128, 16, EPI, 3, 4>(a, s);
         }
-        return launch_dma_staged<128, 128, 16, EPI, 3, 3>(a, s);
+        return launch_dma<64, 128, 16, EPI, 4, 2>(a, s);
     } else {
         if (tiny) {
             // 128-wide K slices: fewer DMA round trips on a chain that is
