@@ -4,23 +4,23 @@
 // per row, and the sliding window is the reference's symmetric inclusive
 // |i - j| <= r.
 //
-// MFMA kernel (head_dim 64 / 128 / 256). All query heads that share a KV
+// MFMA kernels (head_dim 64 / 128 / 256). All query heads that share a KV
 // head are flattened into "query vectors" v = pos * G + g (G = heads per KV
-// head), which is exactly their order in the [T, heads, hd] layout. A
-// workgroup takes 32 * WAVES query vectors of one row and one KV head and
-// streams that row's keys through LDS in tiles of 32, so one K/V tile feeds
-// all G heads (the single shared KV head of EmbeddingGemma).
-//  * S^T = K . Q^T with v_mfma_f32_32x32x2_f32 (head_dim 256: 16x16x4, see
-//    below): A = K tile from LDS, B = the wave's 32 query vectors held in
-//    registers for the whole pass. In the
-//    transposed score tile each lane owns one query column, so the running
-//    max / sum of the online softmax and the rescale of the output are
-//    lane-local (one cross-half shuffle per tile).
-//  * O^T += V^T . P^T: the probabilities are consumed straight from the S^T
-//    accumulator registers as the B operand (register r of lane l is key
-//    8*(r/4) + 4*(l/32) + r%4, the k index that MFMA step r expects), and
-//    the A operand reads V with output-row i mapped to head dims i*NT..+NT so
-//    each lane loads NT contiguous floats.
+// head), which is exactly their order in the [T, heads, hd] layout. A work
+// item is 128 query vectors of one row and one KV head; that row's keys
+// stream through LDS in tiles, so one K/V tile feeds all G heads (the single
+// shared KV head of EmbeddingGemma).
+//  * attn16_kernel (below): K/V tiles by DMA, v_mfma_f32_16x16x4_f32
+//    fragments, 16 vectors per wave. It runs every launch whose rows fit
+//    32-bit buffer offsets (every row the models accept).
+//  * attn_mfma_kernel: the register-staged fallback for longer rows, on
+//    v_mfma_f32_32x32x2_f32 with 32 vectors per wave. S^T = K . Q^T with the
+//    queries in registers; each lane owns one query column of the score
+//    tile, so the online softmax is lane-local (one cross-half shuffle per
+//    tile). O^T += V^T . P^T takes P straight from the score accumulators
+//    (register r of lane l is key 8*(r/4) + 4*(l/32) + r%4, the k index MFMA
+//    step r expects); V is read with output-row i mapped to head dims
+//    i*NT..+NT so each lane loads NT contiguous floats.
 //  * Tiles outside the sliding window of every query in the block are
 //    skipped; padding keys beyond the row length are zero-filled and masked.
 //
@@ -182,195 +182,12 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_mfma_kernel(AttnArgs p) {
     }
 }
 
-// head_dim 64 / 128 variant with the K/V tiles streamed by DMA (the vision
-// tower's heads). Same scheme as the head_dim 256 kernel below: K and V
-// tiles of 32 keys go from HBM/L2 into LDS with buffer_load ... lds, double
-// buffered in separate per-stage LDS objects; one DMA instruction moves
-// 1 KB = 1024 / (4 HD) key rows. K rows keep their 16-byte chunks
-// XOR-swizzled by (key % 16) so the 32 rows read at one chunk by S^T hit
-// distinct banks; V rows stay row-contiguous (lane l reads head dims
-// l * HD/32 .. + HD/32 of a row). Online softmax in log2 units with a lazily
-// moved reference max, as below.
-template <int HD, int WAVES>
-__global__ __launch_bounds__(64 * WAVES, 1) void attn_dma_kernel(AttnArgs p) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    static_assert(HD == 64 || HD == 128, "head dims of this kernel");
-    constexpr int KT = 32;
-    constexpr int NQ = HD / 8;           // float4 query fragments per lane
-    constexpr int NT = HD / 32;          // output tiles
-    constexpr int CPR = HD / 4;          // 16-byte chunks per key row
-    constexpr int RPI = 64 / CPR;        // key rows per 1 KB DMA instruction
-    constexpr int IPW = KT / RPI / WAVES;  // DMA instructions per wave per operand
-    static_assert(IPW >= 1, "tile split");
-    __shared__ float Ks0[KT * HD], Ks1[KT * HD];
-    __shared__ float Vs0[KT * HD], Vs1[KT * HD];
-
-    const AttnTile tile = p.tiles[blockIdx.x];
-    const int G = p.nh / p.nkv;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int l32 = lane & 31, hh = lane >> 5;
-    const int nvec = tile.len * G;
-    const int v = tile.qv0 + wave * 32 + l32;
-    const bool vvalid = v < nvec;
-    const int vq = vvalid ? v : nvec - 1;
-    const int qpos = vq / G;
-    const int qhead = tile.kvh * G + (vq - qpos * G);
-    const float *qrow = p.q + (int64_t)(tile.tok0 + qpos) * p.ldq + qhead * HD;
-
-    // Query fragments pre-scaled by scale * log2(e): S^T comes out in log2 units.
-    const float scale2 = p.scale * 1.4426950408889634f;
-    f32x4 qf[NQ];
-#pragma unroll
-    for (int c = 0; c < NQ; ++c) qf[c] = *(const f32x4 *)(qrow + 8 * c + 4 * hh) * scale2;
-
-    f32x16 o[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
-    float m_ref = -INFINITY, l_run = 0.f;
-
-    const int v_last = min(tile.qv0 + 32 * WAVES, nvec) - 1;
-    const int p_lo = tile.qv0 / G, p_hi = v_last / G;
-    int k_lo = 0, k_hi = tile.len - 1;
-    if (p.window >= 0) {
-        k_lo = max(0, p_lo - p.window);
-        k_hi = min(tile.len - 1, p_hi + p.window);
-    }
-    const int k_first = (k_lo / KT) * KT;
-    const int n_tiles = (k_hi - k_first) / KT + 1;
-
-    const int ldk = (int)p.ldk, ldv = (int)p.ldv;
-    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.k + (int64_t)tile.tok0 * p.ldk + tile.kvh * HD), (short)0,
-        ((tile.len - 1) * ldk + HD) * 4, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.v + (int64_t)tile.tok0 * p.ldv + tile.kvh * HD), (short)0,
-        ((tile.len - 1) * ldv + HD) * 4, 0x00020000);
-    // instruction q of this wave fills LDS floats [(wave * IPW + q) * 256, +256):
-    // lane l writes slot l % CPR of row (wave * IPW + q) * RPI + l / CPR
-    int koff[IPW], voff[IPW];
-#pragma unroll
-    for (int q = 0; q < IPW; ++q) {
-        const int r = (wave * IPW + q) * RPI + lane / CPR;
-        const int slot = lane % CPR;
-        koff[q] = (r * ldk + 4 * (slot ^ (r & 15))) * 4;
-        voff[q] = (r * ldv + 4 * slot) * 4;
-    }
-    auto issue = [&](auto st, int k0) {
-        float *kd = decltype(st)::value == 0 ? Ks0 : Ks1;
-        float *vd = decltype(st)::value == 0 ? Vs0 : Vs1;
-#pragma unroll
-        for (int q = 0; q < IPW; ++q) {
-            const int base = (wave * IPW + q) * 256;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rk, (__attribute__((address_space(3))) void *)&kd[base], 16, koff[q],
-                k0 * ldk * 4, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rv, (__attribute__((address_space(3))) void *)&vd[base], 16, voff[q],
-                k0 * ldv * 4, 0, 0);
-        }
-    };
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    // K fragment c of key row l32: global chunk 2c + hh, stored at slot
-    // (2c + hh) ^ (l32 % 16)
-    const int ksw = l32 & 15;
-
-    issue(S0{}, k_first);
-    auto step = [&](int it, auto st) {
-        constexpr int cur = decltype(st)::value;
-        const int k0 = k_first + it * KT;
-        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
-        __syncthreads();
-        if (it + 1 < n_tiles) issue(std::integral_constant<int, cur ^ 1>{}, k0 + KT);
-
-        const float *kb = (cur == 0 ? Ks0 : Ks1) + l32 * HD;
-        f32x16 s0;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s0[r] = 0.f;
-#pragma unroll
-        for (int c = 0; c < NQ; ++c) {
-            const f32x4 a0 = *(const f32x4 *)(kb + 4 * ((2 * c + hh) ^ ksw));
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[j], qf[c][j], s0, 0, 0, 0);
-        }
-
-        float pr[16];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) pr[r] = s0[r];
-        const bool tail = k0 + KT > tile.len;
-        const bool edge = p.window >= 0 && (k0 < p_hi - p.window || k0 + KT - 1 > p_lo + p.window);
-        if (tail || edge) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = k0 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                const int dist = qpos > key ? qpos - key : key - qpos;
-                const bool ok = (key < tile.len) & ((p.window < 0) | (dist <= p.window));
-                pr[r] = ok ? pr[r] : -INFINITY;
-            }
-        }
-        float tmax = pr[0];
-#pragma unroll
-        for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, pr[r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const bool grow = tmax > m_ref + RESCALE_LOG2;
-        if (__ballot(grow)) {
-            const float m_new = grow ? tmax : m_ref;
-            const float alpha = m_ref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - m_new);
-            l_run *= alpha;
-#pragma unroll
-            for (int t = 0; t < NT; ++t) o[t] = o[t] * alpha;
-            m_ref = m_new;
-        }
-        float psum = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            pr[r] = pr[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pr[r] - m_ref);
-            psum += pr[r];
-        }
-        psum += __shfl_xor(psum, 32, 64);
-        l_run += psum;
-
-        const float *vb = (cur == 0 ? Vs0 : Vs1) + 4 * hh * HD + l32 * NT;
-#pragma unroll
-        for (int si = 0; si < 16; ++si) {
-            float va[NT];
-            load_n<NT>(vb + (8 * (si >> 2) + (si & 3)) * HD, va);
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[t], pr[si], o[t], 0, 0, 0);
-        }
-    };
-    for (int it = 0; it < n_tiles; it += 2) {
-        step(it, S0{});
-        if (it + 1 < n_tiles) step(it + 1, S1{});
-    }
-
-    if (vvalid) {
-        const float inv = 1.0f / l_run;
-        float *orow = p.out + (int64_t)(tile.tok0 + qpos) * p.ldo + qhead * HD;
-        bool ok = isfinite(inv);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 8 * (r >> 2) + 4 * hh + (r & 3);
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const float y = o[t][r] * inv;
-                ok = ok && isfinite(y);
-                orow[i * NT + t] = y;
-            }
-        }
-        if (!ok) raise_flag(p.flag, FLAG_NONFINITE);
-    }
-#endif
-}
-
-// head_dim 256 variant with the K/V tiles streamed by DMA, on
-// v_mfma_f32_16x16x4_f32 fragments: each wave owns 16 query vectors, so its
-// Q fragments and O^T accumulators take 64 + 64 registers. Keys stream in
-// 16-key tiles double buffered in 64 KB, so two workgroups of four waves
+// DMA kernel for head_dim 64, 128 and 256 on v_mfma_f32_16x16x4_f32
+// fragments: each wave owns 16 query vectors, so its Q fragments and O^T
+// accumulators take HD / 4 + HD / 4 registers (64 + 64 at head_dim 256).
+// Keys stream in tiles of KT keys (16 at head_dim 256, 32 at 128, 64 at 64:
+// 64 KB double buffered, and more MFMAs per barrier and softmax at the
+// smaller head dims), so two workgroups of four waves
 // share a CU (two waves per SIMD from independent workgroups: one's barrier
 // and softmax stalls overlap the other's MFMAs), and the small LDS footprint
 // leaves room for the GEMM workgroups of concurrent streams. A 128-vector
@@ -379,9 +196,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma_kernel(AttnArgs p) {
 // depend on the batch. (With 32-key tiles and one 8-wave workgroup per CU the
 // text batch of 64 rows ran 2.5 % slower.)
 //  * K and V tiles go from HBM/L2 straight into LDS with
-//    buffer_load_dwordx4 ... lds, double buffered: tile t+1 is in flight
-//    while tile t is consumed; one barrier per tile. Keys past the row end
-//    fall outside the buffer window and read as zero.
+//    buffer_load_dwordx4 ... lds (one instruction moves 1 KB = 256 / HD
+//    rows), double buffered: tile t+1 is in flight while tile t is
+//    consumed; one barrier per tile. Keys past the row end fall outside the
+//    buffer window and read as zero.
 //  * S^T = K . Q^T per 16-key block: K rows are stored with their 16-byte
 //    chunks XOR-swizzled by (key % 16), so the 16 key rows read at one chunk
 //    hit 16 distinct bank groups. Lane l holds keys 4 (l / 16) + r of each
@@ -395,16 +213,17 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_dma_kernel(AttnArgs p) {
 //  * Online softmax in log2 units (v_exp_f32) with a lazily moved reference
 //    max, so the output accumulators are rescaled only when a query's running
 //    max grows by more than 2^8.
-template <int WAVES, int KT>
-__global__ __launch_bounds__(64 * WAVES, (KT == 16 && WAVES == 4) ? 2 : 1) void attn_dma256_kernel(
-    AttnArgs p) {
+template <int HD, int WAVES, int KT>
+__global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(AttnArgs p) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int HD = 256;
     constexpr int NKB = KT / 16;         // 16-key blocks per tile
     constexpr int SPLIT = 8 / WAVES;     // workgroups per 128-vector work item
-    constexpr int ROWS_PER_WAVE = KT / WAVES;
+    constexpr int RPI = 256 / HD;        // key rows per 1 KB DMA instruction
+    constexpr int CPR = HD / 4;          // 16-byte chunks per key row
+    constexpr int INSTR_PER_WAVE = KT / RPI / WAVES;
+    static_assert(HD == 64 || HD == 128 || HD == 256, "head dim");
     static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4 || WAVES == 8, "waves");
-    static_assert((KT == 16 || KT == 32) && ROWS_PER_WAVE >= 1, "key tile");
+    static_assert(KT % 16 == 0 && INSTR_PER_WAVE >= 1 && (KT / RPI) % WAVES == 0, "key tile");
     // One LDS object per stage, addressed with compile-time stage indices:
     // the compiler can then see that the DMA filling one stage does not alias
     // the reads of the other and need not drain it before reading.
@@ -455,26 +274,28 @@ __global__ __launch_bounds__(64 * WAVES, (KT == 16 && WAVES == 4) ? 2 : 1) void 
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.v + (int64_t)tile.tok0 * p.ldv + tile.kvh * HD), (short)0,
         ((tile.len - 1) * ldv + HD) * 4, 0x00020000);
-    // One DMA instruction moves one 1 KB key row of the tile; lane l fills
-    // chunk slot l (K: with global chunk l ^ (row % 16)).
-    int koff[ROWS_PER_WAVE], voff[ROWS_PER_WAVE];
+    // One DMA instruction moves RPI key rows (1 KB) of the tile: lane l
+    // fills chunk slot l % CPR of row l / CPR (K: with global chunk
+    // slot ^ (row % 16)).
+    int koff[INSTR_PER_WAVE], voff[INSTR_PER_WAVE];
 #pragma unroll
-    for (int q = 0; q < ROWS_PER_WAVE; ++q) {
-        const int r = wave * ROWS_PER_WAVE + q;
-        koff[q] = (r * ldk + 4 * (lane ^ (r & 15))) * 4;
-        voff[q] = (r * ldv + 4 * lane) * 4;
+    for (int q = 0; q < INSTR_PER_WAVE; ++q) {
+        const int r = (wave * INSTR_PER_WAVE + q) * RPI + lane / CPR;
+        const int slot = lane % CPR;
+        koff[q] = (r * ldk + 4 * (slot ^ (r & 15))) * 4;
+        voff[q] = (r * ldv + 4 * slot) * 4;
     }
     auto issue = [&](auto st, int k0) {
         float *kd = decltype(st)::value == 0 ? Ks0 : Ks1;
         float *vd = decltype(st)::value == 0 ? Vs0 : Vs1;
 #pragma unroll
-        for (int q = 0; q < ROWS_PER_WAVE; ++q) {
-            const int r = wave * ROWS_PER_WAVE + q;
+        for (int q = 0; q < INSTR_PER_WAVE; ++q) {
+            const int r0 = (wave * INSTR_PER_WAVE + q) * RPI;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rk, (__attribute__((address_space(3))) void *)&kd[r * HD], 16, koff[q],
+                rk, (__attribute__((address_space(3))) void *)&kd[r0 * HD], 16, koff[q],
                 k0 * ldk * 4, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rv, (__attribute__((address_space(3))) void *)&vd[r * HD], 16, voff[q],
+                rv, (__attribute__((address_space(3))) void *)&vd[r0 * HD], 16, voff[q],
                 k0 * ldv * 4, 0, 0);
         }
     };
@@ -678,50 +499,42 @@ int attn_block_vectors(int hd) {
     return (hd == 64 || hd == 128 || hd == 256) ? 32 * ATTN_WAVES : 0;
 }
 
+// 16x16x4 kernel with one key-tile width per head dim (so a vector's
+// arithmetic never depends on the launch): 16 keys at head_dim 256, 32 at
+// 128 and 64 at 64, each double buffered in 64 KB, so two 4-wave workgroups
+// share a CU. Grids of fewer than 128 work items split every item over 4 or
+// 8 workgroups of fewer waves.
+template <int HD, int KT>
+static hipError_t launch_attn16(const AttnArgs &a, hipStream_t s) {
+    const int64_t t = a.n_tiles;
+    if (2 * t >= 256)
+        hipLaunchKernelGGL((attn16_kernel<HD, 4, KT>), dim3((unsigned)(2 * t)), dim3(256), 0, s, a);
+    else if (4 * t >= 256)
+        hipLaunchKernelGGL((attn16_kernel<HD, 2, KT>), dim3((unsigned)(4 * t)), dim3(128), 0, s, a);
+    else
+        hipLaunchKernelGGL((attn16_kernel<HD, 1, KT>), dim3((unsigned)(8 * t)), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
     if (a.tokens <= 0) return hipSuccess;
     const dim3 block(64 * ATTN_WAVES);
+    // Buffer windows are per row: the longest row bounds the offsets.
+    const int64_t rows = a.max_len > 0 ? a.max_len : a.tokens;
+    const bool dma = rows * std::max(std::max(a.ldk, a.ldv), (int64_t)a.hd) * 4 < INT32_MAX;
     switch (a.hd) {
         case 64:
-            if (a.tokens * std::max(std::max(a.ldk, a.ldv), (int64_t)64) * 4 < INT32_MAX)
-                hipLaunchKernelGGL((attn_dma_kernel<64, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s, a);
-            else
-                hipLaunchKernelGGL((attn_mfma_kernel<64, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
-                                   a);
+            if (dma) return launch_attn16<64, 64>(a, s);
+            hipLaunchKernelGGL((attn_mfma_kernel<64, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s, a);
             return hipGetLastError();
         case 128:
-            if (a.tokens * std::max(std::max(a.ldk, a.ldv), (int64_t)128) * 4 < INT32_MAX)
-                hipLaunchKernelGGL((attn_dma_kernel<128, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
-                                   a);
-            else
-                hipLaunchKernelGGL((attn_mfma_kernel<128, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
-                                   a);
+            if (dma) return launch_attn16<128, 32>(a, s);
+            hipLaunchKernelGGL((attn_mfma_kernel<128, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s, a);
             return hipGetLastError();
-        case 256: {
-            // Buffer windows are per row: the longest row bounds the offsets.
-            const int64_t rows = a.max_len > 0 ? a.max_len : a.tokens;
-            if (rows * std::max(std::max(a.ldk, a.ldv), (int64_t)256) * 4 >= INT32_MAX) {
-                hipLaunchKernelGGL((attn_mfma_kernel<256, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s,
-                                   a);
-                return hipGetLastError();
-            }
-            // 16-key tiles double buffered in 64 KB: two workgroups of four
-            // waves (64 query vectors each) share a CU, so one's barrier and
-            // softmax stalls overlap the other's MFMAs. Smaller grids split a
-            // 128-vector work item over 4 or 8 workgroups of fewer waves; a
-            // vector's arithmetic is the same in every variant.
-            const int64_t t = a.n_tiles;
-            if (2 * t >= 256)
-                hipLaunchKernelGGL((attn_dma256_kernel<4, 16>), dim3((unsigned)(2 * t)), dim3(256),
-                                   0, s, a);
-            else if (4 * t >= 256)
-                hipLaunchKernelGGL((attn_dma256_kernel<2, 16>), dim3((unsigned)(4 * t)), dim3(128),
-                                   0, s, a);
-            else
-                hipLaunchKernelGGL((attn_dma256_kernel<1, 16>), dim3((unsigned)(8 * t)), dim3(64),
-                                   0, s, a);
+        case 256:
+            if (dma) return launch_attn16<256, 16>(a, s);
+            hipLaunchKernelGGL((attn_mfma_kernel<256, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s, a);
             return hipGetLastError();
-        }
         default:
             if (!a.pos || !a.rowlen) return hipErrorInvalidValue;
             hipLaunchKernelGGL(attn_simple_kernel, dim3((unsigned)(a.tokens * a.nh)), dim3(64), 0,
