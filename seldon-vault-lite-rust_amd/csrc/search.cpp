@@ -140,7 +140,7 @@ svl_status select_top(svl_vector_index *ix, int32_t nq, int64_t offset, int64_t 
     }
     if (most <= CAND_LDS) {
         HIP_TRY(sort_candidates_lds(ix->cand_key.p, ix->cand_idx.p, ix->cand_key_alt.p,
-                                    ix->cand_idx_alt.p, ix->cnt.p, nq, cap, s));
+                                    ix->cand_idx_alt.p, ix->cnt.p, nq, cap, most, s));
     } else {
         HIP_TRY(ix->seg_begin.ensure((size_t)nq));
         HIP_TRY(ix->seg_end.ensure((size_t)nq));

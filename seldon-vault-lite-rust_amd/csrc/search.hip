@@ -266,35 +266,87 @@ hipError_t rank_sort(const uint64_t *keys, uint64_t *keys_alt, uint32_t *idx, ui
 }
 
 // ---- top-K selection (offset + limit much smaller than the index) ---------------
-// Ascending bitonic sort of P keys (P a power of two, P / 2 a multiple of the
-// block size or smaller) held in LDS, by the whole block. With an index
-// array the order is (key, index) lexicographic, a total order when the
-// indices are distinct.
-template <int NT, bool WITH_IDX>
-__device__ void bitonic_lds(uint64_t *k, uint32_t *ix, int P) {
-    for (int size = 2; size <= P; size <<= 1) {
+// Ascending bitonic sort of 1024 * E keys by a block of 1024 threads, thread t
+// holding elements t * E .. t * E + E - 1 in registers. With indices the
+// order is (key, index) lexicographic, a total order when the indices are
+// distinct. Strides below E exchange in registers, strides below 64 E across
+// the wave with lane shuffles, and only the wider ones go through LDS (two
+// barriers each), so a 4096-key sort takes 10 LDS stages instead of 78.
+constexpr int SORT_THREADS = 1024;
+
+template <bool WITH_IDX>
+__device__ __forceinline__ bool key_less(uint64_t a, uint32_t ai, uint64_t b, uint32_t bi) {
+    return a < b || (WITH_IDX && a == b && ai < bi);
+}
+
+template <int E, bool WITH_IDX, int J>
+__device__ __forceinline__ void bitonic_in_thread(uint64_t (&k)[E], uint32_t (&x)[E], int size) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        if (e & J) continue;
+        const int f = e ^ J;
+        const bool asc = ((t * E + e) & size) == 0;
+        if (key_less<WITH_IDX>(k[f], x[f], k[e], x[e]) == asc) {
+            const uint64_t tk = k[e];
+            k[e] = k[f];
+            k[f] = tk;
+            if constexpr (WITH_IDX) {
+                const uint32_t tx = x[e];
+                x[e] = x[f];
+                x[f] = tx;
+            }
+        }
+    }
+}
+
+template <int E, bool WITH_IDX>
+__device__ __forceinline__ void bitonic_block(uint64_t (&k)[E], uint32_t (&x)[E], uint64_t *lk,
+                                              uint32_t *lx) {
+    const int t = threadIdx.x;
+    for (int size = 2; size <= SORT_THREADS * E; size <<= 1) {
         for (int j = size >> 1; j > 0; j >>= 1) {
-            for (int t = threadIdx.x; t < P / 2; t += NT) {
-                const int i = 2 * j * (t / j) + (t % j);
-                const int l = i + j;
-                const bool up = (i & size) == 0;
-                const uint64_t a = k[i], b = k[l];
-                bool gt;
-                if constexpr (WITH_IDX)
-                    gt = a > b || (a == b && ix[i] > ix[l]);
-                else
-                    gt = a > b;
-                if (gt == up) {
-                    k[i] = b;
-                    k[l] = a;
-                    if constexpr (WITH_IDX) {
-                        const uint32_t x = ix[i];
-                        ix[i] = ix[l];
-                        ix[l] = x;
-                    }
+            if (j < E) {
+                if (j == 1) bitonic_in_thread<E, WITH_IDX, 1>(k, x, size);
+                if constexpr (E > 2) if (j == 2) bitonic_in_thread<E, WITH_IDX, 2>(k, x, size);
+                if constexpr (E > 4) if (j == 4) bitonic_in_thread<E, WITH_IDX, 4>(k, x, size);
+                continue;
+            }
+            const int m = j / E;   // partner thread t ^ m
+            uint64_t ok[E];
+            uint32_t ox[E];
+            if (j < 64 * E) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    ok[e] = __shfl_xor(k[e], m, 64);
+                    if constexpr (WITH_IDX) ox[e] = __shfl_xor(x[e], m, 64);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    lk[t * E + e] = k[e];
+                    if constexpr (WITH_IDX) lx[t * E + e] = x[e];
+                }
+                __syncthreads();
+                const int p = t ^ m;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    ok[e] = lk[p * E + e];
+                    if constexpr (WITH_IDX) ox[e] = lx[p * E + e];
+                }
+                __syncthreads();
+            }
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const int i = t * E + e;
+                const bool want_min = ((i & j) == 0) == ((i & size) == 0);
+                const uint32_t oxe = WITH_IDX ? ox[e] : 0u;
+                const bool other_less = key_less<WITH_IDX>(ok[e], oxe, k[e], x[e]);
+                if (other_less == want_min) {
+                    k[e] = ok[e];
+                    if constexpr (WITH_IDX) x[e] = oxe;
                 }
             }
-            __syncthreads();
         }
     }
 }
@@ -302,17 +354,22 @@ __device__ void bitonic_lds(uint64_t *k, uint32_t *ix, int P) {
 // One block per query: its SAMPLE_COUNT samples, every stride-th key
 // (stride = n / SAMPLE_COUNT, so every sample position is below n), sorted
 // ascending into sorted[q * SAMPLE_COUNT ...].
-
-__global__ __launch_bounds__(1024) void sort_samples_kernel(const uint64_t *keys, int64_t n,
-                                                            int64_t stride, uint64_t *sorted) {
-    __shared__ uint64_t sk[SAMPLE_COUNT];
-    const int q = blockIdx.x;
-    for (int i = threadIdx.x; i < SAMPLE_COUNT; i += 1024)
-        sk[i] = keys[(int64_t)q * n + (int64_t)i * stride];
-    __syncthreads();
-    bitonic_lds<1024, false>(sk, nullptr, SAMPLE_COUNT);
-    for (int i = threadIdx.x; i < SAMPLE_COUNT; i += 1024)
-        sorted[(int64_t)q * SAMPLE_COUNT + i] = sk[i];
+__global__ __launch_bounds__(SORT_THREADS) void sort_samples_kernel(const uint64_t *keys,
+                                                                    int64_t n, int64_t stride,
+                                                                    uint64_t *sorted) {
+    constexpr int E = SAMPLE_COUNT / SORT_THREADS;
+    __shared__ uint64_t lk[SAMPLE_COUNT];
+    const int q = blockIdx.x, t = threadIdx.x;
+    uint64_t k[E];
+    uint32_t x[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        k[e] = keys[(int64_t)q * n + (int64_t)(t * E + e) * stride];
+        x[e] = 0;
+    }
+    bitonic_block<E, false>(k, x, lk, nullptr);
+#pragma unroll
+    for (int e = 0; e < E; ++e) sorted[(int64_t)q * SAMPLE_COUNT + t * E + e] = k[e];
 }
 
 // Candidates of query q: every admitted key <= sorted sample `rank`, in
@@ -457,36 +514,55 @@ hipError_t sort_candidates(const uint64_t *cand_key, const uint32_t *cand_idx, u
 }
 
 // Candidate lists of at most CAND_LDS entries: one block per query sorts
-// (key, position) pairs in LDS; positions are distinct, so this is the
-// order the stable key sort gives to candidates stored in position order.
-__global__ __launch_bounds__(1024) void sort_candidates_lds_kernel(
+// (key, position) pairs, padded with all-ones to 1024 * E entries (E from the
+// longest list of the launch); positions are distinct, so this is the order
+// the stable key sort gives to candidates stored in position order.
+template <int E>
+__global__ __launch_bounds__(SORT_THREADS) void sort_candidates_lds_kernel(
     const uint64_t *cand_key, const uint32_t *cand_idx, const unsigned int *cnt, int64_t cap,
     uint64_t *key_alt, uint32_t *idx_alt) {
-    __shared__ uint64_t sk[CAND_LDS];
-    __shared__ uint32_t si[CAND_LDS];
-    const int q = blockIdx.x;
-    const int c = (int)min<int64_t>(min<int64_t>((int64_t)cnt[q], cap), CAND_LDS);
-    int P = 2;
-    while (P < c) P <<= 1;
+    __shared__ uint64_t lk[SORT_THREADS * E];
+    __shared__ uint32_t lx[SORT_THREADS * E];
+    const int q = blockIdx.x, t = threadIdx.x;
+    const int c = (int)min<int64_t>(min<int64_t>((int64_t)cnt[q], cap), SORT_THREADS * E);
     const int64_t base = (int64_t)q * cap;
-    for (int i = threadIdx.x; i < P; i += 1024) {
-        sk[i] = i < c ? cand_key[base + i] : ~0ull;
-        si[i] = i < c ? cand_idx[base + i] : ~0u;
+    uint64_t k[E];
+    uint32_t x[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = t * E + e;
+        k[e] = i < c ? cand_key[base + i] : ~0ull;
+        x[e] = i < c ? cand_idx[base + i] : ~0u;
     }
-    __syncthreads();
-    bitonic_lds<1024, true>(sk, si, P);
-    for (int i = threadIdx.x; i < c; i += 1024) {
-        key_alt[base + i] = sk[i];
-        idx_alt[base + i] = si[i];
+    bitonic_block<E, true>(k, x, lk, lx);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int i = t * E + e;
+        if (i < c) {
+            key_alt[base + i] = k[e];
+            idx_alt[base + i] = x[e];
+        }
     }
 }
 
 hipError_t sort_candidates_lds(const uint64_t *cand_key, const uint32_t *cand_idx,
                                uint64_t *key_alt, uint32_t *idx_alt, const unsigned int *cnt,
-                               int nq, int64_t cap, hipStream_t s) {
+                               int nq, int64_t cap, int64_t most, hipStream_t s) {
     if (nq <= 0) return hipSuccess;
-    hipLaunchKernelGGL(sort_candidates_lds_kernel, dim3((unsigned)nq), dim3(1024), 0, s, cand_key,
-                       cand_idx, cnt, cap, key_alt, idx_alt);
+    if (most > CAND_LDS) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)nq), block(SORT_THREADS);
+    if (most <= SORT_THREADS)
+        hipLaunchKernelGGL((sort_candidates_lds_kernel<1>), grid, block, 0, s, cand_key, cand_idx,
+                           cnt, cap, key_alt, idx_alt);
+    else if (most <= 2 * SORT_THREADS)
+        hipLaunchKernelGGL((sort_candidates_lds_kernel<2>), grid, block, 0, s, cand_key, cand_idx,
+                           cnt, cap, key_alt, idx_alt);
+    else if (most <= 4 * SORT_THREADS)
+        hipLaunchKernelGGL((sort_candidates_lds_kernel<4>), grid, block, 0, s, cand_key, cand_idx,
+                           cnt, cap, key_alt, idx_alt);
+    else
+        hipLaunchKernelGGL((sort_candidates_lds_kernel<8>), grid, block, 0, s, cand_key, cand_idx,
+                           cnt, cap, key_alt, idx_alt);
     return hipGetLastError();
 }
 

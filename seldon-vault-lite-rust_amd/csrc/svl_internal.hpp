@@ -261,12 +261,13 @@ hipError_t launch_compact_keys(const uint64_t *keys, int nq, int64_t n,
                                const uint64_t *sorted_samples, int S, int rank, int64_t cap,
                                unsigned int *blk_count, unsigned int *cnt, uint64_t *cand_key,
                                uint32_t *cand_idx, hipStream_t s);
-// Candidates sorted in LDS when every query has at most CAND_LDS of them
-// (cnt[q] <= min(cap, CAND_LDS)), into key_alt / idx_alt.
+// Candidates sorted on chip when every query has at most CAND_LDS of them
+// (cnt[q] <= min(cap, most), most = the longest list <= CAND_LDS), into
+// key_alt / idx_alt.
 constexpr int CAND_LDS = 8192;
 hipError_t sort_candidates_lds(const uint64_t *cand_key, const uint32_t *cand_idx,
                                uint64_t *key_alt, uint32_t *idx_alt, const unsigned int *cnt,
-                               int nq, int64_t cap, hipStream_t s);
+                               int nq, int64_t cap, int64_t most, hipStream_t s);
 // Stable sort of each query's candidates by key into key_alt / idx_alt.
 hipError_t sort_candidates(const uint64_t *cand_key, const uint32_t *cand_idx, uint64_t *key_alt,
                            uint32_t *idx_alt, const unsigned int *cnt, unsigned int *begin,
