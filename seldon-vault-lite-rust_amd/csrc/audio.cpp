@@ -78,7 +78,7 @@ struct svl_audio_model {
     DevBuf<float> mel, l0, col, l1, h, n, tmp, act, qkv, att, gated, proj, projn, soft;
     DevBuf<uint8_t> mask, mask0, mask1;
     DevBuf<SscpRow> rows0, rows1;
-    DevBuf<int32_t> pos, rowlen, valid_idx;
+    DevBuf<int32_t> pos, rowlen, valid_idx, att_blocks;
     DevBuf<int64_t> offsets;
     DevBuf<int> flag;
     int *h_flag = nullptr;
@@ -94,7 +94,7 @@ struct svl_audio_model {
         act.release(); qkv.release(); att.release(); gated.release(); proj.release();
         projn.release(); soft.release(); mask.release(); mask0.release(); mask1.release();
         rows0.release(); rows1.release(); pos.release(); rowlen.release(); valid_idx.release();
-        offsets.release(); flag.release();
+        att_blocks.release(); offsets.release(); flag.release();
         if (h_flag) (void)hipHostFree(h_flag);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -245,6 +245,7 @@ struct AuBatch {
     std::vector<SscpRow> rows0, rows1;
     std::vector<uint8_t> mask0, mask1;
     std::vector<int32_t> valid_idx;
+    std::vector<int32_t> att_blocks;  // first row of each attention block
 };
 
 // Validation in the order AudioModel::forward meets each condition
@@ -276,6 +277,7 @@ svl_status prepare_clips(const svl_audio_model *m, const svl_mel *mels, int32_t 
             b.rows0.push_back({(int32_t)b.frame_off.back(), (int32_t)t, (int32_t)F});
             b.mask0.push_back(2 * t < F ? (uint8_t)(mel.mask[2 * t] != 0) : (uint8_t)0);
         }
+        for (int64_t t = 0; t < f2; t += m->chunk) b.att_blocks.push_back((int32_t)(b.row_off.back() + t));
         int64_t tok = 0;
         for (int64_t t = 0; t < f2; ++t) {
             b.rows1.push_back({(int32_t)row0_off, (int32_t)t, (int32_t)f1});
@@ -327,6 +329,7 @@ svl_status ensure_au_workspace(svl_audio_model *m, const AuBatch &b) {
     HIP_TRY(m->pos.ensure(T));
     HIP_TRY(m->rowlen.ensure(T));
     HIP_TRY(m->valid_idx.ensure(N));
+    HIP_TRY(m->att_blocks.ensure(std::max<size_t>(b.att_blocks.size(), 1)));
     HIP_TRY(m->offsets.ensure((size_t)b.B + 1));
     HIP_TRY(m->flag.ensure(1));
     return SVL_OK;
@@ -340,6 +343,8 @@ svl_status upload_au_meta(svl_audio_model *m, const AuBatch &b, hipStream_t s) {
     HIP_TRY(hipMemcpyAsync(m->mask0.p, b.mask0.data(), b.mask0.size(), hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(m->mask1.p, b.mask1.data(), b.mask1.size(), hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(m->valid_idx.p, b.valid_idx.data(), b.valid_idx.size() * 4,
+                           hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(m->att_blocks.p, b.att_blocks.data(), b.att_blocks.size() * 4,
                            hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(m->offsets.p, b.row_off.data(), b.row_off.size() * 8,
                            hipMemcpyHostToDevice, s));
@@ -431,7 +436,8 @@ svl_status enqueue_audio(svl_audio_model *m, const AuBatch &b, const float *d_me
             a.rowlen = m->rowlen.p;
             a.out = m->att.p;
             a.ldo = H;
-            a.rows = T;
+            a.blocks = m->att_blocks.p;
+            a.n_blocks = (int64_t)b.att_blocks.size();
             a.heads = (int)m->NH;
             a.head_dim = (int)m->hd;
             a.chunk = (int)m->chunk;

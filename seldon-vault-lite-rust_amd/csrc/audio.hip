@@ -271,98 +271,289 @@ hipError_t launch_audio_rows(const float *x, float c1, const float *w1, const fl
 }
 
 // ---- chunked local attention ---------------------------------------------
-// One wave per (row, head). Lane l holds head dims l, l+64, ... of the
-// scaled query (q * qf[d], qf = q_scale * softplus(per_dim_scale)) and keys
-// are scaled by k_scale as they are read. Context entry ci of the row's block
-// is key block*chunk + ci - (left-1) of the same clip; it is valid when that
-// key is in the clip, unmasked, and 0 <= query - key < left - 1. The score
-// is tanh((q.k + q.relk[ci - offset]) / cap) * cap; lane ci keeps score ci
-// (context <= 64). Masked query rows get zeros.
-__global__ __launch_bounds__(256) void audio_attn_kernel(AudioAttnArgs p) {
-    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (wid >= p.rows * p.heads) return;
-    const int64_t i = wid / p.heads;
-    const int h = (int)(wid - i * p.heads);
-    const int hd = p.head_dim;
-    float *orow = p.out + i * p.ldo + (int64_t)h * hd;
-    if (!p.mask[i]) {
-        for (int d = lane; d < hd; d += 64) orow[d] = 0.0f;
-        return;
-    }
-    const int il = p.pos[i], len = p.rowlen[i];
-    const int64_t base = i - il;
-    const int block = il / p.chunk, off = il - block * p.chunk;
+// One wave per (block of `chunk` query rows of a clip, head): every query of
+// a block shares the same `context` keys and values, so the wave stages them
+// once in LDS (keys scaled by k_scale, key rows padded to an odd number of
+// 16-byte chunks so lanes reading different rows at one column hit different
+// banks), together with the head's relative-position keys and the block's
+// queries (scaled by qf[d] = q_scale * softplus(per_dim_scale[d])). All
+// global loads are issued up front; the rest runs out of LDS.
+//
+// Scores: lane (g, ci) = (lane / KL, lane % KL) takes context entry ci for
+// queries g, g + G, g + 2G, ... of the sub-block (G = 64 / KL query groups,
+// QPL queries per lane). Context entry ci is key block*chunk + ci - (left-1)
+// of the clip; it is valid for query row il when the key is in the clip,
+// unmasked, and 0 <= il - key < left - 1. The score is
+// tanh((q.k + q.relk[ci - offset]) / cap) * cap, each dot summed over d in
+// order, the relative term only when 0 <= ci - offset < positions; invalid
+// entries score -1e9. Each query's softmax reduces over its KL lanes.
+//
+// Values: lane t holds head dims t, t + 64, ...; for each context entry in
+// order, every query adds weight * v (keys outside the clip are skipped; a
+// zero weight adds an exact zero, as the values are finite). A masked query
+// row, or one with no valid key, gets zeros.
+//
+// AW waves share one workgroup and its staged keys, values and relative
+// keys; wave w takes query sub-blocks w, w + AW, ... of QB queries each.
+constexpr int AW = 2;
+
+// Elements 4c .. 4c+3 of a row of `hd` floats, zero past the end.
+__device__ __forceinline__ f32x4 load_row4(const float *row, int c, int hd, bool vec) {
+    if (vec) return ((const f32x4 *)row)[c];
+    f32x4 r = {0.f, 0.f, 0.f, 0.f};
+    if (4 * c + 0 < hd) r.x = row[4 * c + 0];
+    if (4 * c + 1 < hd) r.y = row[4 * c + 1];
+    if (4 * c + 2 < hd) r.z = row[4 * c + 2];
+    if (4 * c + 3 < hd) r.w = row[4 * c + 3];
+    return r;
+}
+
+template <int KL, int QPL, int TD>
+__global__ __launch_bounds__(64 * AW) void audio_attn_kernel(AudioAttnArgs p) {
+    constexpr int G = 64 / KL, QB = QPL * G;
+    extern __shared__ f32x4 lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int blk = (int)(blockIdx.x / (unsigned)p.heads);
+    const int h = (int)blockIdx.x - blk * p.heads;
+    const int64_t r0 = p.blocks[blk];
+    const int il0 = p.pos[r0], len = p.rowlen[r0];
+    const int64_t base = r0 - il0;
+    const int nq = min(p.chunk, len - il0);
+    const int hd = p.head_dim, hd4 = (hd + 3) >> 2, rs = hd4 | 1;
     const int max_past = p.left - 1, left_window = p.left - 1;
-    const float *qrow = p.q + i * p.ldq + (int64_t)h * hd;
-    float q[4];  // hd <= 256
+    const int kfirst = il0 - max_past;  // clip row of context entry 0
+    f32x4 *ks = lds;
+    f32x4 *rk = ks + p.context * rs;
+    f32x4 *vs = rk + p.positions * rs;
+    f32x4 *qs = vs + p.context * hd4 + wave * QB * hd4;
+    // 16-byte loads when every row start is 16-byte aligned
+    const bool vec = (hd & 3) == 0 && ((p.ldq | p.ldk | p.ldv) & 3) == 0 &&
+                     (((uintptr_t)p.q | (uintptr_t)p.k | (uintptr_t)p.v | (uintptr_t)p.relk |
+                       (uintptr_t)p.qf) & 15) == 0;
+
+    // Staging issues SB loads per thread before any LDS store, so their
+    // latencies overlap.
+    constexpr int SB = 4, NT = 64 * AW;
+    const int nkv = p.context * hd4;
+    for (int i0 = threadIdx.x; i0 < nkv; i0 += SB * NT) {
+        f32x4 kv[SB], vv[SB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int d = lane + 64 * j;
-        q[j] = d < hd ? qrow[d] * p.qf[d] : 0.0f;
+        for (int u = 0; u < SB; ++u) {
+            const int idx = i0 + u * NT;
+            kv[u] = vv[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int ci = idx / hd4, c = idx - ci * hd4, kl = kfirst + ci;
+            if (idx < nkv && kl >= 0 && kl < len) {
+                kv[u] = load_row4(p.k + (base + kl) * p.ldk + (int64_t)h * hd, c, hd, vec);
+                vv[u] = load_row4(p.v + (base + kl) * p.ldv + (int64_t)h * hd, c, hd, vec);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+            const int idx = i0 + u * NT;
+            const int ci = idx / hd4, c = idx - ci * hd4;
+            if (idx < nkv) {
+                ks[ci * rs + c] = kv[u] * p.k_scale;
+                vs[ci * hd4 + c] = vv[u];
+            }
+        }
     }
-    float my = -INFINITY;
-    for (int ci = 0; ci < p.context; ++ci) {
-        const int kl = block * p.chunk + ci - max_past;
-        const bool valid = kl >= 0 && kl < len && p.mask[base + kl] && il - kl >= 0 &&
-                           il - kl < left_window;
-        float score = -1.0e9f;
-        if (valid) {
-            const float *krow = p.k + (base + kl) * p.ldk + (int64_t)h * hd;
-            const int rel = ci - off;
-            const bool has_rel = rel >= 0 && rel < p.positions;
-            const float *rrow = p.relk + ((int64_t)(has_rel ? rel : 0) * p.heads + h) * hd;
-            float part = 0.f;
+    const int nr = p.positions * hd4;
+    for (int i0 = threadIdx.x; i0 < nr; i0 += SB * NT) {
+        f32x4 rv[SB];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int d = lane + 64 * j;
-                if (d < hd) {
-                    part += q[j] * (krow[d] * p.k_scale);
-                    if (has_rel) part += q[j] * rrow[d];
+        for (int u = 0; u < SB; ++u) {
+            const int idx = i0 + u * NT;
+            const int pi = idx / hd4, c = idx - pi * hd4;
+            rv[u] = idx < nr ? load_row4(p.relk + ((int64_t)pi * p.heads + h) * hd, c, hd, vec)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+            const int idx = i0 + u * NT;
+            const int pi = idx / hd4, c = idx - pi * hd4;
+            if (idx < nr) rk[pi * rs + c] = rv[u];
+        }
+    }
+    // This wave's queries q0 .. q0 + nb - 1 (zeros for the rest of the sub-block).
+    auto stage_queries = [&](int q0, int nb) {
+        for (int i0 = lane; i0 < QB * hd4; i0 += SB * 64) {
+            f32x4 qv[SB];
+#pragma unroll
+            for (int u = 0; u < SB; ++u) {
+                const int idx = i0 + u * 64;
+                const int qi = idx / hd4, c = idx - qi * hd4;
+                qv[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (idx < QB * hd4 && qi < nb)
+                    qv[u] = load_row4(p.q + (r0 + q0 + qi) * p.ldq + (int64_t)h * hd, c, hd, vec) *
+                            load_row4(p.qf, c, hd, vec);
+            }
+#pragma unroll
+            for (int u = 0; u < SB; ++u) {
+                const int idx = i0 + u * 64;
+                if (idx < QB * hd4) qs[idx] = qv[u];
+            }
+        }
+    };
+
+    const int ci = lane % KL, g = lane / KL;
+    const int crow = min(ci, p.context - 1) * rs;
+    const int kl = kfirst + ci;
+    const bool key_ok = ci < p.context && kl >= 0 && kl < len && p.mask[base + kl];
+    bool ok = true;
+    stage_queries(wave * QB, min(QB, nq - wave * QB));
+    // Every wave runs the same number of iterations (the barriers); a wave
+    // past the block's last query has nb <= 0 and writes nothing.
+    for (int qb0 = 0; qb0 < nq; qb0 += AW * QB) {
+        const int q0 = qb0 + wave * QB;
+        const int nb = min(QB, nq - q0);
+        if (qb0 > 0) {
+            __syncthreads();  // the previous sub-block's queries consumed
+            stage_queries(q0, nb);
+        }
+        __syncthreads();
+        int rrow[QPL];
+        float sk[QPL], sr[QPL];
+#pragma unroll
+        for (int j = 0; j < QPL; ++j) {
+            const int rel = ci - (q0 + g + G * j);
+            rrow[j] = min(max(rel, 0), p.positions - 1) * rs;
+            sk[j] = 0.f;
+            sr[j] = 0.f;
+        }
+        for (int c = 0; c < hd4; ++c) {
+            const f32x4 kv = ks[crow + c];
+#pragma unroll
+            for (int j = 0; j < QPL; ++j) {
+                const f32x4 qv = qs[(g + G * j) * hd4 + c];
+                const f32x4 rv = rk[rrow[j] + c];
+                sk[j] += qv.x * kv.x;
+                sk[j] += qv.y * kv.y;
+                sk[j] += qv.z * kv.z;
+                sk[j] += qv.w * kv.w;
+                sr[j] += qv.x * rv.x;
+                sr[j] += qv.y * rv.y;
+                sr[j] += qv.z * rv.z;
+                sr[j] += qv.w * rv.w;
+            }
+        }
+        float wgt[QPL];
+        bool live[QPL];
+#pragma unroll
+        for (int j = 0; j < QPL; ++j) {
+            const int q = g + G * j;
+            const int il = il0 + q0 + q;
+            const int rel = ci - (q0 + q);
+            const bool valid = q < nb && key_ok && il - kl >= 0 && il - kl < left_window;
+            float score = -1.0e9f;
+            if (valid) {
+                const float dot = (rel >= 0 && rel < p.positions) ? sk[j] + sr[j] : sk[j];
+                score = tanhf(dot / p.cap) * p.cap;
+            }
+            float m = ci < p.context ? score : -INFINITY;
+#pragma unroll
+            for (int o = KL / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, KL));
+            const float e = ci < p.context ? expf(score - m) : 0.0f;
+            float sum = e;
+#pragma unroll
+            for (int o = KL / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, KL);
+            live[j] = q < nb && p.mask[r0 + q0 + q] && !(m <= -1.0e9f / 2.0f);
+            if (live[j] && !(isfinite(sum) && sum > 0.0f)) ok = false;
+            wgt[j] = e / sum;
+        }
+        float acc[QB][TD];
+#pragma unroll
+        for (int q = 0; q < QB; ++q)
+#pragma unroll
+            for (int t = 0; t < TD; ++t) acc[q][t] = 0.f;
+        for (int c = 0; c < p.context; ++c) {
+            const int kc = kfirst + c;
+            if (kc < 0 || kc >= len) continue;
+            const float *vr = (const float *)(vs + c * hd4);
+            float vv[TD];
+#pragma unroll
+            for (int t = 0; t < TD; ++t) vv[t] = lane + 64 * t < hd ? vr[lane + 64 * t] : 0.f;
+#pragma unroll
+            for (int j = 0; j < QPL; ++j)
+#pragma unroll
+                for (int gg = 0; gg < G; ++gg) {
+                    const int q = gg + G * j;
+                    if (q >= nb) continue;
+                    const float w = __int_as_float(
+                        __builtin_amdgcn_readlane(__float_as_int(wgt[j]), c + KL * gg));
+#pragma unroll
+                    for (int t = 0; t < TD; ++t) acc[q][t] += w * vv[t];
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < QPL; ++j)
+#pragma unroll
+            for (int gg = 0; gg < G; ++gg) {
+                const int q = gg + G * j;
+                if (q >= nb) continue;
+                const bool on = __builtin_amdgcn_readlane((int)live[j], KL * gg) != 0;
+                float *orow = p.out + (r0 + q0 + q) * p.ldo + (int64_t)h * hd;
+#pragma unroll
+                for (int t = 0; t < TD; ++t) {
+                    const int d = lane + 64 * t;
+                    if (d < hd) {
+                        const float y = on ? acc[q][t] : 0.0f;
+                        ok = ok && isfinite(y);
+                        orow[d] = y;
+                    }
                 }
             }
-            const float dot = wave_sum(part);
-            score = tanhf(dot / p.cap) * p.cap;
-        }
-        if (lane == ci) my = score;
-    }
-    const float maximum = wave_max(lane < p.context ? my : -INFINITY);
-    if (maximum <= -1.0e9f / 2.0f) {
-        for (int d = lane; d < hd; d += 64) orow[d] = 0.0f;
-        return;
-    }
-    const float e = lane < p.context ? expf(my - maximum) : 0.0f;
-    const float sum = wave_sum(e);
-    bool ok = isfinite(sum) && sum > 0.0f;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int ci = 0; ci < p.context; ++ci) {
-        const float wgt = __shfl(e, ci, 64) / sum;
-        const int kl = block * p.chunk + ci - max_past;
-        if (wgt == 0.0f || kl < 0 || kl >= len) continue;
-        const float *vrow = p.v + (base + kl) * p.ldv + (int64_t)h * hd;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int d = lane + 64 * j;
-            if (d < hd) acc[j] += wgt * vrow[d];
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int d = lane + 64 * j;
-        if (d < hd) {
-            ok = ok && isfinite(acc[j]);
-            orow[d] = acc[j];
-        }
     }
     if (!ok) raise_flag(p.flag, FLAG_NONFINITE);
 }
 
-hipError_t launch_audio_attention(const AudioAttnArgs &a, hipStream_t s) {
-    if (a.rows <= 0) return hipSuccess;
-    if (a.head_dim > 256 || a.context > 64) return hipErrorInvalidValue;
-    const int64_t waves = a.rows * a.heads;
-    hipLaunchKernelGGL(audio_attn_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, a);
+size_t audio_attention_lds(const AudioAttnArgs &a, int qb) {
+    const int hd4 = (a.head_dim + 3) / 4, rs = hd4 | 1;
+    return (size_t)((a.context + a.positions) * rs + (a.context + AW * qb) * hd4) * sizeof(f32x4);
+}
+
+template <int KL, int QPL, int TD>
+hipError_t launch_audio_attn(const AudioAttnArgs &a, hipStream_t s) {
+    const size_t lds = audio_attention_lds(a, QPL * (64 / KL));
+    if (lds > 64 * 1024) {
+        const hipError_t e = hipFuncSetAttribute((const void *)audio_attn_kernel<KL, QPL, TD>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((audio_attn_kernel<KL, QPL, TD>), dim3((unsigned)(a.n_blocks * a.heads)),
+                       dim3(64 * AW), lds, s, a);
     return hipGetLastError();
+}
+
+template <int KL, int TD>
+hipError_t launch_audio_attn_q(const AudioAttnArgs &a, hipStream_t s) {
+    // Queries per lane: enough for one block in one pass of the AW waves,
+    // up to 8 (longer blocks take several passes).
+    const int per = AW * (64 / KL);
+    const int need = (a.chunk + per - 1) / per;
+    if (need <= 1) return launch_audio_attn<KL, 1, TD>(a, s);
+    if (need <= 2) return launch_audio_attn<KL, 2, TD>(a, s);
+    if (need <= 3) return launch_audio_attn<KL, 3, TD>(a, s);
+    if (need <= 4) return launch_audio_attn<KL, 4, TD>(a, s);
+    return launch_audio_attn<KL, 8, TD>(a, s);
+}
+
+template <int KL>
+hipError_t launch_audio_attn_d(const AudioAttnArgs &a, hipStream_t s) {
+    switch ((a.head_dim + 63) / 64) {
+        case 1: return launch_audio_attn_q<KL, 1>(a, s);
+        case 2: return launch_audio_attn_q<KL, 2>(a, s);
+        case 3: return launch_audio_attn_q<KL, 3>(a, s);
+        default: return launch_audio_attn_q<KL, 4>(a, s);
+    }
+}
+
+hipError_t launch_audio_attention(const AudioAttnArgs &a, hipStream_t s) {
+    if (a.n_blocks <= 0) return hipSuccess;
+    if (a.head_dim < 1 || a.head_dim > 256 || a.context < 1 || a.context > 64 || a.chunk < 1 ||
+        a.positions < 1 || a.heads < 1 || a.n_blocks * a.heads > INT32_MAX)
+        return hipErrorInvalidValue;
+    return a.context <= 32 ? launch_audio_attn_d<32>(a, s) : launch_audio_attn_d<64>(a, s);
 }
 
 // ---- light convolution: causal depthwise conv + clamp + RMSNorm + SiLU -------

@@ -190,7 +190,8 @@ struct AudioAttnArgs {
     const int32_t *pos, *rowlen; // row index within its clip, clip length
     float *out;
     int64_t ldo;
-    int64_t rows;
+    const int32_t *blocks;       // first row of each block of `chunk` rows of a clip
+    int64_t n_blocks;
     int heads, head_dim, chunk, left, context, positions;
     int *flag;
 };
