@@ -22,65 +22,80 @@ constexpr int FREQ0 = 64;  // after the first stride-2 convolution
 constexpr int FREQ1 = 32;  // after the second
 
 // ---- subsampling convolution 0: 1 -> C0 channels + LayerNorm + ReLU -------
-// One wave per (layer-0 row, frequency); lane l holds channels l, l+64, ...
-template <int NCH>
+// One workgroup per layer-0 row: the three mel rows it reads (zero where the
+// tap is outside the clip, masked or past the 128 bins) and the 3x3 weights
+// go to LDS; four threads per output frequency, each with CPT consecutive
+// channels. Each channel sums its nine taps in (kernel row, kernel column)
+// order; the LayerNorm sums reduce over the four threads.
+constexpr int SSCP_TAPS_W = MEL_BINS + 2;  // one zero column on each side
+
+template <int CPT>
 __global__ __launch_bounds__(256) void sscp_conv0_kernel(const float *__restrict__ mel,
                                                          const uint8_t *__restrict__ mask,
                                                          const SscpRow *__restrict__ rows,
-                                                         int64_t n_rows, const float *__restrict__ w,
+                                                         const float *__restrict__ w,
                                                          const float *__restrict__ ln, int C0,
                                                          float eps, float *__restrict__ out,
                                                          int *flag) {
-    const int64_t pos = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (pos >= n_rows * FREQ0) return;
-    const int64_t r = pos / FREQ0;
-    const int f = (int)(pos - r * FREQ0);
+    __shared__ float taps[3][SSCP_TAPS_W];
+    __shared__ float ws[4 * CPT * 9];
+    const int64_t r = blockIdx.x;
     const SscpRow ri = rows[r];
+    for (int i = threadIdx.x; i < C0 * 9; i += 256) ws[i] = w[i];
+    for (int i = threadIdx.x; i < 3 * SSCP_TAPS_W; i += 256) {
+        const int kt = i / SSCP_TAPS_W, x = i - kt * SSCP_TAPS_W, iff = x - 1;
+        const int it = 2 * ri.t + kt - 1;
+        const bool in = it >= 0 && it < ri.len && iff >= 0 && iff < MEL_BINS && mask[ri.base + it];
+        taps[kt][x] = in ? mel[(int64_t)(ri.base + it) * MEL_BINS + iff] : 0.0f;
+    }
+    __syncthreads();
+    const int f = threadIdx.x >> 2, c0 = (threadIdx.x & 3) * CPT;
     float tap[9];
 #pragma unroll
     for (int kt = 0; kt < 3; ++kt)
 #pragma unroll
-        for (int kf = 0; kf < 3; ++kf) {
-            const int it = 2 * ri.t + kt - 1, iff = 2 * f + kf - 1;
-            const bool ok = it >= 0 && it < ri.len && iff >= 0 && iff < MEL_BINS &&
-                            mask[ri.base + it];
-            tap[kt * 3 + kf] = ok ? mel[(int64_t)(ri.base + it) * MEL_BINS + iff] : 0.0f;
-        }
-    float v[NCH];
-    float s = 0.f;
+        for (int kf = 0; kf < 3; ++kf) tap[kt * 3 + kf] = taps[kt][2 * f + kf];
+    float v[CPT];
+    float sum = 0.f;
     bool ok = true;
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-        const int c = lane + 64 * j;
-        v[j] = 0.f;
-        if (c < C0) {
-            float acc = 0.0f;
+    for (int j = 0; j < CPT; ++j) {
+        float acc = 0.0f;
+        if (c0 + j < C0) {
 #pragma unroll
-            for (int k = 0; k < 9; ++k) acc += tap[k] * w[c * 9 + k];
-            v[j] = acc;
+            for (int k = 0; k < 9; ++k) acc += tap[k] * ws[(c0 + j) * 9 + k];
             ok = ok && isfinite(acc);
-            s += acc;
+            sum += acc;
         }
+        v[j] = acc;
     }
-    const float mean = wave_sum(s) / (float)C0;
+    sum += __shfl_xor(sum, 1, 4);
+    sum += __shfl_xor(sum, 2, 4);
+    const float mean = sum / (float)C0;
     float var = 0.f;
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-        const int c = lane + 64 * j;
-        if (c < C0) {
+    for (int j = 0; j < CPT; ++j)
+        if (c0 + j < C0) {
             const float d = v[j] - mean;
             var += d * d;
         }
-    }
-    var = wave_sum(var) / (float)C0;
+    var += __shfl_xor(var, 1, 4);
+    var += __shfl_xor(var, 2, 4);
+    var = var / (float)C0;
     const float inv = 1.0f / sqrtf(var + eps);
     ok = ok && isfinite(inv);
-    float *o = out + pos * C0;
+    float *o = out + (r * FREQ0 + f) * C0 + c0;
+    if (CPT % 4 == 0 && C0 == 4 * CPT) {
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-        const int c = lane + 64 * j;
-        if (c < C0) o[c] = fmaxf((v[j] - mean) * inv * ln[c], 0.0f);
+        for (int j = 0; j < CPT; j += 4)
+            *(f32x4 *)(o + j) = f32x4{fmaxf((v[j] - mean) * inv * ln[c0 + j], 0.0f),
+                                      fmaxf((v[j + 1] - mean) * inv * ln[c0 + j + 1], 0.0f),
+                                      fmaxf((v[j + 2] - mean) * inv * ln[c0 + j + 2], 0.0f),
+                                      fmaxf((v[j + 3] - mean) * inv * ln[c0 + j + 3], 0.0f)};
+    } else {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j)
+            if (c0 + j < C0) o[j] = fmaxf((v[j] - mean) * inv * ln[c0 + j], 0.0f);
     }
     if (!ok) raise_flag(flag, FLAG_NONFINITE);
 }
@@ -89,14 +104,19 @@ hipError_t launch_sscp_conv0(const float *mel, const uint8_t *mask, const SscpRo
                              int64_t n_rows, const float *w, const float *ln, int C0, float eps,
                              float *out, int *flag, hipStream_t s) {
     if (n_rows <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((n_rows * FREQ0 + 3) / 4));
-    switch ((C0 + 63) / 64) {
-        case 1: hipLaunchKernelGGL(sscp_conv0_kernel<1>, grid, dim3(256), 0, s, mel, mask, rows, n_rows, w, ln, C0, eps, out, flag); break;
-        case 2: hipLaunchKernelGGL(sscp_conv0_kernel<2>, grid, dim3(256), 0, s, mel, mask, rows, n_rows, w, ln, C0, eps, out, flag); break;
-        case 3: case 4: hipLaunchKernelGGL(sscp_conv0_kernel<4>, grid, dim3(256), 0, s, mel, mask, rows, n_rows, w, ln, C0, eps, out, flag); break;
-        case 5: case 6: case 7: case 8: hipLaunchKernelGGL(sscp_conv0_kernel<8>, grid, dim3(256), 0, s, mel, mask, rows, n_rows, w, ln, C0, eps, out, flag); break;
-        default: return hipErrorInvalidValue;
-    }
+    if (n_rows > INT32_MAX || C0 < 1) return hipErrorInvalidValue;
+    static_assert(FREQ0 * 4 == 256, "four threads per output frequency");
+#define C0_LAUNCH(CPT)                                                                       \
+    hipLaunchKernelGGL(sscp_conv0_kernel<CPT>, dim3((unsigned)n_rows), dim3(256), 0, s, mel, \
+                       mask, rows, w, ln, C0, eps, out, flag)
+    const int cpt = (C0 + 3) / 4;
+    if (cpt <= 8) C0_LAUNCH(8);
+    else if (cpt <= 16) C0_LAUNCH(16);
+    else if (cpt <= 32) C0_LAUNCH(32);
+    else if (cpt <= 64) C0_LAUNCH(64);
+    else if (cpt <= 128) C0_LAUNCH(128);
+    else return hipErrorInvalidValue;
+#undef C0_LAUNCH
     return hipGetLastError();
 }
 
@@ -105,20 +125,26 @@ hipError_t launch_sscp_conv0(const float *mel, const uint8_t *mask, const SscpRo
 // where the tap is outside the clip, masked or outside the 64 frequencies:
 // the k order of the layer-1 weight [C1][C0][3][3], so the GEMM against it
 // sums each output in the reference's (channel, row, column) order. One
-// thread per (output position, input channel): coalesced reads over ic.
+// thread per (output position, group of four input channels): nine 16-byte
+// loads, one per tap, coalesced over the channel groups of a layer-0 row,
+// and nine 16-byte stores of the thread's 36 contiguous columns (channel
+// major, tap minor: a register transpose of the loads). Channel counts that
+// are not a multiple of four take the same path element by element.
 __global__ __launch_bounds__(256) void sscp_im2col_kernel(const float *__restrict__ l0,
                                                           const uint8_t *__restrict__ mask0,
                                                           const SscpRow *__restrict__ rows,
-                                                          int64_t n_rows, int C0,
+                                                          int64_t n_pos, int C0,
                                                           float *__restrict__ col) {
+    const int groups = (C0 + 3) >> 2;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= n_rows * FREQ1 * C0) return;
-    const int ic = (int)(idx % C0);
-    const int64_t pos = idx / C0;
+    if (idx >= n_pos * groups) return;
+    const int64_t pos = idx / groups;
+    const int ic0 = 4 * (int)(idx - pos * groups);
     const int64_t r = pos / FREQ1;
     const int f = (int)(pos - r * FREQ1);
     const SscpRow ri = rows[r];
-    float *dst = col + pos * (int64_t)(9 * C0) + ic * 9;
+    const bool vec = (C0 & 3) == 0;
+    f32x4 tap[9];
 #pragma unroll
     for (int kt = 0; kt < 3; ++kt) {
         const int it = 2 * ri.t + kt - 1;
@@ -126,18 +152,51 @@ __global__ __launch_bounds__(256) void sscp_im2col_kernel(const float *__restric
 #pragma unroll
         for (int kf = 0; kf < 3; ++kf) {
             const int iff = 2 * f + kf - 1;
-            const bool ok = row_ok && iff >= 0 && iff < FREQ0;
-            dst[kt * 3 + kf] = ok ? l0[((int64_t)(ri.base + it) * FREQ0 + iff) * C0 + ic] : 0.0f;
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (row_ok && iff >= 0 && iff < FREQ0) {
+                const float *src = l0 + ((int64_t)(ri.base + it) * FREQ0 + iff) * C0 + ic0;
+                if (vec) {
+                    v = *(const f32x4 *)src;
+                } else {
+                    if (ic0 + 0 < C0) v.x = src[0];
+                    if (ic0 + 1 < C0) v.y = src[1];
+                    if (ic0 + 2 < C0) v.z = src[2];
+                    if (ic0 + 3 < C0) v.w = src[3];
+                }
+            }
+            tap[kt * 3 + kf] = v;
         }
+    }
+    // out[j * 9 + t] = channel ic0 + j of tap t, for the 36 columns from ic0 * 9
+    float o[36];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+        o[0 * 9 + t] = tap[t].x;
+        o[1 * 9 + t] = tap[t].y;
+        o[2 * 9 + t] = tap[t].z;
+        o[3 * 9 + t] = tap[t].w;
+    }
+    float *dst = col + pos * (int64_t)(9 * C0) + 9 * ic0;
+    if (vec) {
+#pragma unroll
+        for (int u = 0; u < 9; ++u)
+            ((f32x4 *)dst)[u] = f32x4{o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]};
+    } else {
+        const int n = 9 * (C0 - ic0 < 4 ? C0 - ic0 : 4);
+#pragma unroll
+        for (int u = 0; u < 36; ++u)
+            if (u < n) dst[u] = o[u];
     }
 }
 
 hipError_t launch_sscp_im2col(const float *l0, const uint8_t *mask0, const SscpRow *rows,
                               int64_t n_rows, int C0, float *col, hipStream_t s) {
-    const int64_t n = n_rows * FREQ1 * C0;
-    if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(sscp_im2col_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, l0,
-                       mask0, rows, n_rows, C0, col);
+    const int64_t n = n_rows * FREQ1;
+    if (n <= 0 || C0 <= 0) return hipSuccess;
+    const int64_t threads = n * ((C0 + 3) / 4);
+    if ((threads + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(sscp_im2col_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       s, l0, mask0, rows, n, C0, col);
     return hipGetLastError();
 }
 
