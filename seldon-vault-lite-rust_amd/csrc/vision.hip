@@ -155,6 +155,67 @@ __global__ __launch_bounds__(256) void qkv_post_axial_kernel(
     if (!ok) raise_flag(flag, FLAG_NONFINITE);
 }
 
+// The same per (token, slot) row for head_dim 16 * EPL (64, 128, 256), four
+// rows per wave: lane s of a row's 16 holds elements s, s + 16, ..., so each
+// rotation pair (e, e + hd / 4) sits in one lane and the sum of squares
+// reduces over 16 lanes. At head_dim 64 one row per wave left 3/4 of the
+// wave idle through its reduction and dependent loads.
+template <int EPL>
+__global__ __launch_bounds__(256) void qkv_post_axial_rows_kernel(
+    float *__restrict__ qkv, int64_t ld, int64_t tokens, int nh, int nkv,
+    const float *__restrict__ qn, const float *__restrict__ kn, const float *__restrict__ cos_t,
+    const float *__restrict__ sin_t, const int32_t *__restrict__ pos, float eps, int *flag) {
+    constexpr int RL = 16, HD = RL * EPL, HALF = HD / 2, QUARTER = HD / 4;
+    static_assert(QUARTER % RL == 0, "rotation pairs share a lane");
+    const int slots = nh + 2 * nkv;
+    const int lane = threadIdx.x & 63, sub = lane & (RL - 1);
+    const int64_t r = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+    if (r >= tokens * slots) return;  // whole 16-lane groups: the reductions stay within a group
+    const int64_t t = r / slots;
+    const int slot = (int)(r - t * slots);
+    float *row = qkv + t * ld + (int64_t)slot * HD;
+    const float *w = slot < nh ? qn : (slot < nh + nkv ? kn : nullptr);
+    float v[EPL];
+    float ss = 0.f;
+#pragma unroll
+    for (int m = 0; m < EPL; ++m) {
+        v[m] = row[sub + RL * m];
+        ss += v[m] * v[m];
+    }
+#pragma unroll
+    for (int o = RL / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, RL);
+    const float inv = rms_inverse(ss, HD, eps);
+    bool ok = isfinite(ss);
+    if (w) {
+        const int px = pos[2 * t], py = pos[2 * t + 1];
+#pragma unroll
+        for (int m0 = 0; m0 < EPL; ++m0) {
+            if ((RL * m0) % HALF >= QUARTER) continue;  // m0 holds the pair's first element
+            constexpr int DM = QUARTER / RL;
+            const int m1 = m0 + DM;
+            const int e0 = sub + RL * m0, e1 = e0 + QUARTER;
+            const int hf = e0 >= HALF, i = e0 - hf * HALF;
+            const int64_t ti = (int64_t)(hf ? py : px) * QUARTER + i;
+            const float c = cos_t[ti], sn = sin_t[ti];
+            const float f = v[m0] * inv * w[e0];
+            const float g = v[m1] * inv * w[e1];
+            const float y0 = f * c - g * sn;
+            const float y1 = g * c + f * sn;
+            ok = ok && isfinite(y0) && isfinite(y1);
+            row[e0] = y0;
+            row[e1] = y1;
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < EPL; ++m) {
+            const float y = v[m] * inv;
+            ok = ok && isfinite(y);
+            row[sub + RL * m] = y;
+        }
+    }
+    if (!ok) raise_flag(flag, FLAG_NONFINITE);
+}
+
 hipError_t launch_qkv_post_axial(float *qkv, int64_t ld, int64_t tokens, int nh, int nkv, int hd,
                                  const float *qn, const float *kn, const float *cos_t,
                                  const float *sin_t, const int32_t *pos, float eps, int *flag,
@@ -162,8 +223,19 @@ hipError_t launch_qkv_post_axial(float *qkv, int64_t ld, int64_t tokens, int nh,
     if (tokens <= 0) return hipSuccess;
     if (hd % 4) return hipErrorInvalidValue;
     const int64_t rows = tokens * (nh + 2 * nkv);
-    hipLaunchKernelGGL(qkv_post_axial_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s,
-                       qkv, ld, tokens, nh, nkv, hd, qn, kn, cos_t, sin_t, pos, eps, flag);
+    const dim3 grid16((unsigned)((rows + 15) / 16));
+#define QPA_LAUNCH(EPL)                                                                       \
+    hipLaunchKernelGGL(qkv_post_axial_rows_kernel<EPL>, grid16, dim3(256), 0, s, qkv, ld, tokens, \
+                       nh, nkv, qn, kn, cos_t, sin_t, pos, eps, flag)
+    switch (hd) {
+        case 64: QPA_LAUNCH(4); break;
+        case 128: QPA_LAUNCH(8); break;
+        case 256: QPA_LAUNCH(16); break;
+        default:
+            hipLaunchKernelGGL(qkv_post_axial_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                               s, qkv, ld, tokens, nh, nkv, hd, qn, kn, cos_t, sin_t, pos, eps, flag);
+    }
+#undef QPA_LAUNCH
     return hipGetLastError();
 }
 
