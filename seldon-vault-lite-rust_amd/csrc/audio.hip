@@ -128,14 +128,14 @@ hipError_t launch_sscp_conv0(const float *mel, const uint8_t *mask, const SscpRo
 // thread per (output position, group of four input channels): nine 16-byte
 // loads, one per tap, coalesced over the channel groups of a layer-0 row,
 // and nine 16-byte stores of the thread's 36 contiguous columns (channel
-// major, tap minor: a register transpose of the loads). Channel counts that
-// are not a multiple of four take the same path element by element.
+// major, tap minor: a register transpose of the loads). C0 % 4 == 0 (the
+// configuration requires it).
 __global__ __launch_bounds__(256) void sscp_im2col_kernel(const float *__restrict__ l0,
                                                           const uint8_t *__restrict__ mask0,
                                                           const SscpRow *__restrict__ rows,
                                                           int64_t n_pos, int C0,
                                                           float *__restrict__ col) {
-    const int groups = (C0 + 3) >> 2;
+    const int groups = C0 >> 2;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= n_pos * groups) return;
     const int64_t pos = idx / groups;
@@ -143,7 +143,6 @@ __global__ __launch_bounds__(256) void sscp_im2col_kernel(const float *__restric
     const int64_t r = pos / FREQ1;
     const int f = (int)(pos - r * FREQ1);
     const SscpRow ri = rows[r];
-    const bool vec = (C0 & 3) == 0;
     f32x4 tap[9];
 #pragma unroll
     for (int kt = 0; kt < 3; ++kt) {
@@ -153,17 +152,8 @@ __global__ __launch_bounds__(256) void sscp_im2col_kernel(const float *__restric
         for (int kf = 0; kf < 3; ++kf) {
             const int iff = 2 * f + kf - 1;
             f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (row_ok && iff >= 0 && iff < FREQ0) {
-                const float *src = l0 + ((int64_t)(ri.base + it) * FREQ0 + iff) * C0 + ic0;
-                if (vec) {
-                    v = *(const f32x4 *)src;
-                } else {
-                    if (ic0 + 0 < C0) v.x = src[0];
-                    if (ic0 + 1 < C0) v.y = src[1];
-                    if (ic0 + 2 < C0) v.z = src[2];
-                    if (ic0 + 3 < C0) v.w = src[3];
-                }
-            }
+            if (row_ok && iff >= 0 && iff < FREQ0)
+                v = *(const f32x4 *)(l0 + ((int64_t)(ri.base + it) * FREQ0 + iff) * C0 + ic0);
             tap[kt * 3 + kf] = v;
         }
     }
@@ -176,24 +166,17 @@ __global__ __launch_bounds__(256) void sscp_im2col_kernel(const float *__restric
         o[2 * 9 + t] = tap[t].z;
         o[3 * 9 + t] = tap[t].w;
     }
-    float *dst = col + pos * (int64_t)(9 * C0) + 9 * ic0;
-    if (vec) {
+    f32x4 *dst = (f32x4 *)(col + pos * (int64_t)(9 * C0) + 9 * ic0);
 #pragma unroll
-        for (int u = 0; u < 9; ++u)
-            ((f32x4 *)dst)[u] = f32x4{o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]};
-    } else {
-        const int n = 9 * (C0 - ic0 < 4 ? C0 - ic0 : 4);
-#pragma unroll
-        for (int u = 0; u < 36; ++u)
-            if (u < n) dst[u] = o[u];
-    }
+    for (int u = 0; u < 9; ++u) dst[u] = f32x4{o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]};
 }
 
 hipError_t launch_sscp_im2col(const float *l0, const uint8_t *mask0, const SscpRow *rows,
                               int64_t n_rows, int C0, float *col, hipStream_t s) {
     const int64_t n = n_rows * FREQ1;
-    if (n <= 0 || C0 <= 0) return hipSuccess;
-    const int64_t threads = n * ((C0 + 3) / 4);
+    if (n <= 0) return hipSuccess;
+    if (C0 <= 0 || C0 % 4) return hipErrorInvalidValue;
+    const int64_t threads = n * (C0 / 4);
     if ((threads + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(sscp_im2col_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        s, l0, mask0, rows, n, C0, col);

@@ -136,6 +136,31 @@ def test_batch_and_device_paths_are_bit_identical(au2):
     assert np.array_equal(d_out.cpu().numpy(), np.concatenate([b.pooled() for b in batch]))
 
 
+# Attention shapes beyond config AU: a head_dim of 15 (rows not 16-byte
+# aligned) with 20-row blocks and a 61-entry context (a full wave of lanes
+# per query, two passes over each block's queries, right context), and a
+# head_dim of 256 with a 35-entry context.
+@pytest.mark.parametrize("hidden,heads,chunk,left,right", [(60, 4, 20, 40, 2), (512, 2, 6, 30, 0)])
+def test_attention_shapes_match_oracle(hidden, heads, chunk, left, right):
+    c = svl_synth.config_au(2)
+    c["audio_config"].update(hidden_size=hidden, num_attention_heads=heads,
+                             attention_chunk_size=chunk, attention_context_left=left,
+                             attention_context_right=right, output_proj_dims=40)
+    w = svl_synth.audio_weights(c, 768, seed=11)
+    gpu = A.AudioModel(A.AudioConfig.from_json_value(c), w, 768)
+    om = O.OracleAudioModel(c, w, 768)
+    masks = [np.ones(300, bool), np.ones(157, bool), np.ones(13, bool)]
+    masks[0][41:45] = False       # interior masked frames inside a block
+    masks[1][130:] = False        # padded tail
+    mels = svl_synth.mel_clips([300, 157, 13], seed=9, masks=masks)
+    got = gpu.forward_batch(mels, capture_hidden=True)
+    for i, (g_, m) in enumerate(zip(got, mels)):
+        o = om.forward(m.features, m.mask.astype(bool), True)
+        np.testing.assert_allclose(np.stack(g_.hidden_states()), o["hidden_states"], atol=2e-4,
+                                   rtol=1e-4)
+        check(g_.pooled(), o["pooled"], f"hidden {hidden} clip {i} soft tokens")
+
+
 def test_full_30_second_clip_one_layer():
     """2999 mel frames -> 1500 -> 750 tokens: every chunk block of a real clip."""
     c = svl_synth.config_au(1)
