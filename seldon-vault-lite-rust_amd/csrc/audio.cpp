@@ -766,7 +766,18 @@ svl_status svl_audio_model_create(svl_ctx *ctx, const svl_audio_config *cfg, int
         ST_TRY(read_bounds(by_name, p + "lconv1d.linear_start", ly.bstart));
         ST_TRY(up(p + "lconv1d.linear_end.linear.weight", &ly.w_end));
         ST_TRY(read_bounds(by_name, p + "lconv1d.linear_end", ly.bend));
-        ST_TRY(up(p + "lconv1d.depthwise_conv1d.weight", &ly.dw));
+        // depthwise weight [H, 1, K] uploaded tap-major, [K, H]: the kernel
+        // reads four channels' weights of one tap as one float4
+        ST_TRY(decode_named(by_name, p + "lconv1d.depthwise_conv1d.weight", a));
+        if ((int64_t)a.size() != m->K * m->H)
+            return fail(SVL_INTERNAL, "audio depthwise weight has %zu elements, expected %lld",
+                        a.size(), (long long)(m->K * m->H));
+        {
+            std::vector<float> dwt((size_t)(m->K * m->H));
+            for (int64_t c = 0; c < m->H; ++c)
+                for (int64_t t = 0; t < m->K; ++t) dwt[(size_t)(t * m->H + c)] = a[(size_t)(c * m->K + t)];
+            ST_TRY(upload_owned(m->allocations, dwt.data(), dwt.size(), &ly.dw));
+        }
         ST_TRY(up(p + "lconv1d.conv_norm.weight", &ly.lc_norm));
         ST_TRY(up(p + "norm_pre_attn.weight", &ly.norm_pre_attn));
         ST_TRY(up(p + "norm_post_attn.weight", &ly.norm_post_attn));

@@ -600,7 +600,7 @@ hipError_t launch_audio_attention(const AudioAttnArgs &a, hipStream_t s) {
 
 // ---- light convolution: causal depthwise conv + clamp + RMSNorm + SiLU -------
 // One wave per row; taps ascend from row - (K - 1), rows before the clip's
-// first row are skipped (audio.rs:1490-1503). dw is [width, K].
+// first row are skipped (audio.rs:1490-1503). dw is tap-major, [K, width].
 template <int NC>
 __global__ __launch_bounds__(256) void lconv_kernel(const float *__restrict__ gated,
                                                     const float *__restrict__ dw, int K,
@@ -623,11 +623,11 @@ __global__ __launch_bounds__(256) void lconv_kernel(const float *__restrict__ ga
                 const int src = il - (K - 1) + tap;
                 if (src < 0) continue;
                 const f32x4 g = ((const f32x4 *)(gated + (row - il + src) * width))[i];
-                const int col = 4 * i;
-                acc.x += g.x * dw[(col + 0) * K + tap];
-                acc.y += g.y * dw[(col + 1) * K + tap];
-                acc.z += g.z * dw[(col + 2) * K + tap];
-                acc.w += g.w * dw[(col + 3) * K + tap];
+                const f32x4 wt = ((const f32x4 *)(dw + (int64_t)tap * width))[i];
+                acc.x += g.x * wt.x;
+                acc.y += g.y * wt.y;
+                acc.z += g.z * wt.z;
+                acc.w += g.w * wt.w;
             }
             v[c] = clamp4(acc, -clip, clip);
             ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;

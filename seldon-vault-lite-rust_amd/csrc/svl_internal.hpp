@@ -196,7 +196,7 @@ struct AudioAttnArgs {
     int *flag;
 };
 hipError_t launch_audio_attention(const AudioAttnArgs &a, hipStream_t s);
-// Causal depthwise conv (dw [width, K]) within each clip, clamp, RMSNorm(w), SiLU.
+// Causal depthwise conv (dw tap-major, [K, width]) within each clip, clamp, RMSNorm(w), SiLU.
 hipError_t launch_lconv(const float *gated, const float *dw, int K, const int32_t *pos, float clip,
                         const float *w, float *out, int64_t rows, int width, float eps, int *flag,
                         hipStream_t s);
