@@ -492,6 +492,9 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 //    128x128; per row group, with 32-wide K slices: 168 us against 185 us),
 //    deeper pipelines below two rounds of 128x128 tiles, or 64x64 with the
 //    four waves stacked along M on one-row grids.
+//  * Outputs of at most 32 columns (the audio subsampling's 32 channels):
+//    128x32 tiles, the four waves stacked along M, instead of 64x64 tiles
+//    that would spend half their MFMAs on zero columns.
 //  * Stages: grids of at least two workgroups per CU keep two stages (their
 //    co-resident workgroups hide each other's DMA latency, and a deeper
 //    pipeline measured slower there); short grids, whose few workgroups run
@@ -545,6 +548,7 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
             if (tiles(128, 128) < 4 * 256) return launch_dma_staged<128, 64, 16, EPI, 4, 3>(a, s);
             return launch_dma_staged<128, 128, 16, EPI, 3, 3>(a, s);
         }
+        if (a.N <= 32 && a.K % 32 == 0) return launch_dma<128, 32, 32, EPI, 4, 2, 4>(a, s);
         auto per_cu = [&](int bm, int bn) { return (double)((tiles(bm, bn) + 255) / 256); };
         const double c128 = per_cu(128, 128) * (128.0 * 128.0);
         const double c12864 = per_cu(128, 64) * (128.0 * 64.0) / 0.95;
