@@ -313,9 +313,9 @@ hipError_t launch_audio_rows(const float *x, float c1, const float *w1, const fl
 }
 
 // ---- chunked local attention ---------------------------------------------
-// One wave per (block of `chunk` query rows of a clip, head): every query of
-// a block shares the same `context` keys and values, so the wave stages them
-// once in LDS (keys scaled by k_scale, key rows padded to an odd number of
+// One workgroup of AW waves per (block of `chunk` query rows of a clip,
+// head): every query of a block shares the same `context` keys and values,
+// so the workgroup stages them once in LDS (keys scaled by k_scale, key rows padded to an odd number of
 // 16-byte chunks so lanes reading different rows at one column hit different
 // banks), together with the head's relative-position keys and the block's
 // queries (scaled by qf[d] = q_scale * softplus(per_dim_scale[d])). All
