@@ -20,8 +20,8 @@
 //    each operand to its valid rows, so the ragged M tail (and N tail) reads
 //    zeros without branches.
 //  * LDS rows are unpadded; 16-byte chunks are XOR-swizzled by row
-//    (chunk ^ (row / rows_per_bank_line) % chunks_per_row) on the way in, so
-//    the 16-row fragment loads (one ds_read_b128 per lane) hit distinct banks.
+//    (chunk ^ (row / 2 or 1) % chunks_per_row) on the way in, so the 16-row
+//    fragment loads (one ds_read_b128 per lane) hit distinct banks.
 //  * Lane l reads float4 = k0 + 4 (l / 16) .. + 3 of row l % 16 and feeds
 //    element s to MFMA s, so MFMA s of a 16-k group sums k0 + s, k0 + 4 + s,
 //    k0 + 8 + s, k0 + 12 + s; A and W use the same permutation, so the sum
@@ -264,10 +264,12 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     constexpr int TM = WTM / 16, TN = WTN / 16;  // 16x16 tiles per wave
     constexpr int CPR = BK / 4;                 // 16-byte chunks per row
     constexpr int RPK = 64 / CPR;               // rows per 1 KB DMA instruction
-    // Swizzle: chunk ^ (row / RPL) % SWZ. Rows shorter than a 64-bank LDS
-    // line share one (RPL rows per line); rows of a line or more (BK >= 64)
-    // XOR their row index into the low 4 chunk bits.
-    constexpr int RPL = BK >= 64 ? 1 : 64 / BK;
+    // Swizzle: chunk ^ (row / RPL) % SWZ. Rows of 64 and 128 bytes (BK 16
+    // and 32) change the XOR every second row, rows of 256 bytes or more
+    // (BK >= 64) every row. SQ_LDS_BANK_CONFLICT reads zero for the fragment
+    // loads of both; 64-byte rows changing it every fourth row conflicted on
+    // half the LDS cycles (without a measurable cost to the kernel).
+    constexpr int RPL = BK >= 64 ? 1 : 2;
     constexpr int SWZ = CPR < 16 ? CPR : 16;
     constexpr int A_CH = BM / RPK / 4;          // DMA instructions per wave per slice
     constexpr int W_CH = BN / RPK / 4;
