@@ -213,6 +213,25 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_mfma_kernel(AttnArgs p) {
 //  * Online softmax in log2 units (v_exp_f32) with a lazily moved reference
 //    max, so the output accumulators are rescaled only when a query's running
 //    max grows by more than 2^8.
+// max / sum of v over lanes l, l ^ 16, l ^ 32 and l ^ 48 through the VALU
+// lane swaps v_permlane16_swap and v_permlane32_swap (no LDS round trip as
+// with ds_bpermute). Each swap of v with itself leaves {v[l], v[l ^ 16]}
+// (resp. {v[l], v[l ^ 32]}) in the two results, so folding them gives the
+// same value, bit for bit, as v op __shfl_xor(v, 16) (resp. 32).
+__device__ __forceinline__ float fold_xor16_32_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float fold_xor16_32_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int HD, int WAVES, int KT>
 __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(AttnArgs p) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -370,8 +389,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, pr[kb][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = fold_xor16_32_max(tmax);
         // Lazy rescale: the reference max m_ref only moves when a query's
         // max grows by more than RESCALE_LOG2 (probabilities then stay below
         // 2^RESCALE_LOG2). O and l are divided out at the end, so the result
@@ -394,8 +412,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(
                 pr[kb][r] = pr[kb][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pr[kb][r] - m_ref);
                 psum += pr[kb][r];
             }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
+        psum = fold_xor16_32_sum(psum);
         l_run += psum;
 
         // O^T += V^T P^T, keys 4 (lane / 16) + r of block kb in MFMA r: lane
