@@ -69,8 +69,7 @@ __global__ __launch_bounds__(256) void sscp_conv0_kernel(const float *__restrict
         }
         v[j] = acc;
     }
-    sum += __shfl_xor(sum, 1, 4);
-    sum += __shfl_xor(sum, 2, 4);
+    sum = group_reduce<4, false>(sum);
     const float mean = sum / (float)C0;
     float var = 0.f;
 #pragma unroll
@@ -79,8 +78,7 @@ __global__ __launch_bounds__(256) void sscp_conv0_kernel(const float *__restrict
             const float d = v[j] - mean;
             var += d * d;
         }
-    var += __shfl_xor(var, 1, 4);
-    var += __shfl_xor(var, 2, 4);
+    var = group_reduce<4, false>(var);
     var = var / (float)C0;
     const float inv = 1.0f / sqrtf(var + eps);
     ok = ok && isfinite(inv);
@@ -491,13 +489,9 @@ __global__ __launch_bounds__(64 * AW) void audio_attn_kernel(AudioAttnArgs p) {
                 const float dot = (rel >= 0 && rel < p.positions) ? sk[j] + sr[j] : sk[j];
                 score = tanhf(dot / p.cap) * p.cap;
             }
-            float m = ci < p.context ? score : -INFINITY;
-#pragma unroll
-            for (int o = KL / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, KL));
+            const float m = group_reduce<KL, true>(ci < p.context ? score : -INFINITY);
             const float e = ci < p.context ? expf(score - m) : 0.0f;
-            float sum = e;
-#pragma unroll
-            for (int o = KL / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, KL);
+            const float sum = group_reduce<KL, false>(e);
             live[j] = q < nb && p.mask[r0 + q0 + q] && !(m <= -1.0e9f / 2.0f);
             if (live[j] && !(isfinite(sum) && sum > 0.0f)) ok = false;
             wgt[j] = e / sum;

@@ -25,6 +25,39 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Reductions over aligned groups of W lanes (W = 4, 16, 32 or 64) on VALU
+// lane permutes, with no LDS round trip: DPP within a row of 16 lanes
+// (quad_perm xor 1 and xor 2, then the half-row and row mirrors, which pair
+// lanes whose quads or halves already agree), v_permlane16_swap and
+// v_permlane32_swap across rows (a swap of v with itself leaves
+// {v[l], v[l ^ 16]} resp. {v[l], v[l ^ 32]} in its two results). Every lane
+// of a group ends with the group's result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int W, bool MAX>
+__device__ __forceinline__ float group_reduce(float v) {
+    static_assert(W == 4 || W == 16 || W == 32 || W == 64, "group width");
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    v = op(v, dpp_mov<0xB1>(v));   // quad_perm [1, 0, 3, 2]: lane ^ 1
+    v = op(v, dpp_mov<0x4E>(v));   // quad_perm [2, 3, 0, 1]: lane ^ 2
+    if constexpr (W >= 16) {
+        v = op(v, dpp_mov<0x141>(v));  // row_half_mirror: the other quad of the 8
+        v = op(v, dpp_mov<0x140>(v));  // row_mirror: the other 8 of the row
+    }
+    if constexpr (W >= 32) {
+        const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    }
+    if constexpr (W == 64) {
+        const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    }
+    return v;
+}
+
 // kernels.rs:380-383 gelu_tanh_value, same constants and evaluation order.
 __device__ __forceinline__ float gelu_tanh(float v) {
     float cubic = v * v * v;
