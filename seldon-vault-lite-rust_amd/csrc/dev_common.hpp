@@ -13,17 +13,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int WAVE = 64;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
-}
 
 // Reductions over aligned groups of W lanes (W = 4, 16, 32 or 64) on VALU
 // lane permutes, with no LDS round trip: DPP within a row of 16 lanes
@@ -57,6 +46,11 @@ __device__ __forceinline__ float group_reduce(float v) {
     }
     return v;
 }
+
+// Sum / max over the 64 lanes of a wave (every lane active), every lane
+// receiving the same bits.
+__device__ __forceinline__ float wave_sum(float v) { return group_reduce<64, false>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_reduce<64, true>(v); }
 
 // kernels.rs:380-383 gelu_tanh_value, same constants and evaluation order.
 __device__ __forceinline__ float gelu_tanh(float v) {
