@@ -314,7 +314,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              f"(rows are independent and would shard by data parallelism, see DESIGN.md)",
+              f"(rows are independent and would shard by data parallelism)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -397,7 +397,7 @@ def main():
     fwd_flops = (gemm_flops + attn["work"]) / args.steps
     total_kernel_ms = sum(v["ms"] for v in stats.values()) / args.steps
 
-    # T1 latency: batch 1 x 128 tokens.
+    # Single-request latency: batch 1 x 128 tokens.
     t1_ids = torch.from_numpy(svl_synth.token_rows(cfg["vocab_size"], [128], seed=1)[0]
                               .astype(np.int32)).to("cuda:0")
     t1_off = np.array([0, 128], np.int64)

@@ -127,15 +127,15 @@ def test_shape_a_full_depth_t1_matches_oracle():
 
 
 def test_long_context_rows_match_oracle():
-    # BASELINE T3's row length: two 2048-token rows through a sliding layer
+    # The long-context row length: two 2048-token rows through a sliding layer
     # (window 512: every query's window is cut on both sides) and a full one
     # (the 2048 x 2048 score matrix).
     cfg = svl_synth.config_a(layers=2, vocab=4096)
     _shape_parity(cfg, [2048, 2047])
 
 
-def test_long_context_t3_shape_is_batch_invariant():
-    # The full T3 shape (8 x 2048 tokens, 24 layers): every row of the batch
+def test_long_context_batch_is_batch_invariant():
+    # The full long-context shape (8 x 2048 tokens, 24 layers): every row of the batch
     # equals the same row run alone, bit for bit, and is a finite unit vector.
     cfg = svl_synth.config_a(layers=24, vocab=262144)
     w = svl_synth.weights(cfg, seed=0)
