@@ -352,8 +352,8 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    # Timed region: K steps of the production path (two row groups on two
-    # streams), bracketed by device synchronisation.
+    # Timed region: K steps of the production path (row groups on their own
+    # streams, three by default), bracketed by device synchronisation.
     step_ms = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
