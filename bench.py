@@ -10,14 +10,16 @@ Token ids are resident in HBM before the timed region; every step runs the
 whole encoder and writes the normalised embeddings to HBM.
 
 Prints one JSON line: embeddings/s (value, timed on the production path:
-two row groups on two streams), the roofline of the dominant kernel (the
+three row groups on three streams), the roofline of the dominant kernel (the
 gate/up GEMM; its launches timed with HIP events on the stream they run on,
 in a second pass of the same steps on one stream so that each kernel's
-duration is its own), and the CPU oracle timed on this host's cores on a
-bounded sample. Secondary legs, each with its own workload string: image
-prompts (vision tower + text encoder), audio prompts (audio tower + text
-encoder, from log-mel frames and from 16 kHz samples through the log-mel
-front end), and exact cosine search over a 1M x 768 index.
+duration is its own), the CPU oracle timed on this host's cores on a bounded
+sample of the batch's rows, and the parity of those rows of the timed output
+against the oracle's. Secondary legs, each with its own workload string: the
+same batch from host ids to host vectors, 8 x 2048-token rows, image prompts
+(vision tower + text encoder), audio prompts (audio tower + text encoder,
+from log-mel frames and from 16 kHz samples through the log-mel front end),
+and exact cosine search over a 1M x 768 index.
 """
 import argparse
 import json
@@ -45,8 +47,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-sample-rows", type=int, default=-1,
-                    help="rows of the workload timed on the CPU oracle (default: one per core, "
-                         "at most 16; 0 skips the CPU baseline)")
+                    help="rows of the workload timed on the CPU oracle (default: two per worker "
+                         "thread, at most 16 threads; 0 skips the CPU baseline)")
     ap.add_argument("--t1-runs", type=int, default=20)
     ap.add_argument("--image-steps", type=int, default=5,
                     help="timed batches of the image workload (0 skips it)")
@@ -54,6 +56,10 @@ def parse():
                     help="timed batches of the audio workload (0 skips it)")
     ap.add_argument("--search-steps", type=int, default=5,
                     help="timed batches of the vector-search workload (0 skips it)")
+    ap.add_argument("--long-steps", type=int, default=5,
+                    help="timed batches of the 8 x 2048-token workload (0 skips it)")
+    ap.add_argument("--host-steps", type=int, default=10,
+                    help="timed batches of the host-ids to host-vectors path (0 skips it)")
     ap.add_argument("--row-groups", type=int, default=3,
                     help="row groups (streams) the batch is split into")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -86,25 +92,123 @@ def gemm_traffic():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(cfg, weights, rows_all, n_rows):
-    from oracle import oracle as O
+def host_cpu():
+    """nproc (logical CPUs of the host), the CPUs this process may run on, and
+    the CPU model string from /proc/cpuinfo."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return os.cpu_count(), usable, model
+
+
+def cpu_baseline(cfg, weights, rows_all, n_rows, gpu_out):
+    """The scalar C oracle (the reference's x86-64 path restated) on a seeded
+    subset of the batch's rows, pulled by worker threads from one queue as
+    the reference's request-level bench does (tests/text_bench.rs:58-72), on
+    at most 16 threads: the host share of one GPU on the MI355X boxes. The
+    same rows of the GPU output are compared with the oracle's, giving the
+    line's parity object."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
+    from oracle import oracle as O
 
     if n_rows == 0:
-        return None
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    n = n_rows if n_rows > 0 else max(1, min(cores, 16))
-    rows = rows_all[:n]
-    model = O.OracleTextModel(cfg, weights)
+        return None, None
+    nproc, usable, model_name = host_cpu()
+    threads = max(1, min(usable, 16))
+    n = n_rows if n_rows > 0 else 2 * threads
+    pick = sorted(int(i) for i in np.random.default_rng(12).choice(len(rows_all), n, replace=False))
+    rows = [rows_all[i] for i in pick]
+    oracle = O.OracleTextModel(cfg, weights)
     t0 = time.perf_counter()
-    outs = model.forward_rows(rows, threads=n)
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        outs = list(ex.map(lambda r: oracle.forward(r), rows))
     wall = time.perf_counter() - t0
-    assert all(np.isfinite(o["normalized"]).all() for o in outs)
     toks = sum(len(r) for r in rows)
-    return {"value": n / wall, "unit": "embeddings/s", "cores": n, "kind": "port",
-            "sample": f"first {n} rows of the same batch ({toks} tokens, lengths "
-                      f"{min(len(r) for r in rows)}-{max(len(r) for r in rows)}), one row per "
-                      f"thread, scalar C oracle (-O2, no FMA contraction), {wall:.1f} s wall"}
+    cpu = {"value": n / wall, "unit": "embeddings/s", "cores": threads, "kind": "port",
+           "nproc": nproc, "usable_cpus": usable, "cpu_model": model_name,
+           "sample": f"{n} rows of the same batch (seeded subset, {toks} tokens, lengths "
+                     f"{min(len(r) for r in rows)}-{max(len(r) for r in rows)}), pulled from one "
+                     f"queue by {threads} worker threads, scalar C oracle (-O2, no FMA "
+                     f"contraction), {wall:.1f} s wall"}
+    worst_abs, worst_cos = 0.0, 1.0
+    for i, o in zip(pick, outs):
+        off = 0
+        for d in DIMS:
+            want = O.truncate_and_normalize(o["normalized"], d).astype(np.float64)
+            have = gpu_out[i, off:off + d].astype(np.float64)
+            worst_abs = max(worst_abs, float(np.abs(have - want).max()))
+            worst_cos = min(worst_cos, float(have @ want / (np.linalg.norm(have)
+                                                             * np.linalg.norm(want))))
+            off += d
+    parity = {"rows": n, "dims": DIMS, "max_abs": worst_abs, "min_cos": worst_cos,
+              "tolerance": {"max_abs": 1e-4, "min_cos": 0.99999},
+              "ok": bool(worst_abs <= 1e-4 and worst_cos >= 0.99999),
+              "against": "scalar C oracle, same rows of the timed batch's output"}
+    return cpu, parity
+
+
+def long_context_leg(model, steps):
+    """Long-context workload: the same text encoder on a batch of 8 rows of
+    2048 tokens (ids uniform over the vocabulary, seed 4): 20 sliding-window
+    layers (|i - j| <= 512) and 4 global layers. Attention FLOPs are counted
+    algorithmically, keys per query inside the window only."""
+    import numpy as np
+    import torch
+
+    import svl_synth
+
+    n, L = 8, 2048
+    rows = svl_synth.token_rows(model.config.vocab_size, [L] * n, seed=4)
+    ids = torch.from_numpy(np.concatenate(rows).astype(np.int32)).to("cuda:0")
+    offsets = np.arange(n + 1, dtype=np.int64) * L
+    out = torch.zeros((n, 768), dtype=torch.float32, device="cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        model.forward_device(ids.data_ptr(), offsets, [768], out.data_ptr(), stream)
+
+    step()
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(steps):
+        a = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        ms.append((time.perf_counter() - a) * 1e3)
+    p50 = float(np.median(ms))
+    assert np.isfinite(out.cpu().numpy()).all()
+    groups = model.row_groups
+    model.set_stream_split(False)
+    model.set_kernel_timing(True)
+    step()
+    torch.cuda.synchronize()
+    stats = model.kernel_stats()
+    model.set_kernel_timing(False)
+    model.set_stream_split(groups)
+    attn = stats["attention"]
+    gemm_keys = [k for k in stats if k.startswith("gemm_")]
+    gemm_ms = sum(stats[k]["ms"] for k in gemm_keys)
+    gemm_flops = sum(stats[k]["work"] for k in gemm_keys)
+    flops = gemm_flops + attn["work"]
+    return {"workload": "the same text encoder on 8 rows x 2048 tokens (ids uniform over the "
+                        "vocabulary, seed 4): 20 sliding-window layers (window 512), 4 global",
+            "embeddings_per_s": round(n / (p50 * 1e-3), 2), "p50_ms_per_batch": round(p50, 3),
+            "forward_tflops": round(flops / (p50 * 1e-3) / 1e12, 2),
+            "forward_frac_of_fp32_mfma_peak": round(flops / (p50 * 1e-3) / 1e12
+                                                    / PEAK_FP32_MFMA_TFLOPS, 4),
+            "attention_flops_per_batch": attn["work"],
+            "attention_ms_per_batch": round(attn["ms"], 3),
+            "attention_tflops": round(attn["work"] / (attn["ms"] * 1e-3) / 1e12, 2),
+            "gemm_tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 2),
+            "kernel_timing": "one pass on one stream, HIP events per launch", "steps": steps}
 
 
 def image_leg(text_model, dev, steps):
@@ -397,6 +501,30 @@ def main():
     fwd_flops = (gemm_flops + attn["work"]) / args.steps
     total_kernel_ms = sum(v["ms"] for v in stats.values()) / args.steps
 
+    # The timed batch's output, for the parity check against the oracle.
+    step()
+    torch.cuda.synchronize()
+    gpu_out = out.cpu().numpy()
+
+    # The same batch from ids on the host to Matryoshka vectors on the host
+    # (PCIe upload of the ids and download of the embeddings included).
+    host = None
+    if args.host_steps > 0:
+        model.embed_batch(rows, DIMS)
+        hms = []
+        for _ in range(args.host_steps):
+            a = time.perf_counter()
+            hv = model.embed_batch(rows, DIMS)
+            hms.append((time.perf_counter() - a) * 1e3)
+        # the host truncation sums in order, the device's in a tree: last-bit
+        # differences only
+        assert np.abs(hv - gpu_out).max() <= 1e-6
+        hp50 = float(np.median(hms))
+        host = {"embeddings_per_s": round(BATCH / (hp50 * 1e-3), 3), "p50_ms": round(hp50, 3),
+                "span": "token ids in host memory -> 64 x (768/512/256/128) vectors in host "
+                        "memory (svl_text_forward_batch + host truncate_and_normalize)",
+                "steps": args.host_steps}
+
     # Single-request latency: batch 1 x 128 tokens.
     t1_ids = torch.from_numpy(svl_synth.token_rows(cfg["vocab_size"], [128], seed=1)[0]
                               .astype(np.int32)).to("cuda:0")
@@ -422,7 +550,8 @@ def main():
              if args.audio_steps > 0 else None)
     search = (search_leg(dev, args.search_steps, args.cpu_sample_rows != 0)
               if args.search_steps > 0 else None)
-    cpu = cpu_baseline(cfg, weights, rows, args.cpu_sample_rows)
+    long_ctx = long_context_leg(model, args.long_steps) if args.long_steps > 0 else None
+    cpu, parity = cpu_baseline(cfg, weights, rows, args.cpu_sample_rows, gpu_out)
 
     breakdown = {k: {"ms_per_step": round(v["ms"] / args.steps, 3),
                      "launches_per_step": v["launches"] // max(args.steps, 1)}
@@ -450,7 +579,10 @@ def main():
         "single_stream_ms_per_step": round(single_stream_ms, 3),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "parity": parity,
+        "host_to_host": host,
         "kernels": breakdown,
+        "long_context": long_ctx,
         "image": image,
         "audio": audio,
         "search": search,

@@ -149,6 +149,12 @@ svl_status svl_text_embed_ids(svl_text_model *model, const uint32_t *ids, int64_
 svl_status svl_truncate_and_normalize(const float *values, size_t n, size_t dimension,
                                       float *out);
 
+/* TensorEntry::to_f32 (src/binary/safetensors.rs:69-110): decodes one view
+ * into `out` (capacity floats): F32 read little-endian, BF16 widened exactly
+ * (bits << 16, src/binary/bf16.rs:13-15). LimitExceeded above the element
+ * cap, Unsupported for another dtype. Host only; no device is needed. */
+svl_status svl_tensor_to_f32(const svl_tensor_view *tensor, float *out, int64_t capacity);
+
 /* Batches of 4096 tokens or more run as `groups` groups of rows (1..4,
  * default 3), group 0 on the caller's stream and the others on streams of
  * the model that wait for it and are joined back into it, so one group's

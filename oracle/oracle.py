@@ -511,6 +511,8 @@ def _audio_lib():
         L.svlo_audio_forward.argtypes = [ctypes.POINTER(_AudCfg), ctypes.POINTER(f), sz, f,
                                          ctypes.POINTER(ctypes.c_ubyte), sz,
                                          ctypes.POINTER(sz), f, f, f, ctypes.c_char_p, sz]
+        L.svlo_audio_layer.argtypes = [ctypes.POINTER(_AudCfg), ctypes.POINTER(f), sz, f,
+                                       ctypes.POINTER(ctypes.c_ubyte), sz, f, ctypes.c_char_p, sz]
         L._audio_ready = True
     return L
 
@@ -609,6 +611,24 @@ class OracleAudioModel:
         if capture_hidden:
             out["sscp_output"] = sscp[: n * H].reshape(n, H)
             out["hidden_states"] = hidden[: L * n * H].reshape(L, n, H)
+        return out
+
+
+    def layer(self, layer, hidden, row_mask):
+        """Encoder layer `layer` alone (audio.rs:1001-1083) applied to hidden
+        [rows, hidden_size] with the subsampled row mask [rows]; the code the
+        forward pass runs per layer."""
+        h = _f32(hidden)
+        rows = h.shape[0]
+        m = np.ascontiguousarray(np.asarray(row_mask, np.uint8).reshape(-1))
+        assert m.size == rows
+        out = np.empty_like(h)
+        msg = ctypes.create_string_buffer(256)
+        st = _audio_lib().svlo_audio_layer(ctypes.byref(self._c), self._ptrs, int(layer), _fp(h),
+                                           m.ctypes.data_as(ctypes.POINTER(ctypes.c_ubyte)), rows,
+                                           _fp(out), msg, 256)
+        if st != 0:
+            raise OracleError(st, msg.value.decode())
         return out
 
 

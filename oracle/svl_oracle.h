@@ -217,6 +217,13 @@ int svlo_audio_forward(const svlo_audio_config *cfg, const float *const *weights
                        size_t frames, size_t *out_tokens, float *out_pooled, float *out_sscp,
                        float *out_hidden, char *msg, size_t msg_len);
 
+/* One encoder layer of AudioModel::forward (audio.rs:1001-1083) alone, from a
+ * given hidden state [rows, hidden] and subsampled row mask (0/1 bytes), into
+ * out [rows, hidden]; the same code the forward pass runs per layer. */
+int svlo_audio_layer(const svlo_audio_config *cfg, const float *const *weights, size_t layer,
+                     const float *hidden_in, const unsigned char *mask, size_t rows, float *out,
+                     char *msg, size_t msg_len);
+
 /* Log-mel front end, src/media/audio_preprocess.rs:24-46 constants. */
 #define SVLO_MEL_FRAME_LENGTH 320
 #define SVLO_MEL_HOP 160

@@ -438,6 +438,104 @@ size_t svlo_audio_subsampled_frames(size_t frames) {
     return (f1 + 1) / 2;
 }
 
+/* Scratch of one encoder layer over `rows` subsampled rows. */
+typedef struct {
+    float *h2, *t1, *t2, *t3, *ti, *ti2, *t2h, *qb, *kb, *vb, *relk;
+} au_layer_bufs;
+
+/* One conformer layer of AudioModel::forward (audio.rs:1001-1083): feed-forward
+ * 1, attention sandwich, light conv, feed-forward 2, norm_out; `hidden` [rows,
+ * H] is read and overwritten. */
+static int au_layer(const svlo_audio_config *c, const float *const *weights, size_t l,
+                    float *hidden, const unsigned char *mask1, size_t rows, const float *posemb,
+                    const au_layer_bufs *b) {
+    const size_t H = (size_t)c->hidden_size;
+    const size_t context = (size_t)(c->attention_chunk_size + c->attention_context_left - 1 +
+                                    c->attention_context_right);
+    const size_t positions = context / 2 + 1;
+    int st;
+    if ((st = au_feed_forward(c, weights, l, A_FF1, hidden, rows, b->t1, b->ti, b->ti2, b->h2)))
+        return st;
+    /* residual = h2 */
+    if ((st = svlo_rms_norm_rows(b->h2, AW(l, A_NORM_PRE_ATTN), rows, H, c->rms_norm_eps, b->t1)))
+        return st;
+    if ((st = svlo_linear(posemb, AW(l, A_RELK), positions, H, H, b->relk))) return st;
+    if ((st = au_chunked_attention(c, weights, l, b->t1, mask1, rows, b->relk, b->qb, b->kb, b->vb,
+                                   b->t2, b->t3)))
+        return st;
+    if ((st = svlo_rms_norm_rows(b->t3, AW(l, A_NORM_POST_ATTN), rows, H, c->rms_norm_eps, b->t2)))
+        return st;
+    svlo_add(b->h2, b->t2, rows * H, hidden);
+    if ((st = au_light_conv(c, weights, l, hidden, rows, b->t1, b->t2h, b->t3, b->h2))) return st;
+    if ((st = au_feed_forward(c, weights, l, A_FF2, b->h2, rows, b->t1, b->ti, b->ti2, b->t2)))
+        return st;
+    return svlo_rms_norm_rows(b->t2, AW(l, A_NORM_OUT), rows, H, c->rms_norm_eps, hidden);
+}
+
+static au_layer_bufs au_layer_alloc(size_t rows, size_t H, size_t I, size_t positions) {
+    au_layer_bufs b;
+    b.h2 = (float *)malloc(rows * H * sizeof(float));
+    b.t1 = (float *)malloc(rows * H * sizeof(float));
+    b.t2 = (float *)malloc(rows * H * sizeof(float));
+    b.t3 = (float *)malloc(rows * H * sizeof(float));
+    b.ti = (float *)malloc(rows * I * sizeof(float));
+    b.ti2 = (float *)malloc(rows * I * sizeof(float));
+    b.t2h = (float *)malloc(rows * 2 * H * sizeof(float));
+    b.qb = (float *)malloc(rows * H * sizeof(float));
+    b.kb = (float *)malloc(rows * H * sizeof(float));
+    b.vb = (float *)malloc(rows * H * sizeof(float));
+    b.relk = (float *)malloc(positions * H * sizeof(float));
+    return b;
+}
+
+static int au_layer_ok(const au_layer_bufs *b) {
+    return b->h2 && b->t1 && b->t2 && b->t3 && b->ti && b->ti2 && b->t2h && b->qb && b->kb &&
+           b->vb && b->relk;
+}
+
+static void au_layer_free(au_layer_bufs *b) {
+    free(b->h2);
+    free(b->t1);
+    free(b->t2);
+    free(b->t3);
+    free(b->ti);
+    free(b->ti2);
+    free(b->t2h);
+    free(b->qb);
+    free(b->kb);
+    free(b->vb);
+    free(b->relk);
+}
+
+/* One encoder layer alone, from a given hidden state [rows, H] and the
+ * subsampled row mask (0/1 bytes), into out [rows, H]. */
+int svlo_audio_layer(const svlo_audio_config *c, const float *const *weights, size_t layer,
+                     const float *hidden_in, const unsigned char *mask, size_t rows, float *out,
+                     char *msg, size_t msg_len) {
+    if (msg && msg_len) msg[0] = 0;
+    const size_t H = (size_t)c->hidden_size, I = (size_t)c->intermediate_size;
+    const size_t context = (size_t)(c->attention_chunk_size + c->attention_context_left - 1 +
+                                    c->attention_context_right);
+    const size_t positions = context / 2 + 1;
+    if (layer >= (size_t)c->num_hidden_layers || rows == 0)
+        return au_fail(msg, msg_len, SVLO_INTERNAL, "audio layer %zu of %lld over %zu rows", layer,
+                       (long long)c->num_hidden_layers, rows);
+    au_layer_bufs b = au_layer_alloc(rows, H, I, positions);
+    float *posemb = (float *)malloc(positions * H * sizeof(float));
+    int st = SVLO_OK;
+    if (!au_layer_ok(&b) || !posemb) {
+        st = au_fail(msg, msg_len, SVLO_LIMIT, "allocation failed");
+    } else if ((st = svlo_audio_position_embeddings(H, positions, posemb)) == SVLO_OK) {
+        memcpy(out, hidden_in, rows * H * sizeof(float));
+        st = au_layer(c, weights, layer, out, mask, rows, posemb, &b);
+    }
+    if (st && msg && msg_len && !msg[0])
+        au_fail(msg, msg_len, st, "audio layer failed with status %d", st);
+    au_layer_free(&b);
+    free(posemb);
+    return st;
+}
+
 /* AudioModel::forward (audio.rs:981-1134). */
 int svlo_audio_forward(const svlo_audio_config *c, const float *const *weights,
                        size_t text_hidden, const float *features, const unsigned char *mask,
@@ -452,26 +550,14 @@ int svlo_audio_forward(const svlo_audio_config *c, const float *const *weights,
     const size_t rows = svlo_audio_subsampled_frames(frames);
     if (rows == 0) return au_fail(msg, msg_len, SVLO_CORRUPT, "audio subsampling produced no frames");
     int st = SVLO_OK;
-    size_t n_h = rows * H;
-    float *hidden = (float *)malloc(n_h * sizeof(float));
-    float *h2 = (float *)malloc(n_h * sizeof(float));
-    float *t1 = (float *)malloc(n_h * sizeof(float));
-    float *t2 = (float *)malloc(n_h * sizeof(float));
-    float *t3 = (float *)malloc(n_h * sizeof(float));
-    float *ti = (float *)malloc(rows * I * sizeof(float));
-    float *ti2 = (float *)malloc(rows * I * sizeof(float));
-    float *t2h = (float *)malloc(rows * 2 * H * sizeof(float));
-    float *qb = (float *)malloc(n_h * sizeof(float));
-    float *kb = (float *)malloc(n_h * sizeof(float));
-    float *vb = (float *)malloc(n_h * sizeof(float));
+    float *hidden = (float *)malloc(rows * H * sizeof(float));
+    au_layer_bufs lb = au_layer_alloc(rows, H, I, positions);
     float *posemb = (float *)malloc(positions * H * sizeof(float));
-    float *relk = (float *)malloc(positions * H * sizeof(float));
     float *proj = (float *)malloc(rows * P * sizeof(float));
     float *projn = (float *)malloc(rows * P * sizeof(float));
     float *pooled_all = (float *)malloc(rows * text_hidden * sizeof(float));
     unsigned char *mask1 = (unsigned char *)calloc(rows + 1, 1);
-    if (!hidden || !h2 || !t1 || !t2 || !t3 || !ti || !ti2 || !t2h || !qb || !kb || !vb ||
-        !posemb || !relk || !proj || !projn || !pooled_all || !mask1) {
+    if (!hidden || !au_layer_ok(&lb) || !posemb || !proj || !projn || !pooled_all || !mask1) {
         st = au_fail(msg, msg_len, SVLO_LIMIT, "allocation failed");
         goto done;
     }
@@ -491,20 +577,7 @@ int svlo_audio_forward(const svlo_audio_config *c, const float *const *weights,
             if (mask1[r]) memcpy(out_sscp + (o++) * H, hidden + r * H, H * sizeof(float));
     }
     for (size_t l = 0; l < L; ++l) {
-        if ((st = au_feed_forward(c, weights, l, A_FF1, hidden, rows, t1, ti, ti2, h2))) goto knl;
-        /* residual = h2 */
-        if ((st = svlo_rms_norm_rows(h2, AW(l, A_NORM_PRE_ATTN), rows, H, c->rms_norm_eps, t1)))
-            goto knl;
-        if ((st = svlo_linear(posemb, AW(l, A_RELK), positions, H, H, relk))) goto knl;
-        if ((st = au_chunked_attention(c, weights, l, t1, mask1, rows, relk, qb, kb, vb, t2, t3)))
-            goto knl;
-        if ((st = svlo_rms_norm_rows(t3, AW(l, A_NORM_POST_ATTN), rows, H, c->rms_norm_eps, t2)))
-            goto knl;
-        svlo_add(h2, t2, n_h, hidden);
-        if ((st = au_light_conv(c, weights, l, hidden, rows, t1, t2h, t3, h2))) goto knl;
-        if ((st = au_feed_forward(c, weights, l, A_FF2, h2, rows, t1, ti, ti2, t2))) goto knl;
-        if ((st = svlo_rms_norm_rows(t2, AW(l, A_NORM_OUT), rows, H, c->rms_norm_eps, hidden)))
-            goto knl;
+        if ((st = au_layer(c, weights, l, hidden, mask1, rows, posemb, &lb))) goto knl;
         if (out_hidden) {
             size_t o = 0;
             for (size_t r = 0; r < rows; ++r)
@@ -538,18 +611,8 @@ knl:
     au_fail(msg, msg_len, st, "audio kernel failed with status %d (non-finite value or limit)", st);
 done:
     free(hidden);
-    free(h2);
-    free(t1);
-    free(t2);
-    free(t3);
-    free(ti);
-    free(ti2);
-    free(t2h);
-    free(qb);
-    free(kb);
-    free(vb);
+    au_layer_free(&lb);
     free(posemb);
-    free(relk);
     free(proj);
     free(projn);
     free(pooled_all);

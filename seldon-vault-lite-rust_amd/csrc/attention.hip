@@ -198,8 +198,10 @@ __global__ __launch_bounds__(64 * WAVES, 1) void attn_mfma_kernel(AttnArgs p) {
 //  * K and V tiles go from HBM/L2 straight into LDS with
 //    buffer_load_dwordx4 ... lds (one instruction moves 1 KB = 256 / HD
 //    rows), double buffered: tile t+1 is in flight while tile t is
-//    consumed; one barrier per tile. Keys past the row end fall outside the
-//    buffer window and read as zero.
+//    consumed; one barrier per tile. The whole byte offset of a key row
+//    (tile start included) is the instruction's range-checked vector offset,
+//    so keys past the row end fall outside the buffer window and read as
+//    zero, whatever memory follows the row.
 //  * S^T = K . Q^T per 16-key block: K rows are stored with their 16-byte
 //    chunks XOR-swizzled by (key % 16), so the 16 key rows read at one chunk
 //    hit 16 distinct bank groups. Lane l holds keys 4 (l / 16) + r of each
@@ -310,12 +312,14 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(
 #pragma unroll
         for (int q = 0; q < INSTR_PER_WAVE; ++q) {
             const int r0 = (wave * INSTR_PER_WAVE + q) * RPI;
+            // the tile offset goes into the range-checked vector offset (the
+            // scalar offset is outside the buffer's bounds check)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rk, (__attribute__((address_space(3))) void *)&kd[r0 * HD], 16, koff[q],
-                k0 * ldk * 4, 0, 0);
+                rk, (__attribute__((address_space(3))) void *)&kd[r0 * HD], 16,
+                koff[q] + k0 * ldk * 4, 0, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rv, (__attribute__((address_space(3))) void *)&vd[r0 * HD], 16, voff[q],
-                k0 * ldv * 4, 0, 0);
+                rv, (__attribute__((address_space(3))) void *)&vd[r0 * HD], 16,
+                voff[q] + k0 * ldv * 4, 0, 0, 0);
         }
     };
     using S0 = std::integral_constant<int, 0>;
@@ -538,7 +542,8 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
     if (a.tokens <= 0) return hipSuccess;
     const dim3 block(64 * ATTN_WAVES);
     // Buffer windows are per row: the longest row bounds the offsets.
-    const int64_t rows = a.max_len > 0 ? a.max_len : a.tokens;
+    // A tail tile addresses up to 31 keys past the row end (read as zero).
+    const int64_t rows = (a.max_len > 0 ? a.max_len : a.tokens) + 32;
     const bool dma = rows * std::max(std::max(a.ldk, a.ldv), (int64_t)a.hd) * 4 < INT32_MAX;
     switch (a.hd) {
         case 64:

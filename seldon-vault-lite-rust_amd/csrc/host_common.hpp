@@ -125,10 +125,9 @@ inline svl_status check_inventory(const svl_tensor_view *tensors, size_t n_tenso
 // TensorEntry::to_f32 (safetensors.rs:69-110): F32 little-endian or BF16
 // widened exactly (bf16.rs:13-15, bits << 16). Non-finite values are
 // rejected like Tensor::validate_finite (owned.rs:126-135).
-inline svl_status decode_f32(const svl_tensor_view &t, int64_t numel, std::vector<float> &out) {
-    out.resize((size_t)numel);
+inline svl_status widen_f32(const svl_tensor_view &t, int64_t numel, float *out) {
     if (t.dtype == SVL_F32) {
-        std::memcpy(out.data(), t.data, (size_t)numel * 4);
+        std::memcpy(out, t.data, (size_t)numel * 4);
     } else if (t.dtype == SVL_BF16) {
         const uint16_t *b = (const uint16_t *)t.data;
         for (int64_t i = 0; i < numel; ++i) {
@@ -138,6 +137,12 @@ inline svl_status decode_f32(const svl_tensor_view &t, int64_t numel, std::vecto
     } else {
         return fail(SVL_UNSUPPORTED, "tensor %s has an unsupported dtype", t.name);
     }
+    return SVL_OK;
+}
+
+inline svl_status decode_f32(const svl_tensor_view &t, int64_t numel, std::vector<float> &out) {
+    out.resize((size_t)numel);
+    if (svl_status st = widen_f32(t, numel, out.data())) return st;
     for (int64_t i = 0; i < numel; ++i)
         if (!std::isfinite(out[(size_t)i]))
             return fail(SVL_INTERNAL, "non-finite tensor value at index %lld of %s",

@@ -1078,6 +1078,28 @@ svl_status svl_truncate_and_normalize(const float *values, size_t n, size_t dime
     return SVL_OK;
 }
 
+svl_status svl_tensor_to_f32(const svl_tensor_view *t, float *out, int64_t capacity) {
+    // TensorEntry::to_f32 (safetensors.rs:69-110): element cap, then F32
+    // little-endian or BF16 widened exactly (bf16.rs:13-15).
+    if (!t) return fail(SVL_USAGE, "tensor view is null");
+    if (t->ndim < 0 || t->ndim > 8) return fail(SVL_CORRUPT, "tensor %s has rank %d", t->name, t->ndim);
+    int64_t numel = 1;
+    for (int d = 0; d < t->ndim; ++d) {
+        if (t->shape[d] < 0) return fail(SVL_CORRUPT, "tensor %s has a negative dimension", t->name);
+        if (t->shape[d] && numel > MAX_TENSOR_ELEMENTS / t->shape[d])
+            return fail(SVL_LIMIT, "tensor %s has more elements than the cap", t->name);
+        numel *= t->shape[d];
+    }
+    if (numel > MAX_TENSOR_ELEMENTS)
+        return fail(SVL_LIMIT, "tensor %s has %lld elements, above the cap", t->name, (long long)numel);
+    if (numel > capacity)
+        return fail(SVL_USAGE, "tensor %s has %lld elements, the output holds %lld", t->name,
+                    (long long)numel, (long long)capacity);
+    if (numel == 0) return SVL_OK;
+    if (!t->data || !out) return fail(SVL_USAGE, "tensor %s has no data", t->name);
+    return widen_f32(*t, numel, out);
+}
+
 svl_status svl_text_embed_ids(svl_text_model *m, const uint32_t *ids, int64_t n,
                               int64_t dimension, float *out) {
     if (!m || !out) return fail(SVL_USAGE, "model and output are required");

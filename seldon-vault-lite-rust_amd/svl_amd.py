@@ -112,7 +112,7 @@ EXPORTED = [
     "svl_tokenizer_unk_id", "svl_tokenizer_pad_id", "svl_tokenizer_is_special_id",
     "svl_text_embed_texts", "svl_vector_index_create", "svl_vector_index_destroy",
     "svl_vector_index_size", "svl_vector_index_dimension", "svl_vector_rank",
-    "svl_vector_rank_device",
+    "svl_vector_rank_device", "svl_tensor_to_f32",
 ]
 
 _lib = None
@@ -162,6 +162,7 @@ def lib():
         L.svl_text_forward_device.argtypes = [vp, vp, vp, i32, vp, i32, vp, vp]
         L.svl_text_embed_ids.argtypes = [vp, vp, i64, i64, vp]
         L.svl_truncate_and_normalize.argtypes = [vp, ctypes.c_size_t, ctypes.c_size_t, vp]
+        L.svl_tensor_to_f32.argtypes = [ctypes.POINTER(_TensorView), vp, i64]
         L.svl_text_model_set_kernel_timing.argtypes = [vp, ctypes.c_int]
         L.svl_text_model_set_stream_split.argtypes = [vp, ctypes.c_int]
         L.svl_text_model_kernel_stats.argtypes = [vp, vp, vp, vp]
@@ -438,6 +439,22 @@ class RawTensor:
     def __init__(self, dtype, shape, data: np.ndarray):
         self.dtype, self.shape, self.data = dtype, tuple(shape), data
 
+    def to_f32(self) -> np.ndarray:
+        """TensorEntry::to_f32 (safetensors.rs:69-110), decoded by the library:
+        F32 as stored, BF16 widened exactly (bf16.rs:13-15)."""
+        numel = int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1
+        out = np.zeros(max(numel, 1), np.float32)
+        data = np.ascontiguousarray(self.data)
+        v = _TensorView()
+        v.name = b"tensor"
+        v.dtype = 1 if self.dtype == "BF16" else (0 if self.dtype == "F32" else 99)
+        v.ndim = len(self.shape)
+        for i, d in enumerate(self.shape):
+            v.shape[i] = int(d)
+        v.data = data.ctypes.data if data.size else None
+        _check(lib().svl_tensor_to_f32(ctypes.byref(v), _ptr(out), out.size))
+        return out[:numel].reshape(self.shape)
+
 
 def read_safetensors(path: str) -> dict:
     with open(path, "rb") as f:
@@ -551,6 +568,7 @@ class TextModel:
         _check(lib().svl_text_model_create(self.device.handle, ctypes.byref(cfg), arr, n,
                                            ctypes.byref(h)))
         self.handle = h
+        self.row_groups = 3   # the library's default split of large batches
 
     @classmethod
     def load(cls, model_dir: str, device: Device | None = None) -> "TextModel":
@@ -619,6 +637,29 @@ class TextModel:
             outs.append(ForwardOutput(projected[a:b], pooled[i], normalized[i], hs))
         return outs
 
+    def embed_batch(self, rows, dims):
+        """embed_ids (text.rs:546-554) over many rows in one call: ids on the
+        host, one forward pass of the packed batch returning only the
+        normalized embeddings, then truncate_and_normalize on the host at
+        every dim. Returns [len(rows), sum(dims)]."""
+        lens = [len(r) for r in rows]
+        offsets = np.zeros(len(rows) + 1, np.int64)
+        offsets[1:] = np.cumsum(lens)
+        ids = np.concatenate([np.asarray(r, np.int64) for r in rows]).astype(np.uint32) \
+            if rows else np.zeros(1, np.uint32)
+        E = self.config.embedding_dim
+        normalized = np.zeros((len(rows), E), np.float32)
+        _check(lib().svl_text_forward_batch(self.handle, _ptr(ids), _ptr(offsets), len(rows),
+                                            None, _ptr(normalized), None, None, None))
+        out = np.zeros((len(rows), sum(dims)), np.float32)
+        for i in range(len(rows)):
+            off = 0
+            for d in dims:
+                _check(lib().svl_truncate_and_normalize(_ptr(normalized[i]), E, int(d),
+                                                        _ptr(out[i, off:off + d])))
+                off += d
+        return out
+
     def forward_device(self, ids_dev_ptr: int, offsets, dims, out_dev_ptr: int, stream=0):
         """Device-resident batch: ids already in HBM, Matryoshka outputs to HBM."""
         offsets = np.ascontiguousarray(offsets, np.int64)
@@ -641,6 +682,7 @@ class TextModel:
         tokens; True = 3 (the default), False = 1."""
         g = 3 if groups is True else (1 if groups is False else int(groups))
         _check(lib().svl_text_model_set_stream_split(self.handle, g))
+        self.row_groups = max(1, min(g, 4))
 
     def set_kernel_timing(self, enable: bool):
         _check(lib().svl_text_model_set_kernel_timing(self.handle, 1 if enable else 0))

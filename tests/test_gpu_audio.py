@@ -240,3 +240,80 @@ def test_audio_error_taxonomy(tiny):
     with pytest.raises(S.SvlError) as e:
         A.AudioModel(ac, extra, 16)
     assert e.value.kind == "Corrupt"
+
+
+def test_config_au_full_depth_on_30_second_clips():
+    """Config AU at its full 12 layers on the audio workload's own input:
+    four 30 s clips of three sines plus noise (seed 3) through the GPU log-mel
+    front end (2999 frames, 750 tokens each), then the 754-token audio prompt
+    through the 24-layer shape-A text encoder (vocab 262144).
+
+    Each stage is checked from the GPU's own input to that stage, as the scalar
+    oracle needs minutes for the whole tower: the SSCP output and layer 1
+    against the oracle's one-layer tower, layers 6 and 12 against the oracle's
+    single-layer path (the forward pass's own per-layer code) applied to the
+    GPU's layer 5 and 11 outputs, and the output projection + unscaled norm +
+    text projection (audio.rs:1085-1133) in float64 from the GPU's layer-12
+    output. The four-clip batch equals single calls bit for bit, and the
+    prompt's embedding at dims 768 and 128 matches the text oracle run on the
+    GPU's soft tokens (audio_embedder.rs:223-267)."""
+    tc = svl_synth.config_a()
+    c = svl_synth.config_au(12, text=tc)
+    aw = svl_synth.audio_weights(c, 768, seed=0)
+    am = A.AudioModel(A.AudioConfig.from_json_value(c), aw, 768)
+    clips = svl_synth.sine_clips(4, seed=3)
+    mels = A.LogMel.get().compute_batch(clips)
+    assert all(m.frames == 2999 and m.audio_tokens() == 750 for m in mels)
+
+    batch = am.forward_batch(mels)
+    out = am.forward(mels[0], capture_hidden=True)
+    assert np.array_equal(out.pooled(), batch[0].pooled())
+    assert np.array_equal(am.forward(mels[3]).pooled(), batch[3].pooled())
+    hs = out.hidden_states()
+    assert len(hs) == 12 and hs[0].shape == (750, 1024)
+    for h in hs:
+        assert np.isfinite(h).all()
+
+    tw = svl_synth.weights(tc, seed=0)
+    tm = S.TextModel(S.TextConfig.from_json_value(tc), tw)
+    emb = A.AudioEmbedder(tm, am, A.AudioSpecialTokens())
+    got = {d: emb.embed_mel(mels[0], d) for d in (768, 128)}
+    soft = out.pooled()
+    tokens = A.AudioSpecialTokens()
+    ids = [tokens.bos, tokens.boa] + [tokens.audio] * 750 + [tokens.eoa, tokens.eos]
+
+    om12 = O.OracleAudioModel(c, aw, 768)
+    om1 = O.OracleAudioModel(svl_synth.config_au(1, text=tc), aw, 768)
+    ot = O.OracleTextModel(tc, tw)
+    valid = np.ones(750, bool)
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        f_text = ex.submit(lambda: ot.forward(ids, features=soft, feature_start=2,
+                                              feature_count=750)["normalized"])
+        f_one = ex.submit(lambda: om1.forward(mels[0].features, mels[0].mask.astype(bool), True))
+        f_l6 = ex.submit(lambda: om12.layer(5, hs[4], valid))
+        f_l12 = ex.submit(lambda: om12.layer(11, hs[10], valid))
+
+        def rel(g, r):
+            return float(np.abs(np.asarray(g, np.float64) - r).max() / np.abs(r).max())
+
+        one = f_one.result()
+        e = rel(out.sscp_output(), one["sscp_output"])
+        print(f"SSCP output: relative max error {e:.3g}", flush=True)
+        assert e <= 1e-4
+        for label, g_, r_ in (("layer 1", hs[0], one["hidden_states"][0]),
+                              ("layer 6", hs[5], f_l6.result()),
+                              ("layer 12", hs[11], f_l12.result())):
+            e = rel(g_, r_)
+            print(f"{label}: relative max error {e:.3g}", flush=True)
+            assert e <= 1e-4, label
+
+        G = "audio_tower.output_proj"
+        p = hs[11].astype(np.float64) @ aw[G + ".weight"].astype(np.float64).T + \
+            aw[G + ".bias"].astype(np.float64)
+        p = p / np.sqrt((p * p).mean(1, keepdims=True) + 1e-6)
+        want = p @ aw["embed_audio.embedding_projection.weight"].astype(np.float64).T
+        check(soft, want, "soft tokens from the layer-12 output")
+
+        ref = f_text.result()
+    for d in (768, 128):
+        check(got[d], O.truncate_and_normalize(ref, d), f"754-token audio prompt dim {d}")

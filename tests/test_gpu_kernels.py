@@ -131,6 +131,33 @@ def test_attention_matches_oracle(seq, nh, nkv, hd, window):
     np.testing.assert_allclose(host(out), ref, atol=1e-4, rtol=1e-4)
 
 
+@pytest.mark.parametrize("seq,nh,nkv,hd,window", [
+    (37, 3, 1, 256, None), (50, 8, 8, 128, 7), (131, 6, 2, 128, None), (300, 4, 4, 64, 40),
+    (33, 4, 1, 512, None), (1000, 3, 1, 256, 100)])
+def test_attention_ignores_memory_past_the_keys(seq, nh, nkv, hd, window):
+    """The last key tile of a row reaches past the row end; those keys must
+    read as zero. K and V here sit in allocations whose rows after the last
+    key are NaN, so any read of them makes the output non-finite (and the
+    call fails with Internal)."""
+    rng = np.random.default_rng(7 * seq + hd)
+    q = (rng.standard_normal((seq, nh, hd)) * 0.25).astype(np.float32)
+    k = (rng.standard_normal((seq, nkv, hd)) * 0.25).astype(np.float32)
+    v = rng.standard_normal((seq, nkv, hd)).astype(np.float32)
+    pad = 64 * nkv * hd
+
+    def poisoned(a):
+        t = torch.full((a.size + pad,), float("nan"), dtype=torch.float32, device=DEV)
+        t[:a.size] = dev(a.reshape(-1))
+        return t
+
+    out = empty(seq * nh * hd)
+    S.bidirectional_attention(dev(q), poisoned(k), poisoned(v), seq, nh, nkv, hd, window, 1.0, out)
+    got = host(out)
+    assert np.isfinite(got).all()
+    ref = O.bidirectional_attention(q, k, v, seq, nh, nkv, hd, window, 1.0)
+    np.testing.assert_allclose(got, ref, atol=1e-4, rtol=1e-4)
+
+
 def test_elementwise_kats():  # kernels.rs:1151-1160, 1301-1316
     out = empty(2)
     S.add(dev([1, 2]), dev([3, 4]), 2, out)

@@ -290,3 +290,28 @@ def test_weight_inventory_is_validated():  # weights.rs:130-166
     with pytest.raises(S.SvlError) as e:
         S.TextModel(c, w4)
     assert e.value.kind == "Internal"
+
+
+def _to_bf16_bits(a):
+    """f32_to_bf16 (bf16.rs:21-40): round to nearest, ties to even."""
+    b = np.ascontiguousarray(a, np.float32).view(np.uint32)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_bf16_weights_equal_their_f32_widening():
+    """The tiny model with every weight rounded to BF16 and passed as BF16
+    views (widened by the library, safetensors.rs:69-110) gives the same bits
+    as the widened values passed as F32, and matches the oracle on them."""
+    cfg, w, g = tiny()
+    bf = {k: S.RawTensor("BF16", np.shape(v), _to_bf16_bits(v)) for k, v in w.items()}
+    wide = {k: t.to_f32() for k, t in bf.items()}
+    for k, v in w.items():
+        assert np.abs(wide[k] - v).max() <= np.abs(v).max() * 2.0 ** -8, k
+    a, b = model(cfg, bf), model(cfg, wide)
+    ref = O.OracleTextModel(cfg, wide)
+    for case in g["cases"]:
+        x, y = a.forward(case["input_ids"]), b.forward(case["input_ids"])
+        assert x.normalized().tobytes() == y.normalized().tobytes()
+        assert x.projected().tobytes() == y.projected().tobytes()
+        assert_embedding_parity(x.normalized(), ref.forward(case["input_ids"])["normalized"],
+                                "BF16 tiny model")

@@ -286,3 +286,28 @@ def test_attention_matches_a_float64_softmax_with_soft_cap():
             p = np.exp(s - s.max())
             want[i, sl] = (p / p.sum()) @ v[keys, sl].astype(np.float64)
     np.testing.assert_allclose(got, want, atol=2e-5)
+
+
+def test_single_layer_path_composes_to_the_forward_pass():
+    """OracleAudioModel.layer runs the forward pass's own per-layer code:
+    chaining it from the SSCP output reproduces every layer output bit for bit
+    (the fixture, and a 2-layer config-AU tower on a fully valid clip)."""
+    import svl_synth
+    cfg, g, w = fixture()
+    out = run(cfg, w, g)
+    m = O.OracleAudioModel(cfg, w, cfg["text_config"]["hidden_size"])
+    h = out["sscp_output"]
+    for layer in range(2):
+        h = m.layer(layer, h, np.ones(h.shape[0], bool))
+        assert np.array_equal(h, out["hidden_states"][layer]), f"fixture layer {layer}"
+    c = svl_synth.config_au(2)
+    aw = svl_synth.audio_weights(c, 768, seed=5)
+    om = O.OracleAudioModel(c, aw, 768)
+    mel = svl_synth.mel_clips([97], seed=21)[0]
+    ref = om.forward(mel.features, mel.mask.astype(bool), capture_hidden=True)
+    h = ref["sscp_output"]
+    for layer in range(2):
+        h = om.layer(layer, h, np.ones(h.shape[0], bool))
+        assert np.array_equal(h, ref["hidden_states"][layer]), f"config AU layer {layer}"
+    with pytest.raises(O.OracleError):
+        om.layer(2, h, np.ones(h.shape[0], bool))
