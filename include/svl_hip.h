@@ -199,6 +199,20 @@ svl_status svl_bidirectional_attention(const float *d_q, const float *d_k, const
                                        int64_t num_kv_heads, int64_t head_dim,
                                        int64_t sliding_window, float scale, float *d_out,
                                        void *stream);
+/* No counterpart in the reference: svl_bidirectional_attention for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments, kernels
+ * and results; its work items, position arrays and non-finite flag live in
+ * a 320 KiB device array of the library, one per GPU, instead of per-call
+ * allocations. At most 8192 keys and 16384 work items (LimitExceeded
+ * beyond). Every call on a GPU shares that GPU's array: calls in one process
+ * are serialised by a lock and return after their stream has finished, and
+ * calls that overlap on one GPU by other means race. */
+svl_status svl_bidirectional_attention_noalloc(const float *d_q, const float *d_k,
+                                               const float *d_v, int64_t seq_len,
+                                               int64_t num_heads, int64_t num_kv_heads,
+                                               int64_t head_dim, int64_t sliding_window,
+                                               float scale, float *d_out, void *stream);
 /* kernels.rs:386-400 gelu_tanh / geglu, kernels.rs:44-52 add. */
 svl_status svl_gelu_tanh(const float *d_in, int64_t n, float *d_out, void *stream);
 svl_status svl_geglu(const float *d_gate, const float *d_up, int64_t n, float *d_out,

@@ -814,6 +814,8 @@ svl_status svl_init(int device_ordinal, svl_ctx **out) {
         return fail(SVL_UNSUPPORTED, "device %d is %s; this library is built for gfx950",
                     device_ordinal, prop.gcnArchName);
     HIP_TRY(hipSetDevice(device_ordinal));
+    void *scratch = nullptr;  // the allocation-free entry points' device scratch
+    HIP_TRY(noalloc_scratch(device_ordinal, &scratch));
     *out = new svl_ctx{device_ordinal};
     return SVL_OK;
 }
@@ -1246,10 +1248,8 @@ svl_status svl_rope_with_inv_freq(float *d_values, int64_t seq_len, int64_t num_
     return st;
 }
 
-svl_status svl_bidirectional_attention(const float *d_q, const float *d_k, const float *d_v,
-                                       int64_t seq_len, int64_t num_heads, int64_t num_kv_heads,
-                                       int64_t head_dim, int64_t sliding_window, float scale,
-                                       float *d_out, void *stream) {
+static svl_status check_attention_shape(int64_t seq_len, int64_t num_heads, int64_t num_kv_heads,
+                                        int64_t head_dim, float scale) {
     if (head_dim <= 0) return fail(SVL_INTERNAL, "attention head dimension must be positive");
     if (num_heads <= 0 || num_kv_heads <= 0)
         return fail(SVL_INTERNAL, "attention head counts must be positive");
@@ -1259,10 +1259,41 @@ svl_status svl_bidirectional_attention(const float *d_q, const float *d_k, const
     if (!std::isfinite(scale)) return fail(SVL_INTERNAL, "attention scale must be finite");
     if (seq_len < 0 || seq_len * num_heads * head_dim > MAX_TENSOR_ELEMENTS)
         return fail(SVL_LIMIT, "attention would allocate above the cap");
-    if (seq_len == 0) return SVL_OK;
     if (seq_len > 8192 && attn_block_vectors((int)head_dim) == 0)
         return fail(SVL_UNSUPPORTED, "sequence above 8192 keys for head_dim %lld",
                     (long long)head_dim);
+    return SVL_OK;
+}
+
+// One row of seq_len keys, q/k/v/out packed [seq, heads, head_dim].
+static AttnArgs seam_attention_args(const float *d_q, const float *d_k, const float *d_v,
+                                    int64_t seq_len, int64_t num_heads, int64_t num_kv_heads,
+                                    int64_t head_dim, int64_t sliding_window, float scale,
+                                    float *d_out) {
+    AttnArgs a{};
+    a.q = d_q;
+    a.k = d_k;
+    a.v = d_v;
+    a.out = d_out;
+    a.ldq = num_heads * head_dim;
+    a.ldk = a.ldv = num_kv_heads * head_dim;
+    a.ldo = num_heads * head_dim;
+    a.nh = (int)num_heads;
+    a.nkv = (int)num_kv_heads;
+    a.hd = (int)head_dim;
+    a.window = sliding_window < 0 ? -1 : (int)std::min<int64_t>(sliding_window, INT32_MAX);
+    a.scale = scale;
+    a.tokens = seq_len;
+    a.max_len = seq_len;
+    return a;
+}
+
+svl_status svl_bidirectional_attention(const float *d_q, const float *d_k, const float *d_v,
+                                       int64_t seq_len, int64_t num_heads, int64_t num_kv_heads,
+                                       int64_t head_dim, int64_t sliding_window, float scale,
+                                       float *d_out, void *stream) {
+    ST_TRY(check_attention_shape(seq_len, num_heads, num_kv_heads, head_dim, scale));
+    if (seq_len == 0) return SVL_OK;
     const int bv = attn_block_vectors((int)head_dim);
     const int G = (int)(num_heads / num_kv_heads);
     std::vector<AttnTile> tiles;
@@ -1281,25 +1312,12 @@ svl_status svl_bidirectional_attention(const float *d_q, const float *d_k, const
     HIP_TRY(hipMalloc((void **)&dt, std::max<size_t>(tiles.size(), 1) * sizeof(AttnTile)));
     HIP_TRY(hipMalloc((void **)&dp, pos.size() * 4));
     HIP_TRY(hipMalloc((void **)&dl, rl.size() * 4));
-    AttnArgs a{};
-    a.q = d_q;
-    a.k = d_k;
-    a.v = d_v;
-    a.out = d_out;
-    a.ldq = num_heads * head_dim;
-    a.ldk = a.ldv = num_kv_heads * head_dim;
-    a.ldo = num_heads * head_dim;
-    a.nh = (int)num_heads;
-    a.nkv = (int)num_kv_heads;
-    a.hd = (int)head_dim;
-    a.window = sliding_window < 0 ? -1 : (int)std::min<int64_t>(sliding_window, INT32_MAX);
-    a.scale = scale;
+    AttnArgs a = seam_attention_args(d_q, d_k, d_v, seq_len, num_heads, num_kv_heads, head_dim,
+                                     sliding_window, scale, d_out);
     a.tiles = dt;
     a.n_tiles = (int)tiles.size();
     a.pos = dp;
     a.rowlen = dl;
-    a.tokens = seq_len;
-    a.max_len = seq_len;
     a.flag = flag;
     svl_status st = SVL_OK;
     if ((!tiles.empty() && hipMemcpyAsync(dt, tiles.data(), tiles.size() * sizeof(AttnTile),
@@ -1315,6 +1333,44 @@ svl_status svl_bidirectional_attention(const float *d_q, const float *d_k, const
     (void)hipFree(dp);
     (void)hipFree(dl);
     return st;
+}
+
+std::mutex g_noalloc_mu;
+
+svl_status svl_bidirectional_attention_noalloc(const float *d_q, const float *d_k,
+                                               const float *d_v, int64_t seq_len,
+                                               int64_t num_heads, int64_t num_kv_heads,
+                                               int64_t head_dim, int64_t sliding_window,
+                                               float scale, float *d_out, void *stream) {
+    ST_TRY(check_attention_shape(seq_len, num_heads, num_kv_heads, head_dim, scale));
+    if (seq_len == 0) return SVL_OK;
+    if (seq_len > NOALLOC_MAX_KEYS)
+        return fail(SVL_LIMIT, "%lld keys: the allocation-free attention takes at most %d",
+                    (long long)seq_len, NOALLOC_MAX_KEYS);
+    const int bv = attn_block_vectors((int)head_dim);
+    const int64_t G = num_heads / num_kv_heads;
+    const int64_t per_head = bv > 0 ? (seq_len * G + bv - 1) / bv : 0;
+    if (per_head * num_kv_heads > NOALLOC_MAX_TILES)
+        return fail(SVL_LIMIT, "%lld attention work items: the allocation-free attention takes "
+                    "at most %d", (long long)(per_head * num_kv_heads), NOALLOC_MAX_TILES);
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    void *base = nullptr;
+    HIP_TRY(noalloc_scratch(dev, &base));
+    char *b = (char *)base;
+    AttnArgs a = seam_attention_args(d_q, d_k, d_v, seq_len, num_heads, num_kv_heads, head_dim,
+                                     sliding_window, scale, d_out);
+    a.tiles = (const AttnTile *)(b + NOALLOC_TILES_OFF);
+    a.n_tiles = (int)(per_head * num_kv_heads);
+    a.pos = (const int32_t *)(b + NOALLOC_POS_OFF);
+    a.rowlen = (const int32_t *)(b + NOALLOC_LEN_OFF);
+    a.flag = (int *)(b + NOALLOC_FLAG_OFF);
+    hipStream_t s = (hipStream_t)stream;
+    // one call at a time per process: every call on a GPU shares its scratch
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    HIP_TRY(launch_noalloc_attn_setup(base, (int)seq_len, (int)per_head, bv, a.n_tiles, s));
+    if (launch_attention(a, s) != hipSuccess) return fail(SVL_DEVICE, "attention launch failed");
+    return seam_finish(s, a.flag, "attention");
 }
 
 static svl_status seam_elementwise(const char *what, int kind, const float *a, const float *b,

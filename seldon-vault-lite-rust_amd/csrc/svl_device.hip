@@ -7,3 +7,4 @@
 #include "audio.hip"
 #include "mel.hip"
 #include "search.hip"
+#include "noalloc.hip"

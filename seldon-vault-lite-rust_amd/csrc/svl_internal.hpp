@@ -110,6 +110,23 @@ struct AttnArgs {
 int attn_block_vectors(int hd);
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
 
+// Scratch of the allocation-free attention entry point (noalloc.hip), one
+// copy per GPU: work items, then per-token positions and row lengths, then
+// the non-finite flag. 320 KiB in all.
+constexpr int NOALLOC_MAX_KEYS = 8192;
+constexpr int NOALLOC_MAX_TILES = 16384;
+constexpr size_t NOALLOC_TILES_OFF = 0;
+constexpr size_t NOALLOC_POS_OFF = NOALLOC_TILES_OFF + NOALLOC_MAX_TILES * sizeof(AttnTile);
+constexpr size_t NOALLOC_LEN_OFF = NOALLOC_POS_OFF + NOALLOC_MAX_KEYS * sizeof(int32_t);
+constexpr size_t NOALLOC_FLAG_OFF = NOALLOC_LEN_OFF + NOALLOC_MAX_KEYS * sizeof(int32_t);
+constexpr size_t NOALLOC_SCRATCH_BYTES = NOALLOC_FLAG_OFF + 256;
+// Device address of `device`'s scratch (looked up once per device).
+hipError_t noalloc_scratch(int device, void **out);
+// Work items of one row of `seq` keys (per_head per KV head, bv query
+// vectors each), positions 0..seq-1, row lengths seq, flag cleared.
+hipError_t launch_noalloc_attn_setup(void *base, int seq, int per_head, int bv, int n_tiles,
+                                     hipStream_t s);
+
 // Per row r of [offsets[r], offsets[r+1]): pos[t] = t - offsets[r] and
 // rowlen[t] = offsets[r+1] - offsets[r] (rowlen may be null).
 hipError_t launch_positions(const int64_t *offsets, int batch, int32_t *pos, int32_t *rowlen,

@@ -112,7 +112,7 @@ EXPORTED = [
     "svl_tokenizer_unk_id", "svl_tokenizer_pad_id", "svl_tokenizer_is_special_id",
     "svl_text_embed_texts", "svl_vector_index_create", "svl_vector_index_destroy",
     "svl_vector_index_size", "svl_vector_index_dimension", "svl_vector_rank",
-    "svl_vector_rank_device", "svl_tensor_to_f32",
+    "svl_vector_rank_device", "svl_tensor_to_f32", "svl_bidirectional_attention_noalloc",
 ]
 
 _lib = None
@@ -171,6 +171,8 @@ def lib():
         L.svl_rope_with_inv_freq.argtypes = [vp, i64, i64, i64, vp, i64, i64, vp]
         L.svl_rope_inv_freq.argtypes = [i64, f32, vp]
         L.svl_bidirectional_attention.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, f32, vp, vp]
+        L.svl_bidirectional_attention_noalloc.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64,
+                                                          f32, vp, vp]
         L.svl_gelu_tanh.argtypes = [vp, i64, vp, vp]
         L.svl_geglu.argtypes = [vp, vp, i64, vp, vp]
         L.svl_add.argtypes = [vp, vp, i64, vp, vp]
@@ -742,6 +744,14 @@ def bidirectional_attention(q, k, v, seq, nh, nkv, hd, window, scale, out):
     _check(lib().svl_bidirectional_attention(_dp(q), _dp(k), _dp(v), seq, nh, nkv, hd,
                                              -1 if window is None else int(window), scale,
                                              _dp(out), _stream()))
+
+
+def bidirectional_attention_noalloc(q, k, v, seq, nh, nkv, hd, window, scale, out):
+    """bidirectional_attention without device allocation (the library's
+    per-GPU scratch array; at most 8192 keys)."""
+    _check(lib().svl_bidirectional_attention_noalloc(
+        _dp(q), _dp(k), _dp(v), seq, nh, nkv, hd, -1 if window is None else int(window), scale,
+        _dp(out), _stream()))
 
 
 def gelu_tanh(x, n, out):
