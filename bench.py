@@ -58,6 +58,8 @@ def parse():
                     help="timed batches of the vector-search workload (0 skips it)")
     ap.add_argument("--long-steps", type=int, default=5,
                     help="timed batches of the 8 x 2048-token workload (0 skips it)")
+    ap.add_argument("--shape-b-steps", type=int, default=10,
+                    help="timed batches of the headline batch at the manifest shape (0 skips it)")
     ap.add_argument("--host-steps", type=int, default=10,
                     help="timed batches of the host-ids to host-vectors path (0 skips it)")
     ap.add_argument("--row-groups", type=int, default=3,
@@ -153,6 +155,65 @@ def cpu_baseline(cfg, weights, rows_all, n_rows, gpu_out):
               "ok": bool(worst_abs <= 1e-4 and worst_cos >= 0.99999),
               "against": "scalar C oracle, same rows of the timed batch's output"}
     return cpu, parity
+
+
+def shape_b_leg(rows, offsets, steps, groups):
+    """The headline batch (same 64 rows and ids) through the reference
+    manifest's own shape: hidden 512, 4 query heads, 2 KV heads of 256 on the
+    20 sliding layers and 1 KV head of 512 on the 4 global layers, FFN 2048,
+    PLE 512, vocab 262144, random-init weights (seed 0)."""
+    import numpy as np
+    import torch
+
+    import svl_amd
+    import svl_synth
+
+    cfg = svl_synth.config_b()
+    w = svl_synth.weights(cfg, seed=0)
+    model = svl_amd.TextModel(svl_amd.TextConfig.from_json_value(cfg), w)
+    del w
+    model.set_stream_split(groups)
+    ids = torch.from_numpy(np.concatenate(rows).astype(np.int32)).to("cuda:0")
+    out = torch.zeros((len(rows), sum(DIMS)), dtype=torch.float32, device="cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        model.forward_device(ids.data_ptr(), offsets, DIMS, out.data_ptr(), stream)
+
+    step()
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(steps):
+        a = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        ms.append((time.perf_counter() - a) * 1e3)
+    p50 = float(np.median(ms))
+    assert np.isfinite(out.cpu().numpy()).all()
+    model.set_stream_split(False)
+    model.set_kernel_timing(True)
+    step()
+    torch.cuda.synchronize()
+    stats = model.kernel_stats()
+    model.close()
+    attn = stats["attention"]
+    gemm_keys = [k for k in stats if k.startswith("gemm_")]
+    gemm_ms = sum(stats[k]["ms"] for k in gemm_keys)
+    gemm_flops = sum(stats[k]["work"] for k in gemm_keys)
+    flops = gemm_flops + attn["work"]
+    return {"workload": "the headline batch (64 rows, lengths U[64,512], seed 1) through the "
+                        "reference manifest's shape: hidden 512, 4 q heads, 2 KV heads of 256 on "
+                        "20 sliding layers, 1 KV head of 512 on 4 global layers, FFN 2048, PLE "
+                        "512, vocab 262144",
+            "embeddings_per_s": round(len(rows) / (p50 * 1e-3), 2), "p50_ms": round(p50, 3),
+            "forward_tflops": round(flops / (p50 * 1e-3) / 1e12, 2),
+            "forward_frac_of_fp32_mfma_peak": round(flops / (p50 * 1e-3) / 1e12
+                                                    / PEAK_FP32_MFMA_TFLOPS, 4),
+            "gemm_tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 2),
+            "attention_ms_per_batch": round(attn["ms"], 3),
+            "attention_tflops": round(attn["work"] / (attn["ms"] * 1e-3) / 1e12, 2),
+            "kernels": {k: round(v["ms"], 3) for k, v in stats.items() if v["launches"]},
+            "steps": steps}
 
 
 def long_context_leg(model, steps):
@@ -551,6 +612,8 @@ def main():
     search = (search_leg(dev, args.search_steps, args.cpu_sample_rows != 0)
               if args.search_steps > 0 else None)
     long_ctx = long_context_leg(model, args.long_steps) if args.long_steps > 0 else None
+    shape_b = (shape_b_leg(rows, offsets, args.shape_b_steps, args.row_groups)
+               if args.shape_b_steps > 0 else None)
     cpu, parity = cpu_baseline(cfg, weights, rows, args.cpu_sample_rows, gpu_out)
 
     breakdown = {k: {"ms_per_step": round(v["ms"] / args.steps, 3),
@@ -583,6 +646,7 @@ def main():
         "host_to_host": host,
         "kernels": breakdown,
         "long_context": long_ctx,
+        "shape_b": shape_b,
         "image": image,
         "audio": audio,
         "search": search,

@@ -234,50 +234,70 @@ __device__ __forceinline__ float fold_xor16_32_sum(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Head dims above 256 (512: the global layers of the reference manifest) split
+// each 16-vector group's dims over DS = HD / 256 waves: every wave holds its
+// 256 dims of the queries and of the output, computes the scores' partial sums
+// over them, and the DS partial sums of a score meet through LDS (added in
+// dim-block order, so every wave of a group holds the same bits); the softmax
+// is then repeated identically in each wave, which applies P to its own dims of
+// V. Register use per wave is that of head_dim 256.
+template <int HD>
+constexpr int attn_dim_split() { return HD > 256 ? HD / 256 : 1; }
+
+template <int HD, int WAVES>
+constexpr int attn_min_blocks() { return HD <= 256 && WAVES == 4 ? 2 : 1; }
+
 template <int HD, int WAVES, int KT>
-__global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(AttnArgs p) {
+__global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void attn16_kernel(AttnArgs p) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int NKB = KT / 16;         // 16-key blocks per tile
-    constexpr int SPLIT = 8 / WAVES;     // workgroups per 128-vector work item
-    constexpr int RPI = 256 / HD;        // key rows per 1 KB DMA instruction
-    constexpr int CPR = HD / 4;          // 16-byte chunks per key row
-    constexpr int INSTR_PER_WAVE = KT / RPI / WAVES;
-    static_assert(HD == 64 || HD == 128 || HD == 256, "head dim");
+    constexpr int DS = attn_dim_split<HD>();  // waves per 16-vector group
+    constexpr int HDW = HD / DS;              // head dims per wave
+    constexpr int NKB = KT / 16;              // 16-key blocks per tile
+    constexpr int VPW = 16 * WAVES / DS;      // query vectors per workgroup
+    constexpr int SPLIT = 128 / VPW;          // workgroups per 128-vector work item
+    constexpr int INSTR_PER_WAVE = KT * HD / 256 / WAVES;  // 1 KB DMA instructions per operand
+    static_assert(HD == 64 || HD == 128 || HD == 256 || HD == 512, "head dim");
     static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4 || WAVES == 8, "waves");
-    static_assert(KT % 16 == 0 && INSTR_PER_WAVE >= 1 && (KT / RPI) % WAVES == 0, "key tile");
+    static_assert(WAVES % DS == 0 && 128 % VPW == 0, "vector groups");
+    static_assert(KT % 16 == 0 && INSTR_PER_WAVE >= 1 && (KT * HD / 256) % WAVES == 0, "key tile");
     // One LDS object per stage, addressed with compile-time stage indices:
     // the compiler can then see that the DMA filling one stage does not alias
     // the reads of the other and need not drain it before reading.
     __shared__ float Ks0[KT * HD], Ks1[KT * HD];
     __shared__ float Vs0[KT * HD], Vs1[KT * HD];
+    // partial scores of each wave (DS > 1 only)
+    __shared__ f32x4 Sx[DS > 1 ? WAVES * NKB * 64 : 1];
 
     const AttnTile tile = p.tiles[blockIdx.x / SPLIT];
     const int G = p.nh / p.nkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
+    const int dpart = DS > 1 ? wave % DS : 0;  // this wave's block of head dims
+    const int group = wave / DS;
     const int nvec = tile.len * G;
-    const int vbase = tile.qv0 + (blockIdx.x % SPLIT) * 16 * WAVES;
+    const int vbase = tile.qv0 + (blockIdx.x % SPLIT) * VPW;
     if (vbase >= nvec) return;   // the whole workgroup: a part past the row's vectors
-    const int v = vbase + wave * 16 + l16;
+    const int v = vbase + group * 16 + l16;
     const bool vvalid = v < nvec;
     const int vq = vvalid ? v : nvec - 1;
     const int qpos = vq / G;
     const int qhead = tile.kvh * G + (vq - qpos * G);
-    const float *qrow = p.q + (int64_t)(tile.tok0 + qpos) * p.ldq + qhead * HD;
+    const float *qrow = p.q + (int64_t)(tile.tok0 + qpos) * p.ldq + qhead * HD + dpart * HDW;
 
     // Query fragments pre-scaled by scale * log2(e): S^T comes out in log2
-    // units. Fragment c holds dims 16 c + 4 (lane / 16) .. + 3.
+    // units. Fragment c holds dims 16 c + 4 (lane / 16) .. + 3 of the wave's
+    // block.
     const float scale2 = p.scale * 1.4426950408889634f;
-    f32x4 qf[HD / 16];
+    f32x4 qf[HDW / 16];
 #pragma unroll
-    for (int c = 0; c < HD / 16; ++c) qf[c] = *(const f32x4 *)(qrow + 16 * c + 4 * g) * scale2;
+    for (int c = 0; c < HDW / 16; ++c) qf[c] = *(const f32x4 *)(qrow + 16 * c + 4 * g) * scale2;
 
-    f32x4 o[HD / 16];
+    f32x4 o[HDW / 16];
 #pragma unroll
-    for (int t = 0; t < HD / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < HDW / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_ref = -INFINITY, l_run = 0.f;
 
-    const int v_last = min(vbase + 16 * WAVES, nvec) - 1;
+    const int v_last = min(vbase + VPW, nvec) - 1;
     const int p_lo = vbase / G, p_hi = v_last / G;
     int k_lo = 0, k_hi = tile.len - 1;
     if (p.window >= 0) {
@@ -295,14 +315,16 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.v + (int64_t)tile.tok0 * p.ldv + tile.kvh * HD), (short)0,
         ((tile.len - 1) * ldv + HD) * 4, 0x00020000);
-    // One DMA instruction moves RPI key rows (1 KB) of the tile: lane l
-    // fills chunk slot l % CPR of row l / CPR (K: with global chunk
-    // slot ^ (row % 16)).
+    // DMA instruction j of a tile moves floats 256 j .. 256 j + 255 of the
+    // tile (1 KB: 256 / HD rows, or 1 / (HD / 256) of a row): lane l fills
+    // chunk slot s of row r for float e = 256 j + 4 l = r HD + 4 s (K: with
+    // global chunk s ^ (r % 16)).
     int koff[INSTR_PER_WAVE], voff[INSTR_PER_WAVE];
 #pragma unroll
     for (int q = 0; q < INSTR_PER_WAVE; ++q) {
-        const int r = (wave * INSTR_PER_WAVE + q) * RPI + lane / CPR;
-        const int slot = lane % CPR;
+        const int e = (wave * INSTR_PER_WAVE + q) * 256 + 4 * lane;
+        const int r = e / HD;
+        const int slot = (e % HD) / 4;
         koff[q] = (r * ldk + 4 * (slot ^ (r & 15))) * 4;
         voff[q] = (r * ldv + 4 * slot) * 4;
     }
@@ -311,14 +333,14 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(
         float *vd = decltype(st)::value == 0 ? Vs0 : Vs1;
 #pragma unroll
         for (int q = 0; q < INSTR_PER_WAVE; ++q) {
-            const int r0 = (wave * INSTR_PER_WAVE + q) * RPI;
+            const int f0 = (wave * INSTR_PER_WAVE + q) * 256;
             // the tile offset goes into the range-checked vector offset (the
             // scalar offset is outside the buffer's bounds check)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rk, (__attribute__((address_space(3))) void *)&kd[r0 * HD], 16,
+                rk, (__attribute__((address_space(3))) void *)&kd[f0], 16,
                 koff[q] + k0 * ldk * 4, 0, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rv, (__attribute__((address_space(3))) void *)&vd[r0 * HD], 16,
+                rv, (__attribute__((address_space(3))) void *)&vd[f0], 16,
                 voff[q] + k0 * ldv * 4, 0, 0, 0);
         }
     };
@@ -337,24 +359,27 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(
 
         // S^T for keys kb * 16 + 4 (lane / 16) + r (register r of block kb)
         // and query vector lane % 16. K row kb * 16 + l16 holds dim chunk
-        // 4 c + g at slot (4 c + g) ^ l16.
+        // ch = 4 c + g (of the wave's dim block: ch + HDW / 4 * dpart) at
+        // slot ch ^ l16.
         // The fragments of chunk c + 1 are read while chunk c's MFMAs run,
         // and the two key blocks' chains alternate.
         const float *kb0 = (cur == 0 ? Ks0 : Ks1) + l16 * HD;
+        const int ch0 = dpart * (HDW / 4);
         f32x4 s[NKB], kf[NKB];
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
             s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            kf[kb] = *(const f32x4 *)(kb0 + kb * 16 * HD + 4 * (g ^ l16));
+            kf[kb] = *(const f32x4 *)(kb0 + kb * 16 * HD + 4 * ((ch0 + g) ^ l16));
         }
 #pragma unroll
-        for (int c = 0; c < HD / 16; ++c) {
+        for (int c = 0; c < HDW / 16; ++c) {
             f32x4 nf[NKB];
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) {
                 nf[kb] = kf[kb];
-                if (c + 1 < HD / 16)
-                    nf[kb] = *(const f32x4 *)(kb0 + kb * 16 * HD + 4 * ((4 * (c + 1) + g) ^ l16));
+                if (c + 1 < HDW / 16)
+                    nf[kb] = *(const f32x4 *)(kb0 + kb * 16 * HD +
+                                              4 * ((ch0 + 4 * (c + 1) + g) ^ l16));
             }
             // keep the reads of chunk c + 1 ahead of chunk c's MFMAs
             __builtin_amdgcn_sched_barrier(0);
@@ -365,6 +390,21 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(
                     s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kb][j], qf[c][j], s[kb], 0, 0, 0);
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) kf[kb] = nf[kb];
+        }
+        if constexpr (DS > 1) {
+            // the partial sums of the group's waves meet in LDS; the barrier
+            // at the top of the next tile keeps them until all are read
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) Sx[(wave * NKB + kb) * 64 + lane] = s[kb];
+            __syncthreads();
+            const int w0 = group * DS;
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                f32x4 t = Sx[(w0 * NKB + kb) * 64 + lane];
+#pragma unroll
+                for (int d = 1; d < DS; ++d) t = t + Sx[((w0 + d) * NKB + kb) * 64 + lane];
+                s[kb] = t;
+            }
         }
 
         // Scores in log2 units; masks only on the row-tail tile and on tiles
@@ -405,7 +445,7 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(
             const float alpha = m_ref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - m_new);
             l_run *= alpha;
 #pragma unroll
-            for (int t = 0; t < HD / 16; ++t) o[t] = o[t] * alpha;
+            for (int t = 0; t < HDW / 16; ++t) o[t] = o[t] * alpha;
             m_ref = m_new;
         }
         float psum = 0.f;
@@ -421,14 +461,15 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(
 
         // O^T += V^T P^T, keys 4 (lane / 16) + r of block kb in MFMA r: lane
         // l supplies V row kb * 16 + 4 (l / 16) + r, dims 64 c + 4 (l % 16)
-        // .. + 3, one per output tile 4 c + t (tile row i = dim 64 c + 4 i + t).
-        const float *vb = (cur == 0 ? Vs0 : Vs1) + 4 * g * HD + 4 * l16;
+        // .. + 3 of the wave's block, one per output tile 4 c + t (tile row
+        // i = dim 64 c + 4 i + t).
+        const float *vb = (cur == 0 ? Vs0 : Vs1) + 4 * g * HD + 4 * l16 + dpart * HDW;
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int c = 0; c < HD / 64; ++c) {
+                for (int c = 0; c < HDW / 64; ++c) {
                     const f32x4 va = *(const f32x4 *)(vb + (kb * 16 + r) * HD + 64 * c);
 #pragma unroll
                     for (int t = 0; t < 4; ++t)
@@ -445,10 +486,10 @@ __global__ __launch_bounds__(64 * WAVES, WAVES == 4 ? 2 : 1) void attn16_kernel(
         // lane l holds, for its query vector, dims 64 c + 16 (l / 16) + 4 r
         // + t in register r of tile 4 c + t
         const float inv = 1.0f / l_run;
-        float *orow = p.out + (int64_t)(tile.tok0 + qpos) * p.ldo + qhead * HD;
+        float *orow = p.out + (int64_t)(tile.tok0 + qpos) * p.ldo + qhead * HD + dpart * HDW;
         bool ok = isfinite(inv);
 #pragma unroll
-        for (int c = 0; c < HD / 64; ++c)
+        for (int c = 0; c < HDW / 64; ++c)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 f32x4 d;
@@ -517,7 +558,7 @@ __global__ __launch_bounds__(64) void attn_simple_kernel(AttnArgs p) {
 }
 
 int attn_block_vectors(int hd) {
-    return (hd == 64 || hd == 128 || hd == 256) ? 32 * ATTN_WAVES : 0;
+    return (hd == 64 || hd == 128 || hd == 256 || hd == 512) ? 32 * ATTN_WAVES : 0;
 }
 
 // 16x16x4 kernel with one key-tile width per head dim (so a vector's
@@ -528,13 +569,19 @@ int attn_block_vectors(int hd) {
 // 8 workgroups of fewer waves.
 template <int HD, int KT>
 static hipError_t launch_attn16(const AttnArgs &a, hipStream_t s) {
+    // a work item is 128 query vectors: 8 groups of 16, each group one wave
+    // (DS waves above head_dim 256)
+    constexpr int DS = attn_dim_split<HD>();
     const int64_t t = a.n_tiles;
     if (2 * t >= 256)
-        hipLaunchKernelGGL((attn16_kernel<HD, 4, KT>), dim3((unsigned)(2 * t)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((attn16_kernel<HD, 4 * DS, KT>), dim3((unsigned)(2 * t)),
+                           dim3(256 * DS), 0, s, a);
     else if (4 * t >= 256)
-        hipLaunchKernelGGL((attn16_kernel<HD, 2, KT>), dim3((unsigned)(4 * t)), dim3(128), 0, s, a);
+        hipLaunchKernelGGL((attn16_kernel<HD, 2 * DS, KT>), dim3((unsigned)(4 * t)),
+                           dim3(128 * DS), 0, s, a);
     else
-        hipLaunchKernelGGL((attn16_kernel<HD, 1, KT>), dim3((unsigned)(8 * t)), dim3(64), 0, s, a);
+        hipLaunchKernelGGL((attn16_kernel<HD, DS, KT>), dim3((unsigned)(8 * t)), dim3(64 * DS),
+                           0, s, a);
     return hipGetLastError();
 }
 
@@ -557,6 +604,15 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
         case 256:
             if (dma) return launch_attn16<256, 16>(a, s);
             hipLaunchKernelGGL((attn_mfma_kernel<256, ATTN_WAVES>), dim3(a.n_tiles), block, 0, s, a);
+            return hipGetLastError();
+        case 512:
+            if (dma) return launch_attn16<512, 16>(a, s);
+            // a row whose buffer window would pass 2 GiB (only strides of 128
+            // or more KV heads get there) takes the generic kernel
+            if (!a.pos || !a.rowlen || a.max_len <= 0 || a.max_len > ATTN_SIMPLE_MAX_KEYS)
+                return hipErrorInvalidValue;
+            hipLaunchKernelGGL(attn_simple_kernel, dim3((unsigned)(a.tokens * a.nh)), dim3(64), 0,
+                               s, a);
             return hipGetLastError();
         default:
             if (!a.pos || !a.rowlen) return hipErrorInvalidValue;

@@ -108,3 +108,41 @@ def test_headline_batch_matches_oracle():
             off += d
     print(f"headline batch: {len(pick)} rows x {len(DIMS)} dims, worst max-abs {worst_abs:.3g}, "
           f"worst cosine {worst_cos:.8f}", flush=True)
+
+
+@pytest.mark.gpu
+def test_shape_b_headline_batch_matches_oracle():
+    """The same 64-row batch through the reference manifest's shape (hidden
+    512, 4 query heads, 2 KV heads of 256 on sliding layers and 1 KV head of
+    512 on the 4 global layers, FFN 2048, PLE 512) at 24 layers and vocab
+    262144, three row groups; 8 rows (two per quarter of the batch) against
+    the oracle at every Matryoshka dim."""
+    cfg = svl_synth.config_b()
+    w = svl_synth.weights(cfg, seed=0)
+    lengths = svl_synth.row_lengths(BATCH, LEN_LO, LEN_HI, seed=1)
+    rows = svl_synth.token_rows(cfg["vocab_size"], lengths, seed=1)
+    offsets = np.zeros(BATCH + 1, np.int64)
+    offsets[1:] = np.cumsum(lengths)
+    m = S.TextModel(S.TextConfig.from_json_value(cfg), w)
+    m.set_stream_split(GROUPS)
+    ids = torch.from_numpy(np.concatenate(rows).astype(np.int32)).to("cuda:0")
+    out = torch.zeros((BATCH, sum(DIMS)), dtype=torch.float32, device="cuda:0")
+    m.forward_device(ids.data_ptr(), offsets, DIMS, out.data_ptr(),
+                     torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    m.close()
+    pick = [int(r) for q in range(4) for r in
+            np.random.default_rng(13 + q).choice(np.arange(16 * q, 16 * q + 16), 2, replace=False)]
+    ref = O.OracleTextModel(cfg, w).forward_rows([rows[r] for r in pick], threads=8)
+    for r, o in zip(pick, ref):
+        off = 0
+        for d in DIMS:
+            want = O.truncate_and_normalize(o["normalized"], d)
+            have = got[r, off:off + d]
+            a = float(np.abs(have - want).max())
+            c = cosine(have, want)
+            assert a <= MAX_ABS and c >= MIN_COS, \
+                f"row {r} (len {lengths[r]}) dim {d}: max-abs {a:.3g} cosine {c:.8f}"
+            off += d
+    print(f"shape B batch: rows {pick} match the oracle at dims {DIMS}", flush=True)

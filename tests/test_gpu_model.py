@@ -157,6 +157,13 @@ def test_shape_b_manifest_shape_matches_oracle():
     _shape_parity(cfg, [40, 257])
 
 
+def test_shape_b_long_rows_match_oracle():
+    # Rows past the 512 window on the sliding layers and a 1100 x 1100 score
+    # matrix at head_dim 512 on the full layer (layer 6 of 6).
+    cfg = svl_synth.config_b(layers=6, vocab=4096)
+    _shape_parity(cfg, [1100, 700])
+
+
 def test_packed_batch_equals_independent_calls_bit_for_bit():
     cfg = svl_synth.config_a(layers=3, vocab=4096)
     w = svl_synth.weights(cfg)
