@@ -317,3 +317,55 @@ def test_vision_weight_inventory(small):
     with pytest.raises(S.SvlError) as e:
         V.VisionModel(vc, bad, 48)
     assert e.value.kind == "Corrupt"
+
+
+# ---- the closed forms that pin the oracle, on the GPU ----------------------------------
+
+def test_gpu_tower_meets_the_closed_forms():
+    """Config V at 2 layers on the two degenerate weight sets of the oracle's
+    closed-form pins: with zero projections every GPU layer is the identity
+    (bit for bit) and the soft tokens are the closed form of embedding,
+    pooling, unscaled norm and projection; with identical patches and a zero
+    position table every layer is the one-row closed form."""
+    import test_oracle_vision as TV
+    c = svl_synth.config_v(2)
+    vc = O.resolve_vision_config(c)
+    H = vc["hidden_size"]
+    w = dict(svl_synth.vision_weights(c, 768, seed=21))
+    for l in range(2):
+        for n in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                  "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"):
+            k = TV.L_.format(l) + n + ".linear.weight"
+            w[k] = np.zeros_like(w[k])
+    s = np.float32(3e-3 / np.sqrt(H))
+    w[TV.W_IN] = (w[TV.W_IN] * s).astype(np.float32)
+    w[TV.TABLE] = (w[TV.TABLE] * s).astype(np.float32)
+    gpu = V.VisionModel(V.VisionConfig.from_json_value(c), w, 768)
+    p = svl_synth.image_patches(1, 12, 9, seed=31)[0]
+    out = gpu.forward(p, capture_hidden=True)
+    hs = out.hidden_states()
+    for l in (1, 2):
+        assert np.array_equal(hs[l], hs[0]), f"layer {l} is not the identity"
+    n = p.valid_patches
+    h0 = TV._embedding_closed_form(w, p.pixel_values[:n], p.positions[:n])
+    assert TV._rel(hs[0], h0) <= 1e-5
+    want = TV._soft_closed_form(vc, w, h0, p.positions[:n], p.patch_grid, p.soft_tokens)
+    e = TV._rel(out.pooled(), want)
+    print(f"zero projections: soft tokens relative max error {e:.3g}", flush=True)
+    assert e <= 1e-4
+    gpu.close()
+
+    w = dict(svl_synth.vision_weights(c, 768, seed=22))
+    w[TV.TABLE] = np.zeros_like(w[TV.TABLE])
+    gpu = V.VisionModel(V.VisionConfig.from_json_value(c), w, 768)
+    p = svl_synth.image_patches(1, 12, 12, seed=32)[0]
+    p.pixel_values[:] = p.pixel_values[0]
+    out = gpu.forward(p, capture_hidden=True)
+    hs = out.hidden_states()
+    h = TV._embedding_closed_form(w, p.pixel_values[:1], p.positions[:1])[0]
+    for l in range(2):
+        h = TV._layer_one_row(vc, w, l, h)
+        e = TV._rel(hs[l + 1], np.broadcast_to(h, hs[l + 1].shape))
+        print(f"identical patches: layer {l + 1} relative max error {e:.3g}", flush=True)
+        assert e <= 1e-4
+    gpu.close()

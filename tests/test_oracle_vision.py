@@ -178,3 +178,143 @@ def test_vision_forward_error_taxonomy(small_tower):
     with pytest.raises(oracle.OracleError) as e:
         m.forward(odd)
     assert e.value.status == 7
+
+
+# ---- closed forms of the whole tower (vision.rs:742-959) -----------------------------
+#
+# Two degenerate weight sets reduce the forward pass to formulas that need no
+# attention softmax and no RoPE, so they pin the composition independently of
+# any restatement of the layer loop. Each comparison is shown to fail when a
+# plausible mistake is planted in the closed form.
+
+L_ = "vision_tower.encoder.layers.{}."
+W_IN = "vision_tower.patch_embedder.input_proj.weight"
+TABLE = "vision_tower.patch_embedder.position_embedding_table"
+W_OUT = "embed_vision.embedding_projection.weight"
+
+
+def _config(kind):
+    return small_vision_config(2) if kind == "small" else svl_synth.config_v(2)
+
+
+def _soft_closed_form(vc, w, h, pos, grid, soft, mistake=None):
+    """pool_patches (vision.rs:980-1040: per 3x3 bin, sum / 9 * sqrt(H)),
+    unscaled RMSNorm, embedding projection (vision.rs:937-946), in float64."""
+    gw, _ = grid
+    H = h.shape[1]
+    pooled = np.zeros((soft, H))
+    for i in range(h.shape[0]):
+        pooled[pos[i, 0] // 3 + (gw // 3) * (pos[i, 1] // 3)] += h[i]
+    div = 1.0 if mistake == "pool_no_div9" else 9.0
+    mul = 1.0 if mistake == "pool_no_sqrt_h" else np.sqrt(H)
+    pooled = pooled / div * mul
+    return ref64.rms(pooled, None, vc["rms_norm_eps"]) @ w[W_OUT].astype(np.float64).T
+
+
+def _embedding_closed_form(w, pix, pos, mistake=None):
+    """hidden_0 = 2 (x - 0.5) W_in^T + table[0][x] + table[1][y] (vision.rs:760-809)."""
+    x = pix.astype(np.float64)
+    x = x if mistake == "no_rescale" else 2.0 * (x - 0.5)
+    t = w[TABLE].astype(np.float64)
+    xs, ys = (pos[:, 1], pos[:, 0]) if mistake == "xy_swap" else (pos[:, 0], pos[:, 1])
+    return x @ w[W_IN].astype(np.float64).T + t[0][xs] + t[1][ys]
+
+
+def _rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / np.abs(b).max())
+
+
+@pytest.mark.parametrize("kind", ["small", "config_v"])
+def test_zero_projections_reduce_the_tower_to_its_embedding_and_pooling(kind):
+    """With every q/k/v/o and gate/up/down weight zero, each layer adds
+    RMSNorm(0) = 0 twice, so every hidden state equals the patch embedding bit
+    for bit, and the soft tokens are the closed form of the embedding, the
+    3x3 pooling, the unscaled norm and the projection. The embedding is scaled
+    so the pooled rows' mean square is near eps: the norm then sees the pool's
+    1/9 and sqrt(H) factors too."""
+    c = _config(kind)
+    vc = oracle.resolve_vision_config(c)
+    H, L = vc["hidden_size"], vc["num_hidden_layers"]
+    w = dict(svl_synth.vision_weights(c, 48, seed=21))
+    for l in range(L):
+        for n in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                  "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"):
+            k = L_.format(l) + n + ".linear.weight"
+            w[k] = np.zeros_like(w[k])
+    s = np.float32(3e-3 / np.sqrt(H))
+    w[W_IN] = (w[W_IN] * s).astype(np.float32)
+    w[TABLE] = (w[TABLE] * s).astype(np.float32)
+    p = grid_patches(6, 9, seed=3)
+    out = oracle.OracleVisionModel(c, w, 48).forward(p, capture_hidden=True)
+    hs = out["hidden_states"]
+    for l in range(1, L + 1):
+        assert np.array_equal(hs[l], hs[0]), f"layer {l} is not the identity"
+    h0 = _embedding_closed_form(w, p.pixel_values, p.positions)
+    assert _rel(hs[0], h0) <= 1e-5
+    want = _soft_closed_form(vc, w, h0, p.positions, p.patch_grid, p.soft_tokens)
+    ms = (np.asarray(want) ** 2).mean()
+    assert _rel(out["pooled"], want) <= 1e-4, (ms, _rel(out["pooled"], want))
+    for mistake in ("xy_swap", "no_rescale"):
+        bad = _soft_closed_form(vc, w, _embedding_closed_form(w, p.pixel_values, p.positions,
+                                                              mistake),
+                                p.positions, p.patch_grid, p.soft_tokens)
+        assert _rel(out["pooled"], bad) > 1e-2, mistake
+    for mistake in ("pool_no_div9", "pool_no_sqrt_h"):
+        bad = _soft_closed_form(vc, w, h0, p.positions, p.patch_grid, p.soft_tokens, mistake)
+        assert _rel(out["pooled"], bad) > 1e-2, mistake
+
+
+def _layer_one_row(vc, w, l, h, mistake=None):
+    """One encoder layer (vision.rs:816-935) on a hidden state whose rows are
+    all equal: every key's value row is the same, so attention returns it
+    whatever the softmax weights (sum_j p_j v = v) and RoPE drops out."""
+    NH, NKV, hd, eps = (vc["num_attention_heads"], vc["num_key_value_heads"], vc["head_dim"],
+                        vc["rms_norm_eps"])
+    p = L_.format(l)
+    f64 = lambda n: w[p + n].astype(np.float64)
+    n = ref64.rms(h, w[p + "input_layernorm.weight"], eps)
+    v = (n @ f64("self_attn.v_proj.linear.weight").T).reshape(NKV, hd)
+    v = ref64.rms(v, w[p + "self_attn.k_norm.weight"] if mistake == "scaled_v_norm" else None, eps)
+    attn = np.concatenate([v[hh // (NH // NKV)] for hh in range(NH)])
+    o = attn @ f64("self_attn.o_proj.linear.weight").T
+    h = h + (o if mistake == "no_post_attention_norm" else
+             ref64.rms(o, w[p + "post_attention_layernorm.weight"], eps))
+    n = ref64.rms(h, w[p + "pre_feedforward_layernorm.weight"], eps)
+    g = n @ f64("mlp.gate_proj.linear.weight").T
+    u = n @ f64("mlp.up_proj.linear.weight").T
+    act = ref64.gelu(u) * g if mistake == "gate_up_swapped" else ref64.gelu(g) * u
+    return h + ref64.rms(act @ f64("mlp.down_proj.linear.weight").T,
+                         w[p + "post_feedforward_layernorm.weight"], eps)
+
+
+@pytest.mark.parametrize("kind", ["small", "config_v"])
+def test_identical_patches_reduce_attention_to_the_value_row(kind):
+    """Identical patches and a zero position table make every row of every
+    hidden state equal, so each layer is the closed form of one row: the
+    unscaled V norm, the O projection, the sandwich norms, GeGLU and both
+    residuals (planted: a weighted V norm, a missing post-attention norm,
+    gate and up swapped)."""
+    c = _config(kind)
+    vc = oracle.resolve_vision_config(c)
+    L = vc["num_hidden_layers"]
+    w = dict(svl_synth.vision_weights(c, 48, seed=22))
+    w[TABLE] = np.zeros_like(w[TABLE])
+    p = grid_patches(6, 6, seed=4)
+    p.pixel_values[:] = p.pixel_values[0]
+    out = oracle.OracleVisionModel(c, w, 48).forward(p, capture_hidden=True)
+    hs = out["hidden_states"]
+    h = _embedding_closed_form(w, p.pixel_values[:1], p.positions[:1])[0]
+    assert _rel(hs[0], np.broadcast_to(h, hs[0].shape)) <= 1e-5
+    for l in range(L):
+        prev = h
+        h = _layer_one_row(vc, w, l, prev)
+        e = _rel(hs[l + 1], np.broadcast_to(h, hs[l + 1].shape))
+        assert e <= 1e-4, f"layer {l + 1}: {e}"
+        for mistake in ("scaled_v_norm", "no_post_attention_norm", "gate_up_swapped"):
+            bad = _layer_one_row(vc, w, l, prev, mistake)
+            assert _rel(hs[l + 1], np.broadcast_to(bad, hs[l + 1].shape)) > 1e-3, \
+                (l, mistake)
+    want = _soft_closed_form(vc, w, np.broadcast_to(h, hs[L].shape), p.positions,
+                             p.patch_grid, p.soft_tokens)
+    assert _rel(out["pooled"], want) <= 1e-4
