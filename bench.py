@@ -495,6 +495,7 @@ def main():
 
     torch.cuda.set_device(0)
     dev = svl_amd.Device.get(0)
+    mfma_peak, hbm_peak = dev.measure_peaks()
     cfg = svl_synth.config_a()
     weights = svl_synth.weights(cfg, seed=0)
     lengths = svl_synth.row_lengths(BATCH, LEN_LO, LEN_HI, seed=1)
@@ -641,6 +642,15 @@ def main():
         "kernel_ms_per_step": round(total_kernel_ms, 3),
         "single_stream_ms_per_step": round(single_stream_ms, 3),
         "roofline": roofline,
+        "measured_peaks": {"fp32_mfma_tflops": round(mfma_peak, 2),
+                           "hbm_copy_gbs": round(hbm_peak, 1),
+                           "method": "register-only MFMA chains on every SIMD (16 chains of "
+                                     "16x16x4 f32 in one wave per SIMD, 4 chains of 32x32x2 f32 "
+                                     "in two; the faster); 1 GiB device-to-device copy, one "
+                                     "float4 per thread (read + written bytes); best of a few "
+                                     "launches each",
+                           "published": {"fp32_mfma_tflops": PEAK_FP32_MFMA_TFLOPS,
+                                         "hbm_gbs": PEAK_HBM_GBS}},
         "cpu_baseline": cpu,
         "parity": parity,
         "host_to_host": host,

@@ -155,6 +155,12 @@ svl_status svl_truncate_and_normalize(const float *values, size_t n, size_t dime
  * cap, Unsupported for another dtype. Host only; no device is needed. */
 svl_status svl_tensor_to_f32(const svl_tensor_view *tensor, float *out, int64_t capacity);
 
+/* No counterpart in the reference (a measurement aid): the device's FP32
+ * matrix rate from register-only MFMA chains on every SIMD, and its HBM
+ * bandwidth from a 1 GiB device-to-device copy (read + written bytes per
+ * second); best of a few timed launches each. Takes well under a second. */
+svl_status svl_measure_peaks(svl_ctx *ctx, double *fp32_mfma_tflops, double *hbm_copy_gbs);
+
 /* Batches of 4096 tokens or more run as `groups` groups of rows (1..4,
  * default 3), group 0 on the caller's stream and the others on streams of
  * the model that wait for it and are joined back into it, so one group's

@@ -1102,6 +1102,14 @@ svl_status svl_tensor_to_f32(const svl_tensor_view *t, float *out, int64_t capac
     return widen_f32(*t, numel, out);
 }
 
+svl_status svl_measure_peaks(svl_ctx *ctx, double *fp32_mfma_tflops, double *hbm_copy_gbs) {
+    if (!ctx || !fp32_mfma_tflops || !hbm_copy_gbs) return fail(SVL_USAGE, "null argument");
+    HIP_TRY(hipSetDevice(ctx->device));
+    const hipError_t e = probe_peaks(fp32_mfma_tflops, hbm_copy_gbs);
+    if (e != hipSuccess) return fail(SVL_DEVICE, "peak probe: %s", hipGetErrorString(e));
+    return SVL_OK;
+}
+
 svl_status svl_text_embed_ids(svl_text_model *m, const uint32_t *ids, int64_t n,
                               int64_t dimension, float *out) {
     if (!m || !out) return fail(SVL_USAGE, "model and output are required");

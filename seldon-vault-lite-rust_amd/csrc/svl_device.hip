@@ -8,3 +8,4 @@
 #include "mel.hip"
 #include "search.hip"
 #include "noalloc.hip"
+#include "probe.hip"

@@ -127,6 +127,10 @@ hipError_t noalloc_scratch(int device, void **out);
 hipError_t launch_noalloc_attn_setup(void *base, int seq, int per_head, int bv, int n_tiles,
                                      hipStream_t s);
 
+// Measured FP32 MFMA rate (register-only chains on every SIMD) and HBM copy
+// bandwidth of the current device (probe.hip).
+hipError_t probe_peaks(double *fp32_mfma_tflops, double *hbm_copy_gbs);
+
 // Per row r of [offsets[r], offsets[r+1]): pos[t] = t - offsets[r] and
 // rowlen[t] = offsets[r+1] - offsets[r] (rowlen may be null).
 hipError_t launch_positions(const int64_t *offsets, int batch, int32_t *pos, int32_t *rowlen,

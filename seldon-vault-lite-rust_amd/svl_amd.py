@@ -113,6 +113,7 @@ EXPORTED = [
     "svl_text_embed_texts", "svl_vector_index_create", "svl_vector_index_destroy",
     "svl_vector_index_size", "svl_vector_index_dimension", "svl_vector_rank",
     "svl_vector_rank_device", "svl_tensor_to_f32", "svl_bidirectional_attention_noalloc",
+    "svl_measure_peaks",
 ]
 
 _lib = None
@@ -163,6 +164,8 @@ def lib():
         L.svl_text_embed_ids.argtypes = [vp, vp, i64, i64, vp]
         L.svl_truncate_and_normalize.argtypes = [vp, ctypes.c_size_t, ctypes.c_size_t, vp]
         L.svl_tensor_to_f32.argtypes = [ctypes.POINTER(_TensorView), vp, i64]
+        L.svl_measure_peaks.argtypes = [vp, ctypes.POINTER(ctypes.c_double),
+                                        ctypes.POINTER(ctypes.c_double)]
         L.svl_text_model_set_kernel_timing.argtypes = [vp, ctypes.c_int]
         L.svl_text_model_set_stream_split.argtypes = [vp, ctypes.c_int]
         L.svl_text_model_kernel_stats.argtypes = [vp, vp, vp, vp]
@@ -505,6 +508,12 @@ class Device:
         if ordinal not in cls._cache:
             cls._cache[ordinal] = cls(ordinal)
         return cls._cache[ordinal]
+
+    def measure_peaks(self):
+        """(FP32 MFMA TFLOP/s, HBM copy GB/s) measured on this device."""
+        t, b = ctypes.c_double(), ctypes.c_double()
+        _check(lib().svl_measure_peaks(self.handle, ctypes.byref(t), ctypes.byref(b)))
+        return t.value, b.value
 
 
 def tensor_views(weights: dict):
