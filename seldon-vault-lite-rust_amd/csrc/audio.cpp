@@ -229,10 +229,39 @@ std::vector<float> position_table(int64_t hidden, int64_t positions) {
     return out;
 }
 
+// A clipped linear (audio.rs:558-601). Its A operand is written already
+// clamped to b's input bounds by the kernel that produces it (in_clamp).
 GemmArgs clipped(const float *A, int64_t lda, const float *W, int64_t ldw, float *C, int64_t ldc,
                  int64_t M, int64_t N, int64_t K, int epi, const Bounds &b) {
     GemmArgs g{A, lda, W, ldw, C, ldc, (int)M, (int)N, (int)K, epi, 1.f, nullptr, 0, 0};
     for (int k = 0; k < 4; ++k) g.clip[0][k] = b.v[k];
+    return g;
+}
+
+// Store clamp that makes a row kernel's output the A operand of the clipped
+// linears with input bounds b[0 .. n-1] (one copy each, `stride` floats apart).
+OutClamp in_clamp(const Bounds *const *b, int n, int64_t stride) {
+    OutClamp oc;
+    oc.copies = n;
+    oc.stride = stride;
+    for (int k = 0; k < n; ++k) {
+        oc.lo[k] = b[k]->v[0];
+        oc.hi[k] = b[k]->v[1];
+    }
+    return oc;
+}
+
+OutClamp in_clamp(const Bounds &b) {
+    const Bounds *p = &b;
+    return in_clamp(&p, 1, 0);
+}
+
+// The FFN up projection's SiLU output is the down projection's A operand.
+GemmArgs ffn_up(const float *A, int64_t lda, const float *W, float *C, int64_t M, int64_t N,
+                int64_t K, const Bounds &up, const Bounds &down) {
+    GemmArgs g = clipped(A, lda, W, K, C, N, M, N, K, EPI_CLIP_SILU, up);
+    g.post_lo = down.v[0];
+    g.post_hi = down.v[1];
     return g;
 }
 
@@ -313,7 +342,7 @@ svl_status ensure_au_workspace(svl_audio_model *m, const AuBatch &b) {
     HIP_TRY(m->col.ensure(T * FREQ1 * 9 * m->C0));
     HIP_TRY(m->l1.ensure(T * FREQ1 * m->C1));
     HIP_TRY(m->h.ensure(T * m->H));
-    HIP_TRY(m->n.ensure(T * m->H));
+    HIP_TRY(m->n.ensure(3 * T * m->H));  // three clamped copies feed the Q/K/V projection
     HIP_TRY(m->tmp.ensure(T * m->H));
     HIP_TRY(m->act.ensure(T * m->I));
     HIP_TRY(m->qkv.ensure(T * 3 * m->H));
@@ -393,31 +422,36 @@ svl_status enqueue_audio(svl_audio_model *m, const AuBatch &b, const float *d_me
         HIP_TRY(hipMemcpyAsync(h_sscp, m->h.p, (size_t)(T * H) * 4, hipMemcpyDeviceToHost, s));
     if (m->L > 0)  // feed_forward1's input clamp + pre norm of layer 0
         HIP_TRY(launch_audio_rows(m->h.p, m->clip, m->layers[0].ff_pre[0], nullptr, 1.f, m->n.p,
-                                  inf, nullptr, nullptr, T, W, m->eps, flag, s));
+                                  inf, nullptr, nullptr, T, W, m->eps, flag, s,
+                                  in_clamp(m->layers[0].ff_b1[0])));
     for (int64_t l = 0; l < m->L; ++l) {
         const AuLayer &ly = m->layers[(size_t)l];
         // feed_forward1 (audio.rs:1374-1433): n holds rms(clamp(h), pre).
-        HIP_TRY(launch_gemm(clipped(m->n.p, H, ly.ff_w1[0], H, m->act.p, I, T, I, H, EPI_CLIP_SILU,
-                                    ly.ff_b1[0]), s));
+        HIP_TRY(launch_gemm(ffn_up(m->n.p, H, ly.ff_w1[0], m->act.p, T, I, H, ly.ff_b1[0],
+                                   ly.ff_b2[0]), s));
         HIP_TRY(launch_gemm(clipped(m->act.p, I, ly.ff_w2[0], I, m->tmp.p, H, T, H, I,
                                     EPI_CLIP_STORE, ly.ff_b2[0]), s));
-        // h += rms(clamp(ff), post) * rw; n = rms(h, norm_pre_attn)
+        // h += rms(clamp(ff), post) * rw; n = rms(h, norm_pre_attn), one copy
+        // per projection of Q, K and V, each clamped to its input bounds
+        const Bounds *bs[3] = {&ly.bq, &ly.bk, &ly.bv};
         HIP_TRY(launch_audio_rows(m->tmp.p, m->clip, ly.ff_post[0], m->h.p, m->rw, m->h.p, inf,
-                                  ly.norm_pre_attn, m->n.p, T, W, m->eps, flag, s));
+                                  ly.norm_pre_attn, m->n.p, T, W, m->eps, flag, s,
+                                  in_clamp(bs, 3, T * H)));
         // chunked attention (audio.rs:1529-1669)
         if (H % 128 == 0) {
             GemmArgs g = clipped(m->n.p, H, ly.w_qkv, H, m->qkv.p, 3 * H, T, 3 * H, H,
                                  EPI_CLIP_STORE, ly.bq);
             g.clip_cols = (int)H;
+            g.a_seg = T * H;
             for (int k = 0; k < 4; ++k) {
                 g.clip[1][k] = ly.bk.v[k];
                 g.clip[2][k] = ly.bv.v[k];
             }
             HIP_TRY(launch_gemm(g, s));
         } else {
-            const Bounds *bs[3] = {&ly.bq, &ly.bk, &ly.bv};
             for (int j = 0; j < 3; ++j)
-                HIP_TRY(launch_gemm(clipped(m->n.p, H, ly.w_qkv + (int64_t)j * H * H, H,
+                HIP_TRY(launch_gemm(clipped(m->n.p + (int64_t)j * T * H, H,
+                                            ly.w_qkv + (int64_t)j * H * H, H,
                                             m->qkv.p + (int64_t)j * H, 3 * H, T, H, H,
                                             EPI_CLIP_STORE, *bs[j]), s));
         }
@@ -445,13 +479,15 @@ svl_status enqueue_audio(svl_audio_model *m, const AuBatch &b, const float *d_me
             a.context = (int)m->context;
             a.positions = (int)m->positions;
             a.flag = flag;
+            a.out_lo = ly.bpost.v[0];
+            a.out_hi = ly.bpost.v[1];
             HIP_TRY(launch_audio_attention(a, s));
         }
         HIP_TRY(launch_gemm(clipped(m->att.p, H, ly.w_post, H, m->tmp.p, H, T, H, H, EPI_CLIP_STORE,
                                     ly.bpost), s));
         // h += rms(post, norm_post_attn); n = rms(h, lconv pre)
         HIP_TRY(launch_audio_rows(m->tmp.p, inf, ly.norm_post_attn, m->h.p, 1.f, m->h.p, inf,
-                                  ly.lc_pre, m->n.p, T, W, m->eps, flag, s));
+                                  ly.lc_pre, m->n.p, T, W, m->eps, flag, s, in_clamp(ly.bstart)));
         // light conv (audio.rs:1448-1527)
         {
             GemmArgs g = clipped(m->n.p, H, ly.w_start, H, m->gated.p, H, T, 2 * m->H_pad, H,
@@ -460,15 +496,15 @@ svl_status enqueue_audio(svl_audio_model *m, const AuBatch &b, const float *d_me
             HIP_TRY(launch_gemm(g, s));
         }
         HIP_TRY(launch_lconv(m->gated.p, ly.dw, (int)m->K, m->pos.p, m->clip, ly.lc_norm, m->n.p,
-                             T, W, m->eps, flag, s));
+                             T, W, m->eps, flag, s, ly.bend.v[0], ly.bend.v[1]));
         HIP_TRY(launch_gemm(clipped(m->n.p, H, ly.w_end, H, m->tmp.p, H, T, H, H, EPI_CLIP_STORE,
                                     ly.bend), s));
         // h += end; n = rms(clamp(h), feed_forward2 pre)
         HIP_TRY(launch_audio_rows(m->tmp.p, inf, nullptr, m->h.p, 1.f, m->h.p, m->clip,
-                                  ly.ff_pre[1], m->n.p, T, W, m->eps, flag, s));
+                                  ly.ff_pre[1], m->n.p, T, W, m->eps, flag, s, in_clamp(ly.ff_b1[1])));
         // feed_forward2
-        HIP_TRY(launch_gemm(clipped(m->n.p, H, ly.ff_w1[1], H, m->act.p, I, T, I, H, EPI_CLIP_SILU,
-                                    ly.ff_b1[1]), s));
+        HIP_TRY(launch_gemm(ffn_up(m->n.p, H, ly.ff_w1[1], m->act.p, T, I, H, ly.ff_b1[1],
+                                   ly.ff_b2[1]), s));
         HIP_TRY(launch_gemm(clipped(m->act.p, I, ly.ff_w2[1], I, m->tmp.p, H, T, H, I,
                                     EPI_CLIP_STORE, ly.ff_b2[1]), s));
         // h = rms(h + rms(clamp(ff), post) * rw, norm_out)
@@ -479,7 +515,8 @@ svl_status enqueue_audio(svl_audio_model *m, const AuBatch &b, const float *d_me
                                    hipMemcpyDeviceToHost, s));
         if (l + 1 < m->L)
             HIP_TRY(launch_audio_rows(m->h.p, m->clip, m->layers[(size_t)l + 1].ff_pre[0], nullptr,
-                                      1.f, m->n.p, inf, nullptr, nullptr, T, W, m->eps, flag, s));
+                                      1.f, m->n.p, inf, nullptr, nullptr, T, W, m->eps, flag, s,
+                                      in_clamp(m->layers[(size_t)l + 1].ff_b1[0])));
     }
     // Output projection + bias, unscaled RMSNorm of the valid rows, text
     // projection (audio.rs:1085-1133).

@@ -227,7 +227,7 @@ template <int NC>
 __global__ __launch_bounds__(256) void audio_rows_kernel(
     const float *x, float c1, const float *__restrict__ w1, const float *res, float rw,
     float *h_out, float c2, const float *__restrict__ w2, float *n_out, int64_t rows, int width,
-    float eps, int *flag) {
+    float eps, int *flag, OutClamp oc) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
@@ -264,7 +264,15 @@ __global__ __launch_bounds__(256) void audio_rows_kernel(
         if (i < nv) {
             if (res) v[c] = ((const f32x4 *)(res + row * width))[i] + v[c] * rw;
             ok = ok && finite4(v[c]);
-            if (h_out) ((f32x4 *)(h_out + row * width))[i] = v[c];
+            if (h_out) {
+                if (w2) {
+                    ((f32x4 *)(h_out + row * width))[i] = v[c];
+                } else {
+                    for (int k = 0; k < oc.copies; ++k)
+                        ((f32x4 *)(h_out + k * oc.stride + row * width))[i] =
+                            clamp4(v[c], oc.lo[k], oc.hi[k]);
+                }
+            }
             if (w2) {
                 const f32x4 y = clamp4(v[c], -c2, c2);
                 v[c] = y;
@@ -282,7 +290,8 @@ __global__ __launch_bounds__(256) void audio_rows_kernel(
             if (i < nv) {
                 const f32x4 y = v[c] * inv * ((const f32x4 *)w2)[i];
                 ok = ok && finite4(y);
-                ((f32x4 *)(n_out + row * width))[i] = y;
+                for (int k = 0; k < oc.copies; ++k)
+                    ((f32x4 *)(n_out + k * oc.stride + row * width))[i] = clamp4(y, oc.lo[k], oc.hi[k]);
             }
         }
     }
@@ -291,13 +300,13 @@ __global__ __launch_bounds__(256) void audio_rows_kernel(
 
 hipError_t launch_audio_rows(const float *x, float c1, const float *w1, const float *res, float rw,
                              float *h_out, float c2, const float *w2, float *n_out, int64_t rows,
-                             int width, float eps, int *flag, hipStream_t s) {
+                             int width, float eps, int *flag, hipStream_t s, const OutClamp &oc) {
     if (rows <= 0) return hipSuccess;
-    if (width % 4 || width > 2048) return hipErrorInvalidValue;
+    if (width % 4 || width > 2048 || oc.copies < 1 || oc.copies > 3) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((rows + 3) / 4));
 #define AR_LAUNCH(NC)                                                                          \
     hipLaunchKernelGGL(audio_rows_kernel<NC>, grid, dim3(256), 0, s, x, c1, w1, res, rw, h_out, \
-                       c2, w2, n_out, rows, width, eps, flag)
+                       c2, w2, n_out, rows, width, eps, flag, oc)
     switch ((width + 255) / 256) {
         case 1: AR_LAUNCH(1); break;
         case 2: AR_LAUNCH(2); break;
@@ -534,7 +543,7 @@ __global__ __launch_bounds__(64 * AW) void audio_attn_kernel(AudioAttnArgs p) {
                     if (d < hd) {
                         const float y = on ? acc[q][t] : 0.0f;
                         ok = ok && isfinite(y);
-                        orow[d] = y;
+                        orow[d] = clamp_ref(y, p.out_lo, p.out_hi);
                     }
                 }
             }
@@ -600,7 +609,8 @@ __global__ __launch_bounds__(256) void lconv_kernel(const float *__restrict__ ga
                                                     const float *__restrict__ dw, int K,
                                                     const int32_t *__restrict__ pos, float clip,
                                                     const float *__restrict__ w, float *__restrict__ out,
-                                                    int64_t rows, int width, float eps, int *flag) {
+                                                    int64_t rows, int width, float eps, int *flag,
+                                                    float out_lo, float out_hi) {
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
@@ -640,7 +650,7 @@ __global__ __launch_bounds__(256) void lconv_kernel(const float *__restrict__ ga
             y.z = silu_ref(y.z);
             y.w = silu_ref(y.w);
             ok = ok && finite4(y);
-            ((f32x4 *)(out + row * width))[i] = y;
+            ((f32x4 *)(out + row * width))[i] = clamp4(y, out_lo, out_hi);
         }
     }
     if (!ok) raise_flag(flag, FLAG_NONFINITE);
@@ -648,13 +658,13 @@ __global__ __launch_bounds__(256) void lconv_kernel(const float *__restrict__ ga
 
 hipError_t launch_lconv(const float *gated, const float *dw, int K, const int32_t *pos, float clip,
                         const float *w, float *out, int64_t rows, int width, float eps, int *flag,
-                        hipStream_t s) {
+                        hipStream_t s, float out_lo, float out_hi) {
     if (rows <= 0) return hipSuccess;
     if (width % 4 || width > 2048) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((rows + 3) / 4));
 #define LC_LAUNCH(NC)                                                                           \
     hipLaunchKernelGGL(lconv_kernel<NC>, grid, dim3(256), 0, s, gated, dw, K, pos, clip, w, out, \
-                       rows, width, eps, flag)
+                       rows, width, eps, flag, out_lo, out_hi)
     switch ((width + 255) / 256) {
         case 1: LC_LAUNCH(1); break;
         case 2: LC_LAUNCH(2); break;

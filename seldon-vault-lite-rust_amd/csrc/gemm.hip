@@ -138,7 +138,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x4 (&a
                         x = gelu_tanh(x) * (n < p.N ? p.aux[(int64_t)m * p.ldaux + n] : 0.f);
                     if constexpr (EPI == EPI_BIAS) x = x + (n < p.N ? p.aux[n] : 0.f);
                     if constexpr (EPI == EPI_CLIP_STORE) x = clamp_ref(x, olo, ohi);
-                    if constexpr (EPI == EPI_CLIP_SILU) x = silu_ref(clamp_ref(x, olo, ohi));
+                    if constexpr (EPI == EPI_CLIP_SILU)
+                        x = clamp_ref(silu_ref(clamp_ref(x, olo, ohi)), p.post_lo, p.post_hi);
                     v[r] = x;
                 }
                 store_cols4(crow, n0, p.N, vec, v);
@@ -167,11 +168,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
     const int l16 = lane & 15, g = lane >> 4;
     const int M = p.M, N = p.N, K = p.K;
     const int seg = clip_segment(p, n0);
-    float alo = 0.f, ahi = 0.f;
-    if constexpr (clipped_epi<EPI>()) {
-        alo = p.clip[seg][0];
-        ahi = p.clip[seg][1];
-    }
+    const float *A = p.A + (int64_t)seg * p.a_seg;
 
     f32x4 acc[S::TM][S::TN];
 #pragma unroll
@@ -186,7 +183,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
             const int f = tid + 256 * i, row = f >> 3, gk = k0 + ((f & 7) << 2);
             const int gm = m0 + row;
             f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (gm < M && gk < K) v = *(const f32x4 *)(p.A + (int64_t)gm * p.lda + gk);
+            if (gm < M && gk < K) v = *(const f32x4 *)(A + (int64_t)gm * p.lda + gk);
             ra[i] = v;
         }
 #pragma unroll
@@ -224,10 +221,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
         for (int kk = 0; kk < S::BK; kk += 16) {
             f32x4 a[S::TM], b[S::TN];
 #pragma unroll
-            for (int i = 0; i < S::TM; ++i) {
-                a[i] = *(const f32x4 *)(as + i * 16 * S::LDS + kk);
-                if constexpr (clipped_epi<EPI>()) a[i] = clamp4(a[i], alo, ahi);
-            }
+            for (int i = 0; i < S::TM; ++i) a[i] = *(const f32x4 *)(as + i * 16 * S::LDS + kk);
 #pragma unroll
             for (int j = 0; j < S::TN; ++j) b[j] = *(const f32x4 *)(ws + j * 16 * S::LDS + kk);
 #pragma unroll
@@ -310,17 +304,12 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     const int l16 = lane & 15, g = lane >> 4;
     const int M = p.M, N = p.N;
     const int seg = clip_segment(p, n0);
-    float alo = 0.f, ahi = 0.f;
-    if constexpr (clipped_epi<EPI>()) {
-        alo = p.clip[seg][0];
-        ahi = p.clip[seg][1];
-    }
 
     // Operand windows: [valid rows of this tile] x lda floats; reads past
     // the last valid row return zero.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.A + (int64_t)m0 * p.lda), (short)0, (int)(min(BM, M - m0) * p.lda * 4),
-        0x00020000);
+        (void *)(p.A + (int64_t)seg * p.a_seg + (int64_t)m0 * p.lda), (short)0,
+        (int)(min(BM, M - m0) * p.lda * 4), 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.W + (int64_t)n0 * p.ldw), (short)0, (int)(min(BN, N - n0) * p.ldw * 4),
         0x00020000);
@@ -387,10 +376,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
             const int pos = ((kk >> 2) + g) ^ sw;
             f32x4 a[TM], b[TN];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                a[i] = *(const f32x4 *)(as + i * 16 * BK + 4 * pos);
-                if constexpr (clipped_epi<EPI>()) a[i] = clamp4(a[i], alo, ahi);
-            }
+            for (int i = 0; i < TM; ++i) a[i] = *(const f32x4 *)(as + i * 16 * BK + 4 * pos);
 #pragma unroll
             for (int j = 0; j < TN; ++j) b[j] = *(const f32x4 *)(ws + j * 16 * BK + 4 * pos);
 #pragma unroll
@@ -421,11 +407,11 @@ __global__ __launch_bounds__(256) void gemm_nt_simple(GemmArgs p) {
     const int ncols = paired_epi<EPI>() ? p.n_out : p.N;
     if (idx >= (int64_t)p.M * ncols) return;
     const int m = (int)(idx / ncols), n = (int)(idx % ncols);
-    const float *a = p.A + (int64_t)m * p.lda;
+    const int seg = clipped_epi<EPI>() && p.clip_cols > 0 ? (paired_epi<EPI>() ? 0 : n / p.clip_cols) : 0;
+    const float *a = p.A + (int64_t)seg * p.a_seg + (int64_t)m * p.lda;
     float *crow = p.C + (int64_t)m * p.ldc;
     float alo = 0.f, ahi = 0.f, olo = 0.f, ohi = 0.f;
     if constexpr (clipped_epi<EPI>()) {
-        const int seg = p.clip_cols > 0 ? (paired_epi<EPI>() ? 0 : n / p.clip_cols) : 0;
         alo = p.clip[seg][0];
         ahi = p.clip[seg][1];
         olo = p.clip[seg][2];
@@ -458,7 +444,8 @@ __global__ __launch_bounds__(256) void gemm_nt_simple(GemmArgs p) {
         if constexpr (EPI == EPI_GELU_MUL) s = gelu_tanh(s) * p.aux[(int64_t)m * p.ldaux + n];
         if constexpr (EPI == EPI_BIAS) s = s + p.aux[n];
         if constexpr (EPI == EPI_CLIP_STORE) s = clamp_ref(s, olo, ohi);
-        if constexpr (EPI == EPI_CLIP_SILU) s = silu_ref(clamp_ref(s, olo, ohi));
+        if constexpr (EPI == EPI_CLIP_SILU)
+            s = clamp_ref(silu_ref(clamp_ref(s, olo, ohi)), p.post_lo, p.post_hi);
         crow[n] = s;
     }
 }

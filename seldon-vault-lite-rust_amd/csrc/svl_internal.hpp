@@ -22,11 +22,15 @@ enum GemmEpi : int {
     EPI_GEGLU = 2,     // W rows interleaved in 32-blocks (gate, up); C[m,j] = gelu(g) * u
     EPI_GELU_MUL = 3,  // C[m,n] = gelu(acc) * aux[m * ldaux + n]
     EPI_BIAS = 4,      // C[m,n] = acc + aux[n]
-    // Clipped linears (audio tower): A elements are clamped to
-    // [clip[s][0], clip[s][1]] before the product and the sum to
+    // Clipped linears (audio tower): the sum is clamped to
     // [clip[s][2], clip[s][3]], s = n / clip_cols (0 when clip_cols == 0).
+    // The A operand must already hold values clamped to the segment's input
+    // bounds [clip[s][0], clip[s][1]]: the kernel that writes A applies that
+    // clamp as it stores (the same operation on the same value, so the
+    // product is unchanged), instead of every tile clamping every fragment
+    // it reads. Segment s reads A + s * a_seg.
     EPI_CLIP_STORE = 5,  // C[m,n] = clamp(acc)
-    EPI_CLIP_SILU = 6,   // C[m,n] = silu(clamp(acc))
+    EPI_CLIP_SILU = 6,   // C[m,n] = clamp(silu(clamp(acc)), post_lo, post_hi)
     EPI_CLIP_GLU = 7,    // W rows interleaved in 32-blocks (x, y); C[m,j] = clamp(x) * sigmoid(clamp(y))
 };
 
@@ -46,6 +50,10 @@ struct GemmArgs {
     int cus = 0;               // > 0: the launch shares the GPU with other streams
     int clip_cols = 0;         // output columns per clip segment (0: one segment)
     float clip[4][4] = {};     // per segment: input min, input max, output min, output max
+    int64_t a_seg = 0;         // floats from one clip segment's A operand to the next's
+    // EPI_CLIP_SILU: bounds of the next clipped linear's input, applied as
+    // the result is stored (the identity by default)
+    float post_lo = -__builtin_huge_valf(), post_hi = __builtin_huge_valf();
 };
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
@@ -195,11 +203,22 @@ hipError_t launch_sscp_im2col(const float *l0, const uint8_t *mask0, const SscpR
 // In place: x[p] = relu(layernorm(x[p], ln)) over C channels, n positions.
 hipError_t launch_sscp_ln_relu(float *x, const float *ln, int C, int64_t n, float eps, int *flag,
                                hipStream_t s);
+// Clamped stores of a row kernel's last output (the A operand of a clipped
+// linear): copy c goes to out + c * stride clamped to [lo[c], hi[c]]. The
+// default is one unclamped copy.
+struct OutClamp {
+    int copies = 1;
+    int64_t stride = 0;
+    float lo[3] = {-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf()};
+    float hi[3] = {__builtin_huge_valf(), __builtin_huge_valf(), __builtin_huge_valf()};
+};
 // t = w1 ? rms(clamp(x, +-c1), w1) : x; h = res ? res + t * rw : t (-> h_out);
-// if w2: n_out = rms(clamp(h, +-c2), w2).
+// if w2: n_out = rms(clamp(h, +-c2), w2). `oc` applies to the last output
+// written: n_out when w2 is given, else h_out.
 hipError_t launch_audio_rows(const float *x, float c1, const float *w1, const float *res, float rw,
                              float *h_out, float c2, const float *w2, float *n_out, int64_t rows,
-                             int width, float eps, int *flag, hipStream_t s);
+                             int width, float eps, int *flag, hipStream_t s,
+                             const OutClamp &oc = OutClamp());
 
 struct AudioAttnArgs {
     const float *q, *k, *v;      // head h of row i at q + i * ldq + h * head_dim
@@ -215,12 +234,16 @@ struct AudioAttnArgs {
     int64_t n_blocks;
     int heads, head_dim, chunk, left, context, positions;
     int *flag;
+    // the output projection's input bounds, applied as the output is stored
+    float out_lo = -__builtin_huge_valf(), out_hi = __builtin_huge_valf();
 };
 hipError_t launch_audio_attention(const AudioAttnArgs &a, hipStream_t s);
-// Causal depthwise conv (dw tap-major, [K, width]) within each clip, clamp, RMSNorm(w), SiLU.
+// Causal depthwise conv (dw tap-major, [K, width]) within each clip, clamp, RMSNorm(w), SiLU,
+// stored clamped to [out_lo, out_hi] (the next linear's input bounds).
 hipError_t launch_lconv(const float *gated, const float *dw, int K, const int32_t *pos, float clip,
                         const float *w, float *out, int64_t rows, int width, float eps, int *flag,
-                        hipStream_t s);
+                        hipStream_t s, float out_lo = -__builtin_huge_valf(),
+                        float out_hi = __builtin_huge_valf());
 // out[j] = unscaled_rms(x[idx[j]]).
 hipError_t launch_compact_rms(const float *x, const int32_t *idx, float *out, int64_t rows,
                               int width, float eps, int *flag, hipStream_t s);
