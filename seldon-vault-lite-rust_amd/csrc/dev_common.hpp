@@ -13,6 +13,21 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int WAVE = 64;
 
+// Values that are the same in every lane (derived from blockIdx and kernel
+// arguments) but that the compiler computed in vector registers, moved to
+// scalar registers. A buffer resource built from vector registers makes the
+// compiler wrap every buffer load in a loop over the distinct values of the
+// wave; these keep the resources scalar.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+template <typename T>
+__device__ __forceinline__ T *uniform(T *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return (T *)(((uint64_t)hi << 32) | lo);
+}
+
 
 // Reductions over aligned groups of W lanes (W = 4, 16, 32 or 64) on VALU
 // lane permutes, with no LDS round trip: DPP within a row of 16 lanes

@@ -297,22 +297,22 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     const int xcd = bid & 7, local = bid >> 3;
     const int q8 = ntiles >> 3, r8 = ntiles & 7;
     const int tile = xcd * q8 + min(xcd, r8) + local;
-    const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
+    const int tm = uniform(tile / tiles_n), tn = tile - tm * tiles_n;
     const int m0 = tm * BM, n0 = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WNW, wn = wave % WNW;
     const int l16 = lane & 15, g = lane >> 4;
     const int M = p.M, N = p.N;
-    const int seg = clip_segment(p, n0);
+    const int seg = uniform(clip_segment(p, n0));
 
     // Operand windows: [valid rows of this tile] x lda floats; reads past
     // the last valid row return zero.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.A + (int64_t)seg * p.a_seg + (int64_t)m0 * p.lda), (short)0,
-        (int)(min(BM, M - m0) * p.lda * 4), 0x00020000);
+        (void *)uniform(p.A + (int64_t)seg * p.a_seg + (int64_t)m0 * p.lda), (short)0,
+        uniform((int)(min(BM, M - m0) * p.lda * 4)), 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.W + (int64_t)n0 * p.ldw), (short)0, (int)(min(BN, N - n0) * p.ldw * 4),
-        0x00020000);
+        (void *)uniform(p.W + (int64_t)n0 * p.ldw), (short)0,
+        uniform((int)(min(BN, N - n0) * p.ldw * 4)), 0x00020000);
     int a_off[A_CH], w_off[W_CH];
 #pragma unroll
     for (int q = 0; q < A_CH; ++q) {
