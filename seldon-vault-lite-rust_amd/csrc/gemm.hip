@@ -78,9 +78,10 @@ __device__ __forceinline__ int clip_segment(const GemmArgs &p, int n0) {
 // Epilogue shared by the GEMM kernels. The MFMAs take the W fragment as
 // their first operand, so a 16x16 accumulator tile is C transposed: lane l
 // holds row l % 16 of the tile and its four consecutive columns
-// 4 (l / 16) .. + 3, stored as one float4. Paired epilogues take the
-// 64-column groups of W (32 first-operand rows, then 32 second-operand rows):
-// tiles j and j + 2 of each group of four.
+// 4 (l / 16) .. + 3, stored as one float4 (pairs of adjacent tiles are
+// stored through store_pair). Paired epilogues take the 64-column groups of
+// W (32 first-operand rows, then 32 second-operand rows): tiles j and j + 2
+// of each group of four.
 __device__ __forceinline__ void store_cols4(float *crow, int n0, int limit, bool vec,
                                             const f32x4 &v) {
     if (vec && n0 + 3 < limit) {
@@ -90,6 +91,46 @@ __device__ __forceinline__ void store_cols4(float *crow, int n0, int limit, bool
         for (int r = 0; r < 4; ++r)
             if (n0 + r < limit) crow[n0 + r] = v[r];
     }
+}
+
+// Value lane l16 ^ 8 of the same 16-lane row holds (DPP row_ror:8).
+__device__ __forceinline__ f32x4 row_swap8(f32x4 v) {
+    f32x4 r;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        r[c] = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[c]), 0x128, 0xF, 0xF, false));
+    return r;
+}
+
+// Epilogue value of accumulator element r of 16x16 block (i, j) at row m,
+// column n (unpaired epilogues).
+template <int EPI>
+__device__ __forceinline__ float epi_value(const GemmArgs &p, float x, int m, int n, float olo,
+                                           float ohi) {
+    if constexpr (EPI == EPI_SCALE) x = x * p.alpha;
+    if constexpr (EPI == EPI_GELU_MUL)
+        x = gelu_tanh(x) * (m < p.M && n < p.N ? p.aux[(int64_t)m * p.ldaux + n] : 0.f);
+    if constexpr (EPI == EPI_BIAS) x = x + (n < p.N ? p.aux[n] : 0.f);
+    if constexpr (EPI == EPI_CLIP_STORE) x = clamp_ref(x, olo, ohi);
+    if constexpr (EPI == EPI_CLIP_SILU)
+        x = clamp_ref(silu_ref(clamp_ref(x, olo, ohi)), p.post_lo, p.post_hi);
+    return x;
+}
+
+// Stores a pair of horizontally adjacent 16x16 output blocks, X (columns
+// cx .. cx + 15) and Y (cx + 16 .. cx + 31), rows r0 .. r0 + 15: lane l holds
+// row r0 + l % 16, columns + 4 (l / 16) .. + 3 of each. Lanes with l % 16 < 8
+// trade their Y values for the X values of lane l ^ 8, so each of the two
+// stores writes 8 rows x 128 contiguous bytes (rows r0 .. r0 + 7, then
+// r0 + 8 .. r0 + 15) instead of 16 rows x 64 bytes, and every 128-byte line
+// of the output is written whole by one instruction.
+__device__ __forceinline__ void store_pair(const GemmArgs &p, int limit, bool vec, int r0, int cx,
+                                           int l16, int g, const f32x4 &X, const f32x4 &Y) {
+    const bool lo = l16 < 8;
+    const f32x4 t = row_swap8(lo ? Y : X);
+    const int ra = r0 + (l16 & 7), col = (lo ? cx : cx + 16) + 4 * g;
+    if (ra < p.M) store_cols4(p.C + (int64_t)ra * p.ldc, col, limit, vec, lo ? X : t);
+    if (ra + 8 < p.M) store_cols4(p.C + (int64_t)(ra + 8) * p.ldc, col, limit, vec, lo ? t : Y);
 }
 
 template <int TM, int TN, int EPI>
@@ -104,44 +145,44 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x4 (&a
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const int m = mw + i * 16 + l16;
-        if (m >= p.M) continue;
-        float *crow = p.C + (int64_t)m * p.ldc;
         if constexpr (paired_epi<EPI>()) {
 #pragma unroll
             for (int j = 0; j < TN; j += 4) {
+                f32x4 v[2];
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const int oc = (nw + j * 16) / 2 + 16 * u + 4 * g;
-                    f32x4 v;
+                for (int u = 0; u < 2; ++u)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float x = acc[i][j + u][r], y = acc[i][j + 2 + u][r];
                         if constexpr (EPI == EPI_GEGLU)
-                            v[r] = gelu_tanh(x) * y;
+                            v[u][r] = gelu_tanh(x) * y;
                         else
-                            v[r] = clamp_ref(x, olo, ohi) * sigmoid_ref(clamp_ref(y, olo, ohi));
+                            v[u][r] = clamp_ref(x, olo, ohi) * sigmoid_ref(clamp_ref(y, olo, ohi));
                     }
-                    store_cols4(crow, oc, p.n_out, vec, v);
+                store_pair(p, p.n_out, vec, mw + i * 16, (nw + j * 16) / 2, l16, g, v[0], v[1]);
+            }
+        } else if constexpr (TN % 2 == 0) {
+#pragma unroll
+            for (int j = 0; j < TN; j += 2) {
+                f32x4 v[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int n0 = nw + (j + u) * 16 + 4 * g;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        v[u][r] = epi_value<EPI>(p, acc[i][j + u][r], m, n0 + r, olo, ohi);
                 }
+                store_pair(p, p.N, vec, mw + i * 16, nw + j * 16, l16, g, v[0], v[1]);
             }
         } else {
+            if (m >= p.M) continue;
+            float *crow = p.C + (int64_t)m * p.ldc;
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int n0 = nw + j * 16 + 4 * g;
                 f32x4 v;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int n = n0 + r;
-                    float x = acc[i][j][r];
-                    if constexpr (EPI == EPI_SCALE) x = x * p.alpha;
-                    if constexpr (EPI == EPI_GELU_MUL)
-                        x = gelu_tanh(x) * (n < p.N ? p.aux[(int64_t)m * p.ldaux + n] : 0.f);
-                    if constexpr (EPI == EPI_BIAS) x = x + (n < p.N ? p.aux[n] : 0.f);
-                    if constexpr (EPI == EPI_CLIP_STORE) x = clamp_ref(x, olo, ohi);
-                    if constexpr (EPI == EPI_CLIP_SILU)
-                        x = clamp_ref(silu_ref(clamp_ref(x, olo, ohi)), p.post_lo, p.post_hi);
-                    v[r] = x;
-                }
+                for (int r = 0; r < 4; ++r) v[r] = epi_value<EPI>(p, acc[i][j][r], m, n0 + r, olo, ohi);
                 store_cols4(crow, n0, p.N, vec, v);
             }
         }
