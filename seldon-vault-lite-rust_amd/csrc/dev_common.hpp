@@ -91,15 +91,19 @@ __device__ __forceinline__ f32x4 clamp4(f32x4 v, float lo, float hi) {
     return v;
 }
 
-// audio.rs:1349-1364 silu_value / sigmoid_value, same branches.
+// audio.rs:1349-1364 silu_value / sigmoid_value. Both branches take the
+// exponential of -|v| (exp(-v) for v >= 0, exp(v) otherwise), so it is
+// computed once: v >= 0 gives v / (1 + e) and 1 / (1 + e), v < 0 gives
+// v * e / (1 + e) and e / (1 + e), the reference's operations on the same
+// values (NaN and -0 take the same branch as in the reference).
 __device__ __forceinline__ float silu_ref(float v) {
-    return v >= 0.0f ? v / (1.0f + expf(-v)) : v * expf(v) / (1.0f + expf(v));
+    const float e = expf(-fabsf(v));
+    return (v >= 0.0f ? v : v * e) / (1.0f + e);
 }
 
 __device__ __forceinline__ float sigmoid_ref(float v) {
-    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
-    const float e = expf(v);
-    return e / (1.0f + e);
+    const float e = expf(-fabsf(v));
+    return (v >= 0.0f ? 1.0f : e) / (1.0f + e);
 }
 
 __device__ __forceinline__ void raise_flag(int *flag, int bit) {
