@@ -247,8 +247,18 @@ constexpr int attn_dim_split() { return HD > 256 ? HD / 256 : 1; }
 template <int HD, int WAVES>
 constexpr int attn_min_blocks() { return HD <= 256 && WAVES == 4 ? 2 : 1; }
 
+// With xcd_chunks, workgroup b runs entry local + start(x) of the work list,
+// x = b % 8 (the XCD the hardware dispatches it to), local = b / 8: each XCD
+// takes one contiguous eighth of the list. Consecutive work items of a row
+// then share one L2, which matters when a sliding window gives neighbouring
+// query blocks overlapping key ranges that differ from the rest of the row.
+__device__ __forceinline__ int xcd_chunk(int b, int n) {
+    const int x = b & 7, local = b >> 3, q = n >> 3, r = n & 7;
+    return x * q + min(x, r) + local;
+}
+
 template <int HD, int WAVES, int KT>
-__global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void attn16_kernel(AttnArgs p) {
+__global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void attn16_kernel(AttnArgs p, int xcd_chunks) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int DS = attn_dim_split<HD>();  // waves per 16-vector group
     constexpr int HDW = HD / DS;              // head dims per wave
@@ -268,14 +278,15 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void at
     // partial scores of each wave (DS > 1 only)
     __shared__ f32x4 Sx[DS > 1 ? WAVES * NKB * 64 : 1];
 
-    const AttnTile tile = p.tiles[blockIdx.x / SPLIT];
+    const int wg = xcd_chunks ? xcd_chunk((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
+    const AttnTile tile = p.tiles[wg / SPLIT];
     const int G = p.nh / p.nkv;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int dpart = DS > 1 ? wave % DS : 0;  // this wave's block of head dims
     const int group = wave / DS;
     const int nvec = tile.len * G;
-    const int vbase = tile.qv0 + (blockIdx.x % SPLIT) * VPW;
+    const int vbase = tile.qv0 + (wg % SPLIT) * VPW;
     if (vbase >= nvec) return;   // the whole workgroup: a part past the row's vectors
     const int v = vbase + group * 16 + l16;
     const bool vvalid = v < nvec;
@@ -567,21 +578,26 @@ int attn_block_vectors(int hd) {
 // vision tower: 31.4 ms per 4 images against 31.8 with 64-key and 32.5 with
 // 16-key tiles). Grids of fewer than 128 work items split every item over 4 or
 // 8 workgroups of fewer waves.
+// Workgroups go to XCDs in contiguous chunks of the work list when a sliding
+// window is narrower than some row (the 8 x 2048-token batch's sliding
+// layers: 0.42 against 0.54 ms per launch); rows within the window read the
+// whole row from every block, and there the default interleaving is as fast.
 template <int HD, int KT>
 static hipError_t launch_attn16(const AttnArgs &a, hipStream_t s) {
     // a work item is 128 query vectors: 8 groups of 16, each group one wave
     // (DS waves above head_dim 256)
     constexpr int DS = attn_dim_split<HD>();
     const int64_t t = a.n_tiles;
+    const int chunks = a.window >= 0 && a.longest > a.window + 1;
     if (2 * t >= 256)
         hipLaunchKernelGGL((attn16_kernel<HD, 4 * DS, KT>), dim3((unsigned)(2 * t)),
-                           dim3(256 * DS), 0, s, a);
+                           dim3(256 * DS), 0, s, a, chunks);
     else if (4 * t >= 256)
         hipLaunchKernelGGL((attn16_kernel<HD, 2 * DS, KT>), dim3((unsigned)(4 * t)),
-                           dim3(128 * DS), 0, s, a);
+                           dim3(128 * DS), 0, s, a, chunks);
     else
         hipLaunchKernelGGL((attn16_kernel<HD, DS, KT>), dim3((unsigned)(8 * t)), dim3(64 * DS),
-                           0, s, a);
+                           0, s, a, chunks);
     return hipGetLastError();
 }
 

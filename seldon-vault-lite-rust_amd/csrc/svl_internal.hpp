@@ -112,7 +112,8 @@ struct AttnArgs {
     const int32_t *rowlen;  // per token: length of its row (simple kernel)
     int64_t tokens;
     int *flag;
-    int64_t max_len = 0;    // longest row (0: unknown, bounded by tokens)
+    int64_t max_len = 0;    // bound on the row length (0: unknown, bounded by tokens)
+    int64_t longest = 0;    // longest row actually present (0: unknown)
 };
 // Query vectors per work item of the MFMA kernel (0 if hd has no MFMA kernel).
 int attn_block_vectors(int hd);
