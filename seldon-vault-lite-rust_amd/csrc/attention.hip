@@ -247,7 +247,7 @@ constexpr int attn_dim_split() { return HD > 256 ? HD / 256 : 1; }
 template <int HD, int WAVES>
 constexpr int attn_min_blocks() { return HD <= 256 && WAVES == 4 ? 2 : 1; }
 
-// With xcd_chunks, workgroup b runs entry local + start(x) of the work list,
+// With xcd_chunks, workgroup b runs entry start(x) + local of the work list,
 // x = b % 8 (the XCD the hardware dispatches it to), local = b / 8: each XCD
 // takes one contiguous eighth of the list. Consecutive work items of a row
 // then share one L2, which matters when a sliding window gives neighbouring
@@ -579,16 +579,19 @@ int attn_block_vectors(int hd) {
 // 16-key tiles). Grids of fewer than 128 work items split every item over 4 or
 // 8 workgroups of fewer waves.
 // Workgroups go to XCDs in contiguous chunks of the work list when a sliding
-// window is narrower than some row (the 8 x 2048-token batch's sliding
-// layers: 0.42 against 0.54 ms per launch); rows within the window read the
-// whole row from every block, and there the default interleaving is as fast.
+// window is narrower than every row (the 8 x 2048-token batch's sliding
+// layers: 0.42 against 0.54 ms per launch). Every work item then spans about
+// the same number of keys, so equal chunks are equal work. Rows within the
+// window read the whole row from every block, where the default interleaving
+// is as fast, and a list of unequal items keeps its longest-first order
+// spread over all XCDs.
 template <int HD, int KT>
 static hipError_t launch_attn16(const AttnArgs &a, hipStream_t s) {
     // a work item is 128 query vectors: 8 groups of 16, each group one wave
     // (DS waves above head_dim 256)
     constexpr int DS = attn_dim_split<HD>();
     const int64_t t = a.n_tiles;
-    const int chunks = a.window >= 0 && a.longest > a.window + 1;
+    const int chunks = a.window >= 0 && a.shortest > a.window + 1;
     if (2 * t >= 256)
         hipLaunchKernelGGL((attn16_kernel<HD, 4 * DS, KT>), dim3((unsigned)(2 * t)),
                            dim3(256 * DS), 0, s, a, chunks);

@@ -335,7 +335,7 @@ struct Group {
     int32_t r0 = 0, nrows = 0;  // rows [r0, r0 + nrows)
     int64_t t0 = 0, T = 0;      // tokens [t0, t0 + T)
     int64_t off_slot = 0;       // first entry of this group's rebased offsets
-    int64_t longest = 0;        // longest row of the group
+    int64_t shortest = 0;       // shortest row of the group
     // attention work lists per distinct (nkv, hd): (first tile, count)
     std::map<std::pair<int, int>, std::pair<int, int>> tile_ranges;
     double attn_flops[2] = {0, 0};  // algorithmic attention FLOPs per layer type
@@ -353,8 +353,10 @@ struct Batch {
 void build_group(const svl_text_model *m, Batch &b, Group &g) {
     g.off_slot = (int64_t)b.dev_offsets.size();
     for (int r = 0; r <= g.nrows; ++r) b.dev_offsets.push_back(b.offsets[g.r0 + r] - g.t0);
-    for (int r = 0; r < g.nrows; ++r)
-        g.longest = std::max(g.longest, b.offsets[g.r0 + r + 1] - b.offsets[g.r0 + r]);
+    for (int r = 0; r < g.nrows; ++r) {
+        const int64_t len = b.offsets[g.r0 + r + 1] - b.offsets[g.r0 + r];
+        g.shortest = r == 0 ? len : std::min(g.shortest, len);
+    }
     std::vector<int> order(g.nrows);
     for (int r = 0; r < g.nrows; ++r) order[r] = g.r0 + r;
     // longest rows first: the attention cost of a work item grows with its row
@@ -405,20 +407,17 @@ void build_groups(const svl_text_model *m, Batch &b, int max_groups) {
     b.dev_offsets.clear();
     int ng = 1;
     if (b.T >= SPLIT_MIN_TOKENS) ng = std::max(1, std::min<int>(max_groups, b.B));
-    // When most tokens are in rows longer than the sliding window, the sliding
-    // layers' attention gives each XCD a contiguous range of its work items
+    // When every row is longer than the sliding window, the sliding layers'
+    // attention gives each XCD a contiguous range of its work items
     // (launch_attention). Concurrent row groups interleave their workgroups
     // over the XCDs and lose that placement, which is worth more than their
     // overlap: 8 x 2048 tokens take 43.2 ms as one group, 44.3 ms as three.
     bool windowed = false;
     for (const DevLayer &ly : m->layers) windowed = windowed || !ly.full;
-    if (windowed && m->window >= 0) {
-        int64_t long_tokens = 0;
-        for (int32_t i = 0; i < b.B; ++i) {
-            const int64_t len = b.offsets[i + 1] - b.offsets[i];
-            if (len > m->window + 1) long_tokens += len;
-        }
-        if (2 * long_tokens > b.T) ng = 1;
+    if (windowed && m->window >= 0 && b.B > 0) {
+        int64_t shortest = b.offsets[1] - b.offsets[0];
+        for (int32_t i = 1; i < b.B; ++i) shortest = std::min(shortest, b.offsets[i + 1] - b.offsets[i]);
+        if (shortest > m->window + 1) ng = 1;
     }
     // group k starts at the first row boundary at or past k/ng of the tokens,
     // every group keeping at least one row
@@ -554,7 +553,7 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
             a.tokens = T;
             a.flag = flag;
             a.max_len = std::min<int64_t>(T, MAX_TEXT_TOKENS);  // validate_row caps every row
-            a.longest = grp.longest;
+            a.shortest = grp.shortest;
             Timer tm(m, s, KC_ATTENTION, grp.attn_flops[ly.full]);
             HIP_TRY(launch_attention(a, s));
         }
@@ -1312,7 +1311,7 @@ static AttnArgs seam_attention_args(const float *d_q, const float *d_k, const fl
     a.scale = scale;
     a.tokens = seq_len;
     a.max_len = seq_len;
-    a.longest = seq_len;
+    a.shortest = seq_len;
     return a;
 }
 

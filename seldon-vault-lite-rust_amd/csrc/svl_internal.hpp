@@ -113,7 +113,7 @@ struct AttnArgs {
     int64_t tokens;
     int *flag;
     int64_t max_len = 0;    // bound on the row length (0: unknown, bounded by tokens)
-    int64_t longest = 0;    // longest row actually present (0: unknown)
+    int64_t shortest = 0;   // shortest row of the launch (0: unknown)
 };
 // Query vectors per work item of the MFMA kernel (0 if hd has no MFMA kernel).
 int attn_block_vectors(int hd);

@@ -180,8 +180,8 @@ def test_packed_batch_equals_independent_calls_bit_for_bit():
 
 
 def test_two_stream_row_groups_are_bit_identical():
-    # Batches above 4096 tokens run as row groups on concurrent streams (rows
-    # within the 512 window: a batch mostly of longer rows runs as one group).
+    # Batches above 4096 tokens run as row groups on concurrent streams (a
+    # batch whose rows are all longer than the 512 window runs as one group).
     cfg = svl_synth.config_a(layers=2, vocab=4096)
     w = svl_synth.weights(cfg)
     m = model(cfg, w)
