@@ -244,6 +244,14 @@ __device__ __forceinline__ float fold_xor16_32_sum(float v) {
 template <int HD>
 constexpr int attn_dim_split() { return HD > 256 ? HD / 256 : 1; }
 
+// Short grids (a few rows of a few hundred tokens) leave most SIMDs idle, and
+// each wave's time is its dependent MFMA work: per 16-key tile, HD / 4 score
+// MFMAs and HD / 4 P.V MFMAs. With OS > 1 the OS waves of a group share one
+// 16-vector group: each computes all the scores (the same instructions in the
+// same order, so the same bits), runs the same softmax, and applies P to its
+// own HD / OS dims of V. A wave's chain shrinks to HD / 4 + HD / (4 OS) MFMAs
+// per tile, and every output element is the sum it is with OS = 1.
+
 template <int HD, int WAVES>
 constexpr int attn_min_blocks() { return HD <= 256 && WAVES == 4 ? 2 : 1; }
 
@@ -257,24 +265,41 @@ __device__ __forceinline__ int xcd_chunk(int b, int n) {
     return x * q + min(x, r) + local;
 }
 
-template <int HD, int WAVES, int KT>
+template <int HD, int WAVES, int KT, int OS = 1, int NS = 2>
 __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void attn16_kernel(AttnArgs p, int xcd_chunks) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    constexpr int DS = attn_dim_split<HD>();  // waves per 16-vector group
-    constexpr int HDW = HD / DS;              // head dims per wave
+    constexpr int DS = attn_dim_split<HD>();  // waves per 16-vector group (score dims)
+    constexpr int HDW = HD / DS;              // head dims per wave (scores)
+    constexpr int HDO = HDW / OS;             // output dims per wave
     constexpr int NKB = KT / 16;              // 16-key blocks per tile
-    constexpr int VPW = 16 * WAVES / DS;      // query vectors per workgroup
+    constexpr int VPW = 16 * WAVES / (DS * OS);  // query vectors per workgroup
     constexpr int SPLIT = 128 / VPW;          // workgroups per 128-vector work item
     constexpr int INSTR_PER_WAVE = KT * HD / 256 / WAVES;  // 1 KB DMA instructions per operand
     static_assert(HD == 64 || HD == 128 || HD == 256 || HD == 512, "head dim");
     static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4 || WAVES == 8, "waves");
-    static_assert(WAVES % DS == 0 && 128 % VPW == 0, "vector groups");
+    static_assert(WAVES % (DS * OS) == 0 && 128 % VPW == 0, "vector groups");
+    static_assert(OS == 1 || (DS == 1 && HDO % 64 == 0), "output split");
     static_assert(KT % 16 == 0 && INSTR_PER_WAVE >= 1 && (KT * HD / 256) % WAVES == 0, "key tile");
+    static_assert(NS >= 2 && NS <= 4 && (NS - 2) * 2 * INSTR_PER_WAVE < 64, "pipeline depth");
     // One LDS object per stage, addressed with compile-time stage indices:
     // the compiler can then see that the DMA filling one stage does not alias
-    // the reads of the other and need not drain it before reading.
-    __shared__ float Ks0[KT * HD], Ks1[KT * HD];
-    __shared__ float Vs0[KT * HD], Vs1[KT * HD];
+    // the reads of another and need not drain it before reading.
+    __shared__ float Ks0[KT * HD], Ks1[KT * HD], Ks2[NS > 2 ? KT * HD : 4], Ks3[NS > 3 ? KT * HD : 4];
+    __shared__ float Vs0[KT * HD], Vs1[KT * HD], Vs2[NS > 2 ? KT * HD : 4], Vs3[NS > 3 ? KT * HD : 4];
+    auto kstage = [&](auto st) -> float * {
+        constexpr int i = decltype(st)::value;
+        if constexpr (i == 0) return Ks0;
+        else if constexpr (i == 1) return Ks1;
+        else if constexpr (i == 2) return Ks2;
+        else return Ks3;
+    };
+    auto vstage = [&](auto st) -> float * {
+        constexpr int i = decltype(st)::value;
+        if constexpr (i == 0) return Vs0;
+        else if constexpr (i == 1) return Vs1;
+        else if constexpr (i == 2) return Vs2;
+        else return Vs3;
+    };
     // partial scores of each wave (DS > 1 only)
     __shared__ f32x4 Sx[DS > 1 ? WAVES * NKB * 64 : 1];
 
@@ -284,7 +309,8 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void at
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int dpart = DS > 1 ? wave % DS : 0;  // this wave's block of head dims
-    const int group = wave / DS;
+    const int opart = OS > 1 ? wave % OS : 0;  // this wave's block of output dims
+    const int group = wave / (DS * OS);
     const int nvec = tile.len * G;
     const int vbase = tile.qv0 + (wg % SPLIT) * VPW;
     if (vbase >= nvec) return;   // the whole workgroup: a part past the row's vectors
@@ -303,9 +329,9 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void at
 #pragma unroll
     for (int c = 0; c < HDW / 16; ++c) qf[c] = *(const f32x4 *)(qrow + 16 * c + 4 * g) * scale2;
 
-    f32x4 o[HDW / 16];
+    f32x4 o[HDO / 16];
 #pragma unroll
-    for (int t = 0; t < HDW / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < HDO / 16; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_ref = -INFINITY, l_run = 0.f;
 
     const int v_last = min(vbase + VPW, nvec) - 1;
@@ -340,8 +366,8 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void at
         voff[q] = (r * ldv + 4 * slot) * 4;
     }
     auto issue = [&](auto st, int k0) {
-        float *kd = decltype(st)::value == 0 ? Ks0 : Ks1;
-        float *vd = decltype(st)::value == 0 ? Vs0 : Vs1;
+        float *kd = kstage(st);
+        float *vd = vstage(st);
 #pragma unroll
         for (int q = 0; q < INSTR_PER_WAVE; ++q) {
             const int f0 = (wave * INSTR_PER_WAVE + q) * 256;
@@ -357,16 +383,24 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void at
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
 
     issue(S0{}, k_first);
-    // key tile it lives in stage it % 2; the loop is unrolled twice so the
-    // stage index is a constant
+    if constexpr (NS > 2) if (1 < n_tiles) issue(S1{}, k_first + KT);
+    if constexpr (NS > 3) if (2 < n_tiles) issue(S2{}, k_first + 2 * KT);
+    // key tile it lives in stage it % NS; the loop is unrolled NS times so
+    // the stage index is a constant
     auto step = [&](int it, auto st) {
         constexpr int cur = decltype(st)::value;
         const int k0 = k_first + it * KT;
-        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
-        __syncthreads();
-        if (it + 1 < n_tiles) issue(std::integral_constant<int, cur ^ 1>{}, k0 + KT);
+        // this wave's DMA of tile it has landed: only the NS - 2 later tiles
+        // (2 x INSTR_PER_WAVE instructions each) may still be in flight
+        if (it + NS - 2 < n_tiles) wait_vmcnt<(NS - 2) * 2 * INSTR_PER_WAVE>();
+        else wait_vmcnt<0>();
+        __syncthreads();   // ... and every wave's; tile it - 1 is no longer read
+        if (it + NS - 1 < n_tiles)
+            issue(std::integral_constant<int, (cur + NS - 1) % NS>{}, k0 + (NS - 1) * KT);
 
         // S^T for keys kb * 16 + 4 (lane / 16) + r (register r of block kb)
         // and query vector lane % 16. K row kb * 16 + l16 holds dim chunk
@@ -374,7 +408,7 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void at
         // slot ch ^ l16.
         // The fragments of chunk c + 1 are read while chunk c's MFMAs run,
         // and the two key blocks' chains alternate.
-        const float *kb0 = (cur == 0 ? Ks0 : Ks1) + l16 * HD;
+        const float *kb0 = kstage(st) + l16 * HD;
         const int ch0 = dpart * (HDW / 4);
         f32x4 s[NKB], kf[NKB];
 #pragma unroll
@@ -456,7 +490,7 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void at
             const float alpha = m_ref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - m_new);
             l_run *= alpha;
 #pragma unroll
-            for (int t = 0; t < HDW / 16; ++t) o[t] = o[t] * alpha;
+            for (int t = 0; t < HDO / 16; ++t) o[t] = o[t] * alpha;
             m_ref = m_new;
         }
         float psum = 0.f;
@@ -474,13 +508,13 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void at
         // l supplies V row kb * 16 + 4 (l / 16) + r, dims 64 c + 4 (l % 16)
         // .. + 3 of the wave's block, one per output tile 4 c + t (tile row
         // i = dim 64 c + 4 i + t).
-        const float *vb = (cur == 0 ? Vs0 : Vs1) + 4 * g * HD + 4 * l16 + dpart * HDW;
+        const float *vb = vstage(st) + 4 * g * HD + 4 * l16 + dpart * HDW + opart * HDO;
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int c = 0; c < HDW / 64; ++c) {
+                for (int c = 0; c < HDO / 64; ++c) {
                     const f32x4 va = *(const f32x4 *)(vb + (kb * 16 + r) * HD + 64 * c);
 #pragma unroll
                     for (int t = 0; t < 4; ++t)
@@ -488,19 +522,21 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void at
                                                                           o[4 * c + t], 0, 0, 0);
                 }
     };
-    for (int it = 0; it < n_tiles; it += 2) {
+    for (int it = 0; it < n_tiles; it += NS) {
         step(it, S0{});
         if (it + 1 < n_tiles) step(it + 1, S1{});
+        if constexpr (NS > 2) if (it + 2 < n_tiles) step(it + 2, S2{});
+        if constexpr (NS > 3) if (it + 3 < n_tiles) step(it + 3, S3{});
     }
 
     if (vvalid) {
         // lane l holds, for its query vector, dims 64 c + 16 (l / 16) + 4 r
         // + t in register r of tile 4 c + t
         const float inv = 1.0f / l_run;
-        float *orow = p.out + (int64_t)(tile.tok0 + qpos) * p.ldo + qhead * HD + dpart * HDW;
+        float *orow = p.out + (int64_t)(tile.tok0 + qpos) * p.ldo + qhead * HD + dpart * HDW + opart * HDO;
         bool ok = isfinite(inv);
 #pragma unroll
-        for (int c = 0; c < HDW / 64; ++c)
+        for (int c = 0; c < HDO / 64; ++c)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 f32x4 d;
@@ -577,7 +613,12 @@ int attn_block_vectors(int hd) {
 // double buffered, two 4-wave workgroups per CU), 32 at 128 and at 64 (the
 // vision tower: 31.4 ms per 4 images against 31.8 with 64-key and 32.5 with
 // 16-key tiles). Grids of fewer than 128 work items split every item over 4 or
-// 8 workgroups of fewer waves.
+// 8 workgroups of fewer waves; below 64 items each 16-vector group also takes
+// OS waves that split the output dims (4 at head_dim 256, 2 at 128), up to
+// one wave per SIMD (32 items at OS 4), with three LDS stages. Per layer, the
+// 1 x 128-token row's attention (3 items) went from 24.0 to 17.6 us, a
+// 754-token row's from 124 to 83 us (two stages: 17.8 and 85 us; four: 18.0
+// and 85 us).
 // Workgroups go to XCDs in contiguous chunks of the work list when a sliding
 // window is narrower than every row (the 8 x 2048-token batch's sliding
 // layers: 0.42 against 0.54 ms per launch). Every work item then spans about
@@ -598,7 +639,15 @@ static hipError_t launch_attn16(const AttnArgs &a, hipStream_t s) {
     else if (4 * t >= 256)
         hipLaunchKernelGGL((attn16_kernel<HD, 2 * DS, KT>), dim3((unsigned)(4 * t)),
                            dim3(128 * DS), 0, s, a, chunks);
-    else
+    else if constexpr (DS == 1 && HD >= 128) {
+        constexpr int OS = HD / 64 >= 4 ? 4 : HD / 64;
+        if (OS * 8 * t <= 1024)
+            hipLaunchKernelGGL((attn16_kernel<HD, OS, KT, OS, 3>), dim3((unsigned)(8 * t)),
+                               dim3(64 * OS), 0, s, a, chunks);
+        else
+            hipLaunchKernelGGL((attn16_kernel<HD, 2, KT, 2>), dim3((unsigned)(8 * t)), dim3(128),
+                               0, s, a, chunks);
+    } else
         hipLaunchKernelGGL((attn16_kernel<HD, DS, KT>), dim3((unsigned)(8 * t)), dim3(64 * DS),
                            0, s, a, chunks);
     return hipGetLastError();

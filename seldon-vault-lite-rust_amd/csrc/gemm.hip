@@ -189,6 +189,42 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x4 (&a
     }
 }
 
+// Paired epilogue over two waves (short grids): the wave holding the first
+// halves x of a 32-column pair block (wn = 0) receives the second halves y
+// from its partner through LDS (yv: block (i, u) of the partner at
+// yv[(2 i + u) * 64 + lane]) and stores the 32 output columns of the pair.
+// Same values as the one-wave paired epilogue above.
+template <int TM, int EPI>
+__device__ __forceinline__ void gemm_epilogue_pair_split(const GemmArgs &p,
+                                                         const f32x4 (&acc)[TM][2],
+                                                         const f32x4 *yv, int mw, int nw, int l16,
+                                                         int g) {
+    float olo = 0.f, ohi = 0.f;
+    if constexpr (clipped_epi<EPI>()) {
+        olo = p.clip[0][2];
+        ohi = p.clip[0][3];
+    }
+    const bool vec = (p.ldc & 3) == 0 && ((uintptr_t)p.C & 15) == 0;
+    const int lane = l16 + 16 * g;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        f32x4 v[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const f32x4 y4 = yv[(2 * i + u) * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float x = acc[i][u][r], y = y4[r];
+                if constexpr (EPI == EPI_GEGLU)
+                    v[u][r] = gelu_tanh(x) * y;
+                else
+                    v[u][r] = clamp_ref(x, olo, ohi) * sigmoid_ref(clamp_ref(y, olo, ohi));
+            }
+        }
+        store_pair(p, p.n_out, vec, mw + i * 16, nw / 2, l16, g, v[0], v[1]);
+    }
+}
+
 template <int BM, int BN, int EPI, int MINB = 2>
 __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_m, int tiles_n) {
     using S = GemmShape<BM, BN>;
@@ -281,13 +317,6 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
     gemm_epilogue<S::TM, S::TN, EPI>(p, acc, m0 + wm * S::WM, n0 + wn * S::WN, l16, g, seg);
 }
 
-// s_waitcnt vmcnt(N): at most N vector-memory operations of this wave in flight.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // Direct-to-LDS variant; requires K % BK == 0 and 16-byte aligned rows. NS
 // LDS stages: NS - 1 slices are in flight while one is consumed. WMW waves
 // along M, 4 / WMW along N.
@@ -311,7 +340,12 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     static_assert(WMW == 1 || WMW == 2 || WMW == 4, "wave layout");
     static_assert(BK % 16 == 0 && WTM % 16 == 0 && WTN % 16 == 0 && A_CH >= 1 && W_CH >= 1,
                   "tile shape");
-    static_assert(!paired_epi<EPI>() || TN % 4 == 0, "paired epilogues take 64-column wave tiles");
+    // paired epilogues: 64-column wave tiles (x and y halves in one wave), or
+    // 64-column workgroup tiles whose two wave columns hold x and y
+    constexpr bool PAIR_SPLIT = paired_epi<EPI>() && TN == 2;
+    static_assert(!paired_epi<EPI>() || TN % 4 == 0 || (PAIR_SPLIT && WNW == 2),
+                  "paired epilogues take 64-column wave or workgroup tiles");
+    static_assert(!PAIR_SPLIT || WMW * TM * 2 * 64 * 4 <= BM * BK, "pair exchange fits stage 0");
     static_assert(NS >= 2 && NS <= 4 && (NS - 2) * (A_CH + W_CH) < 64, "pipeline depth");
     // One LDS object per stage, addressed with compile-time stage indices, so
     // the compiler can see that the DMA filling one stage never aliases the
@@ -436,7 +470,20 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
         if constexpr (NS > 2) if (kt + 2 < nk) step(kt + 2, S2{});
         if constexpr (NS > 3) if (kt + 3 < nk) step(kt + 3, S3{});
     }
-    gemm_epilogue<TM, TN, EPI>(p, acc, m0 + wm * WTM, n0 + wn * WTN, l16, g, seg);
+    if constexpr (PAIR_SPLIT) {
+        __syncthreads();  // every wave is done reading the stages
+        f32x4 *xch = (f32x4 *)As0 + wm * TM * 2 * 64;
+        if (wn == 1) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) xch[(2 * i + u) * 64 + lane] = acc[i][u];
+        }
+        __syncthreads();
+        if (wn == 0) gemm_epilogue_pair_split<TM, EPI>(p, acc, xch, m0 + wm * WTM, n0, l16, g);
+    } else {
+        gemm_epilogue<TM, TN, EPI>(p, acc, m0 + wm * WTM, n0 + wn * WTN, l16, g, seg);
+    }
 #endif
 }
 
@@ -515,13 +562,13 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 //    rounds that the cost model above optimises for.
 //  * Grids that 64x64 tiles would not cover once (one short row, 128 tokens:
 //    QKV at 6.9 us against 15.9 us for 64x64 tiles): 32x32 tiles, one 16x16
-//    block per wave; paired epilogues 64x64 tiles with the four waves
-//    stacked along M (one 16x64 block each).
-//  * Paired epilogues need the 32 + 32 columns of a pair in one wave: 64x128
-//    tiles (4 per CU; the 18688-token gate/up: 481 us against 502 us for
-//    128x128; per row group, with 32-wide K slices: 168 us against 185 us),
-//    deeper pipelines below two rounds of 128x128 tiles, or 64x64 with the
-//    four waves stacked along M on one-row grids.
+//    block per wave; paired epilogues 32x64 tiles whose two wave columns
+//    hold the x and y halves of the pair block (two 16x16 blocks per wave),
+//    joined through LDS for the epilogue.
+//  * Otherwise paired epilogues keep the 32 + 32 columns of a pair in one
+//    wave: 64x128 tiles (4 per CU; the 18688-token gate/up: 481 us against
+//    502 us for 128x128; per row group, with 32-wide K slices: 168 us against
+//    185 us), with deeper pipelines below two rounds of 128x128 tiles.
 //  * Outputs of at most 32 columns (the audio subsampling's 32 channels):
 //    128x32 tiles, the four waves stacked along M, instead of 64x64 tiles
 //    that would spend half their MFMAs on zero columns.
@@ -556,8 +603,13 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
     const bool tiny = tiles(64, 64) < 256 && a.K % 32 == 0;
     if constexpr (paired_epi<EPI>()) {
         if (tiny) {
-            if (a.K % 64 == 0) return launch_dma<64, 64, 64, EPI, 1, 3, 4>(a, s);
-            return launch_dma<64, 64, 32, EPI, 1, 4, 4>(a, s);
+            // 32x64 tiles: the x and y halves of each pair on two waves, so a
+            // wave's chain is 2 x K / 4 MFMAs (gate/up at 128 tokens: 12.1 us
+            // against 17.6 us for 64x64 tiles with one 16x64 block per wave;
+            // three or four stages measured no faster)
+            if (a.K % 128 == 0) return launch_dma<32, 64, 128, EPI, 1, 2, 2>(a, s);
+            if (a.K % 64 == 0) return launch_dma<32, 64, 64, EPI, 1, 3, 2>(a, s);
+            return launch_dma<32, 64, 32, EPI, 1, 4, 2>(a, s);
         }
         if (a.cus > 0 && a.K % 32 == 0) return launch_dma<64, 128, 32, EPI, 3, 2>(a, s);
         if (tiles(128, 128) < 2 * 256) {
