@@ -296,11 +296,12 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(
     if (!ok) raise_flag(flag, FLAG_NONFINITE);
 }
 
-// head_dim 256 fast path: one wave per token. Lane l holds elements
-// [4l, 4l+4) of every head row of the token (one float4 per head row), so
-// each head-row norm is one wave reduction, and the rotate-half partner of
-// element j < 128 (element j + 128) sits in lane l ^ 32.
-template <int ROWS>
+// head_dim 256 fast path: one wave per token, two head rows per wave
+// instruction. Lane l works on row 2 i + l / 32 of the token, elements
+// [4 (l % 32), +4) and [128 + 4 (l % 32), +4): the rotate-half partner of
+// each element (j and j + 128) sits in the same lane, and each row's norm is
+// a 32-lane reduction.
+template <int PAIRS>
 __global__ __launch_bounds__(256) void qkv_post256_kernel(
     float *__restrict__ qkv, int64_t ld, int64_t tokens, int nh, int nkv,
     const float *__restrict__ qn, const float *__restrict__ kn, const float *__restrict__ cos_t,
@@ -309,23 +310,84 @@ __global__ __launch_bounds__(256) void qkv_post256_kernel(
     const int lane = threadIdx.x & 63;
     if (t >= tokens) return;
     const int per_tok = nh + 2 * nkv;
+    const int h = lane >> 5, l32 = lane & 31;
+    f32x4 *row = (f32x4 *)(qkv + t * ld) + 64 * h + l32;  // row h of the token
+    f32x4 x[PAIRS][2];
+    float ss[PAIRS];
+#pragma unroll
+    for (int i = 0; i < PAIRS; ++i) {
+        ss[i] = 0.f;
+        if (2 * i + h < per_tok) {
+            x[i][0] = row[128 * i];
+            x[i][1] = row[128 * i + 32];
+            ss[i] = x[i][0].x * x[i][0].x + x[i][0].y * x[i][0].y + x[i][0].z * x[i][0].z +
+                    x[i][0].w * x[i][0].w + x[i][1].x * x[i][1].x + x[i][1].y * x[i][1].y +
+                    x[i][1].z * x[i][1].z + x[i][1].w * x[i][1].w;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < PAIRS; ++i) ss[i] = group_reduce<32, false>(ss[i]);
+    const f32x4 wq0 = ((const f32x4 *)qn)[l32], wq1 = ((const f32x4 *)qn)[l32 + 32];
+    const f32x4 wk0 = ((const f32x4 *)kn)[l32], wk1 = ((const f32x4 *)kn)[l32 + 32];
+    const int64_t tab = (int64_t)pos[t] * 128 + 4 * l32;
+    const f32x4 c = *(const f32x4 *)(cos_t + tab);
+    const f32x4 sn = *(const f32x4 *)(sin_t + tab);
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < PAIRS; ++i) {
+        const int k = 2 * i + h;
+        if (k >= per_tok) continue;
+        ok = ok && isfinite(ss[i]);
+        const float inv = rms_inverse(ss[i], 256, eps);
+        if (k >= nh + nkv) {  // value head: unscaled norm, no rotation
+            const f32x4 y0 = x[i][0] * inv, y1 = x[i][1] * inv;
+            ok = ok && finite4(y0) && finite4(y1);
+            row[128 * i] = y0;
+            row[128 * i + 32] = y1;
+            continue;
+        }
+        const f32x4 first = x[i][0] * inv * (k < nh ? wq0 : wk0);
+        const f32x4 second = x[i][1] * inv * (k < nh ? wq1 : wk1);
+        const f32x4 a = first * c - second * sn;
+        const f32x4 b = first * sn + second * c;
+        ok = ok && finite4(a) && finite4(b);
+        row[128 * i] = a;
+        row[128 * i + 32] = b;
+    }
+    if (!ok) raise_flag(flag, FLAG_NONFINITE);
+}
+
+// head_dim 512 fast path: one wave per token. Lane l holds elements
+// [4l, 4l+4) and [256+4l, 256+4l+4) of every head row, so the rotate-half
+// partner of each element (j and j + 256) sits in the same lane.
+template <int ROWS>
+__global__ __launch_bounds__(256) void qkv_post512_kernel(
+    float *__restrict__ qkv, int64_t ld, int64_t tokens, int nh, int nkv,
+    const float *__restrict__ qn, const float *__restrict__ kn, const float *__restrict__ cos_t,
+    const float *__restrict__ sin_t, const int32_t *__restrict__ pos, float eps, int *flag) {
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= tokens) return;
+    const int per_tok = nh + 2 * nkv;
     f32x4 *row = (f32x4 *)(qkv + t * ld) + lane;
-    f32x4 x[ROWS];
+    f32x4 x[ROWS][2];
     float ss[ROWS];
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
         if (k < per_tok) {
-            x[k] = row[64 * k];
-            ss[k] = x[k].x * x[k].x + x[k].y * x[k].y + x[k].z * x[k].z + x[k].w * x[k].w;
+            x[k][0] = row[128 * k];
+            x[k][1] = row[128 * k + 64];
+            ss[k] = x[k][0].x * x[k][0].x + x[k][0].y * x[k][0].y + x[k][0].z * x[k][0].z +
+                    x[k][0].w * x[k][0].w + x[k][1].x * x[k][1].x + x[k][1].y * x[k][1].y +
+                    x[k][1].z * x[k][1].z + x[k][1].w * x[k][1].w;
         }
     }
 #pragma unroll
     for (int k = 0; k < ROWS; ++k)
         if (k < per_tok) ss[k] = wave_sum(ss[k]);
-    const f32x4 wq = ((const f32x4 *)qn)[lane];
-    const f32x4 wk = ((const f32x4 *)kn)[lane];
-    const int half = lane >> 5;  // 0: elements j < 128, 1: j >= 128
-    const int64_t tab = (int64_t)pos[t] * 128 + 4 * (lane & 31);
+    const f32x4 wq0 = ((const f32x4 *)qn)[lane], wq1 = ((const f32x4 *)qn)[lane + 64];
+    const f32x4 wk0 = ((const f32x4 *)kn)[lane], wk1 = ((const f32x4 *)kn)[lane + 64];
+    const int64_t tab = (int64_t)pos[t] * 256 + 4 * lane;
     const f32x4 c = *(const f32x4 *)(cos_t + tab);
     const f32x4 sn = *(const f32x4 *)(sin_t + tab);
     bool ok = true;
@@ -333,23 +395,21 @@ __global__ __launch_bounds__(256) void qkv_post256_kernel(
     for (int k = 0; k < ROWS; ++k) {
         if (k >= per_tok) continue;
         ok = ok && isfinite(ss[k]);
-        const float inv = rms_inverse(ss[k], 256, eps);
+        const float inv = rms_inverse(ss[k], 512, eps);
         if (k >= nh + nkv) {  // value head: unscaled norm, no rotation
-            const f32x4 y = x[k] * inv;
-            ok = ok && finite4(y);
-            row[64 * k] = y;
+            const f32x4 y0 = x[k][0] * inv, y1 = x[k][1] * inv;
+            ok = ok && finite4(y0) && finite4(y1);
+            row[128 * k] = y0;
+            row[128 * k + 64] = y1;
             continue;
         }
-        const f32x4 y = x[k] * inv * (k < nh ? wq : wk);
-        f32x4 other;
-        other.x = __shfl_xor(y.x, 32, 64);
-        other.y = __shfl_xor(y.y, 32, 64);
-        other.z = __shfl_xor(y.z, 32, 64);
-        other.w = __shfl_xor(y.w, 32, 64);
-        // first half: first*c - second*s; second half: first*s + second*c
-        const f32x4 out = half ? other * sn + y * c : y * c - other * sn;
-        ok = ok && finite4(out);
-        row[64 * k] = out;
+        const f32x4 first = x[k][0] * inv * (k < nh ? wq0 : wk0);
+        const f32x4 second = x[k][1] * inv * (k < nh ? wq1 : wk1);
+        const f32x4 a = first * c - second * sn;
+        const f32x4 b = first * sn + second * c;
+        ok = ok && finite4(a) && finite4(b);
+        row[128 * k] = a;
+        row[128 * k + 64] = b;
     }
     if (!ok) raise_flag(flag, FLAG_NONFINITE);
 }
@@ -364,12 +424,17 @@ hipError_t launch_qkv_post(float *qkv, int64_t ld, int64_t tokens, int nh, int n
     const bool aligned = ld % 4 == 0 && (uintptr_t)qkv % 16 == 0;
     if (hd == 256 && aligned && nh + 2 * nkv <= 8) {
         const dim3 grid((unsigned)((tokens + 3) / 4));
-        if (nh + 2 * nkv <= 5)
-            hipLaunchKernelGGL(qkv_post256_kernel<5>, grid, dim3(256), 0, s, qkv, ld, tokens, nh,
+        if (nh + 2 * nkv <= 6)
+            hipLaunchKernelGGL(qkv_post256_kernel<3>, grid, dim3(256), 0, s, qkv, ld, tokens, nh,
                                nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
         else
-            hipLaunchKernelGGL(qkv_post256_kernel<8>, grid, dim3(256), 0, s, qkv, ld, tokens, nh,
+            hipLaunchKernelGGL(qkv_post256_kernel<4>, grid, dim3(256), 0, s, qkv, ld, tokens, nh,
                                nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
+        return hipGetLastError();
+    }
+    if (hd == 512 && aligned && nh + 2 * nkv <= 6) {
+        hipLaunchKernelGGL(qkv_post512_kernel<6>, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0,
+                           s, qkv, ld, tokens, nh, nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(qkv_post_kernel, dim3((unsigned)((head_rows + 3) / 4)), dim3(256), 0, s,
