@@ -252,8 +252,8 @@ constexpr int attn_dim_split() { return HD > 256 ? HD / 256 : 1; }
 // own HD / OS dims of V. A wave's chain shrinks to HD / 4 + HD / (4 OS) MFMAs
 // per tile, and every output element is the sum it is with OS = 1.
 
-template <int HD, int WAVES>
-constexpr int attn_min_blocks() { return HD <= 256 && WAVES == 4 ? 2 : 1; }
+template <int HD, int WAVES, int NS>
+constexpr int attn_min_blocks() { return HD <= 256 && WAVES == 4 && NS == 2 ? 2 : 1; }
 
 // With xcd_chunks, workgroup b runs entry start(x) + local of the work list,
 // x = b % 8 (the XCD the hardware dispatches it to), local = b / 8: each XCD
@@ -266,7 +266,7 @@ __device__ __forceinline__ int xcd_chunk(int b, int n) {
 }
 
 template <int HD, int WAVES, int KT, int OS = 1, int NS = 2>
-__global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES>())) void attn16_kernel(AttnArgs p, int xcd_chunks) {
+__global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES, NS>())) void attn16_kernel(AttnArgs p, int xcd_chunks) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int DS = attn_dim_split<HD>();  // waves per 16-vector group (score dims)
     constexpr int HDW = HD / DS;              // head dims per wave (scores)
