@@ -613,7 +613,13 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
         }
         if (a.cus > 0 && a.K % 32 == 0) return launch_dma<64, 128, 32, EPI, 3, 2>(a, s);
         if (tiles(128, 128) < 2 * 256) {
-            if (tiles(64, 128) < 256 && a.K % 64 == 0) return launch_dma<64, 128, 64, EPI, 1, 3>(a, s);
+            // grids of a few thousand rows: tiles small enough to spread over
+            // every CU (gate/up at 1040 / 2000 / 3016 rows: 34.7 / 63.8 / 88.0
+            // us against 53.9 / 76.6 / 104.2 us for 64x128 tiles)
+            if (a.K % 32 == 0) {
+                if (tiles(64, 64) < 1280) return launch_dma<32, 64, 32, EPI, 4, 2, 2>(a, s);
+                return launch_dma<64, 64, 32, EPI, 4, 2, 4>(a, s);
+            }
             return launch_dma<64, 128, 16, EPI, 3, 4>(a, s);
         }
         return launch_dma<64, 128, 16, EPI, 4, 2>(a, s);
@@ -631,6 +637,10 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
             return launch_dma_staged<128, 128, 16, EPI, 3, 3>(a, s);
         }
         if (a.N <= 32 && a.K % 32 == 0) return launch_dma<128, 32, 32, EPI, 4, 2, 4>(a, s);
+        // less than one round of 64x64 tiles at four per CU: 64x32 tiles
+        // spread the work over every CU (N = 768 at 2000 / 3016 / 4500 rows:
+        // 22.1 / 33.2 / 49.5 us against 28.4 / 39.6 / 55.0 us)
+        if (tiles(64, 64) < 4 * 256 && a.K % 32 == 0) return launch_dma<64, 32, 32, EPI, 4, 2, 2>(a, s);
         auto per_cu = [&](int bm, int bn) { return (double)((tiles(bm, bn) + 255) / 256); };
         const double c128 = per_cu(128, 128) * (128.0 * 128.0);
         const double c12864 = per_cu(128, 64) * (128.0 * 64.0) / 0.95;
