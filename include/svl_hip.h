@@ -276,6 +276,15 @@ svl_status svl_vision_model_create(svl_ctx *ctx, const svl_vision_config *cfg,
                                    size_t n_tensors, svl_vision_model **out);
 svl_status svl_vision_model_destroy(svl_vision_model *model);
 
+/* Batches of two or more images and 4096 or more patches run the encoder
+ * layers as `groups` groups of consecutive images (1..2, default 2), group 0
+ * on the caller's stream and group 1 on a stream of the model, so that one
+ * group's attention and norms overlap the other's projections. groups 1 runs
+ * every batch on one stream; so does a call that captures hidden states.
+ * Results are bit-identical for any setting. No reference counterpart (the
+ * reference encodes one image at a time). */
+svl_status svl_vision_model_set_stream_split(svl_vision_model *model, int groups);
+
 /* VisionModel::forward (vision.rs:742-959) for `batch` images at once; image
  * i's result equals the reference's forward(image i).
  *  out_soft    [sum soft_tokens, text_hidden]  (VisionOutput::pooled of each

@@ -70,6 +70,10 @@ struct svl_vision_model {
     DevBuf<int> flag;
     int *h_flag = nullptr;
     hipStream_t stream = nullptr;
+    // image groups: the encoder layers of the second group run on `extra`
+    int groups = 2;
+    hipStream_t extra = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     std::mutex mu;
 
     ~svl_vision_model() {
@@ -82,6 +86,9 @@ struct svl_vision_model {
         bin_patch.release(); offsets.release(); tiles.release(); flag.release();
         if (h_flag) (void)hipHostFree(h_flag);
         if (stream) (void)hipStreamDestroy(stream);
+        if (extra) (void)hipStreamDestroy(extra);
+        if (ev_fork) (void)hipEventDestroy(ev_fork);
+        if (ev_join) (void)hipEventDestroy(ev_join);
     }
 };
 
@@ -189,6 +196,12 @@ struct VisBatch {
     std::vector<AttnTile> tiles;
     int64_t max_coord = 0;
     double attn_flops = 0;
+    // image groups for the encoder layers: patches [t0, t1), attention work
+    // items [w0, w1) of `tiles`
+    struct Group {
+        int64_t t0, t1, w0, w1;
+    };
+    std::vector<Group> groups;
 };
 
 svl_status checked_len(int i, int64_t rows, int64_t width, const char *label) {
@@ -203,7 +216,7 @@ svl_status checked_len(int i, int64_t rows, int64_t width, const char *label) {
 // Validation in the order VisionModel::forward meets each condition
 // (vision.rs:743-809, then pool_patches :981-1032), and the batch layout.
 svl_status prepare_images(const svl_vision_model *v, const svl_image_patches *im, int32_t batch,
-                          bool need_pixels, VisBatch &b) {
+                          bool need_pixels, VisBatch &b, bool single) {
     if (batch < 0) return fail(SVL_USAGE, "negative batch");
     if (batch > 0 && !im) return fail(SVL_USAGE, "images are null");
     b.B = batch;
@@ -281,21 +294,45 @@ svl_status prepare_images(const svl_vision_model *v, const svl_image_patches *im
         std::vector<int32_t> fill(b.bin_start.begin(), b.bin_start.end() - 1);
         for (int64_t t = 0; t < b.T; ++t) b.bin_patch[(size_t)fill[(size_t)bin_of[(size_t)t]]++] = (int32_t)t;
     }
-    // attention work items, longest images first
+    // Image groups: consecutive images in two groups of about equal patch
+    // counts when there are two or more images and 4096 or more patches
+    // (and the MFMA attention applies); otherwise one group.
     const int bv = attn_block_vectors((int)v->hd);
-    std::vector<int> order(batch);
-    for (int i = 0; i < batch; ++i) order[i] = i;
-    std::stable_sort(order.begin(), order.end(), [&](int x, int y) {
-        return im[x].valid_patches > im[y].valid_patches;
-    });
-    const int G = (int)(v->NH / v->NKV);
-    if (bv > 0)
-        for (int i : order) {
-            const int64_t len = im[i].valid_patches;
-            for (int kv = 0; kv < v->NKV; ++kv)
-                for (int64_t v0 = 0; v0 < len * G; v0 += bv)
-                    b.tiles.push_back({(int32_t)b.offsets[i], (int32_t)len, kv, (int32_t)v0});
+    int cut = 0;  // first image of the second group
+    if (!single && v->groups >= 2 && batch >= 2 && b.T >= 4096 && bv > 0) {
+        int64_t best = b.T;
+        for (int c = 1; c < batch; ++c) {
+            const int64_t d = std::llabs(2 * b.offsets[(size_t)c] - b.T);
+            if (d < best) {
+                best = d;
+                cut = c;
+            }
         }
+    }
+    // attention work items of each group, longest images first
+    const int G = (int)(v->NH / v->NKV);
+    auto add_group = [&](int i0, int i1) {
+        const int64_t w0 = (int64_t)b.tiles.size();
+        std::vector<int> order;
+        for (int i = i0; i < i1; ++i) order.push_back(i);
+        std::stable_sort(order.begin(), order.end(), [&](int x, int y) {
+            return im[x].valid_patches > im[y].valid_patches;
+        });
+        if (bv > 0)
+            for (int i : order) {
+                const int64_t len = im[i].valid_patches;
+                for (int kv = 0; kv < v->NKV; ++kv)
+                    for (int64_t v0 = 0; v0 < len * G; v0 += bv)
+                        b.tiles.push_back({(int32_t)b.offsets[i], (int32_t)len, kv, (int32_t)v0});
+            }
+        b.groups.push_back({b.offsets[(size_t)i0], b.offsets[(size_t)i1], w0, (int64_t)b.tiles.size()});
+    };
+    if (cut > 0) {
+        add_group(0, cut);
+        add_group(cut, batch);
+    } else {
+        add_group(0, batch);
+    }
     for (int i = 0; i < batch; ++i) {
         const double len = (double)im[i].valid_patches;
         b.attn_flops += 4.0 * (double)v->hd * (double)v->NH * len * len;
@@ -340,6 +377,82 @@ svl_status upload_vis_meta(svl_vision_model *v, const VisBatch &b, hipStream_t s
     return SVL_OK;
 }
 
+// The encoder layers (vision.rs:852-930) over patches [g.t0, g.t1) of the
+// batch on stream s; every kernel works row by row or within the group's
+// images, so the rows get the same arithmetic as one launch over the batch.
+// h_hidden: [L + 1, T, H] host capture (one group only).
+svl_status enqueue_vis_layers(svl_vision_model *v, const VisBatch &b, const VisBatch::Group &g,
+                              hipStream_t s, float *h_hidden) {
+    const int64_t T = b.T, H = v->H, R = g.t1 - g.t0;
+    if (R <= 0) return SVL_OK;
+    int *flag = v->flag.p;
+    const int64_t ldqkv = v->qd + 2 * v->kd;
+    const int cus = b.groups.size() > 1 ? (int)(256 / b.groups.size()) : 0;
+    float *h = v->h.p + g.t0 * H, *n = v->n.p + g.t0 * H, *tmp = v->tmp.p + g.t0 * H,
+          *qkv = v->qkv.p + g.t0 * ldqkv, *attn = v->attn.p + g.t0 * v->qd, *act = v->act.p + g.t0 * v->I;
+    for (int64_t l = 0; l < v->L; ++l) {
+        const VisLayer &ly = v->layers[(size_t)l];
+        {
+            GemmArgs ga{n, H, ly.w_qkv, H, qkv, ldqkv, (int)R, (int)ldqkv, (int)H, EPI_STORE, 1.f,
+                        nullptr, 0, 0};
+            ga.cus = cus;
+            HIP_TRY(launch_gemm(ga, s));
+        }
+        HIP_TRY(launch_qkv_post_axial(qkv, ldqkv, R, (int)v->NH, (int)v->NKV, (int)v->hd,
+                                      ly.q_norm, ly.k_norm, v->cos_t.p, v->sin_t.p,
+                                      v->coord.p + 2 * g.t0, v->eps, flag, s));
+        {
+            AttnArgs a{};
+            a.q = v->qkv.p;
+            a.k = v->qkv.p + v->qd;
+            a.v = v->qkv.p + v->qd + v->kd;
+            a.out = v->attn.p;
+            a.ldq = a.ldk = a.ldv = ldqkv;
+            a.ldo = v->qd;
+            a.nh = (int)v->NH;
+            a.nkv = (int)v->NKV;
+            a.hd = (int)v->hd;
+            a.window = -1;   // vision.rs:880 sliding_window: None
+            a.scale = 1.0f;  // vision.rs:881
+            a.tiles = v->tiles.p + g.w0;  // absolute first patches of the group's images
+            a.n_tiles = (int)(g.w1 - g.w0);
+            a.pos = v->apos.p;
+            a.rowlen = v->rowlen.p;
+            a.tokens = T;
+            a.flag = flag;
+            HIP_TRY(launch_attention(a, s));
+        }
+        {
+            GemmArgs ga{attn, v->qd, ly.w_o, v->qd, tmp, H, (int)R, (int)H, (int)v->qd, EPI_STORE,
+                        1.f, nullptr, 0, 0};
+            ga.cus = cus;
+            HIP_TRY(launch_gemm(ga, s));
+        }
+        HIP_TRY(launch_resnorm(tmp, ly.ln_post_attn, h, h, ly.ln_pre_ff, n, 1.0f, R, (int)H, v->eps,
+                               flag, s));
+        {
+            GemmArgs ga{n, H, ly.w_gu, H, act, v->I, (int)R, (int)(2 * v->I_pad), (int)H, EPI_GEGLU,
+                        1.f, nullptr, 0, (int)v->I};
+            ga.cus = cus;
+            HIP_TRY(launch_gemm(ga, s));
+        }
+        {
+            GemmArgs ga{act, v->I, ly.w_down, v->I, tmp, H, (int)R, (int)H, (int)v->I, EPI_STORE,
+                        1.f, nullptr, 0, 0};
+            ga.cus = cus;
+            HIP_TRY(launch_gemm(ga, s));
+        }
+        const float *next = l + 1 < v->L ? v->layers[(size_t)l + 1].ln_in : nullptr;
+        HIP_TRY(launch_resnorm(tmp, ly.ln_post_ff, h, h, next, next ? n : nullptr, 1.0f, R, (int)H,
+                               v->eps, flag, s));
+        if (h_hidden)
+            HIP_TRY(hipMemcpyAsync(h_hidden + (size_t)((l + 1) * T * H), v->h.p,
+                                   (size_t)(T * H) * 4, hipMemcpyDeviceToHost, s));
+    }
+
+    return SVL_OK;
+}
+
 // The tower over the packed patches in d_pix (overwritten with the rescaled
 // values), enqueued on s (vision.rs:760-951). Soft tokens land in v->soft.
 svl_status enqueue_vision(svl_vision_model *v, const VisBatch &b, float *d_pix, hipStream_t s,
@@ -360,61 +473,16 @@ svl_status enqueue_vision(svl_vision_model *v, const VisBatch &b, float *d_pix, 
     if (h_hidden)
         HIP_TRY(hipMemcpyAsync(h_hidden, v->h.p, (size_t)(T * H) * 4, hipMemcpyDeviceToHost, s));
 
-    const int64_t ldqkv = v->qd + 2 * v->kd;
-    for (int64_t l = 0; l < v->L; ++l) {
-        const VisLayer &ly = v->layers[(size_t)l];
-        {
-            GemmArgs g{v->n.p, H, ly.w_qkv, H, v->qkv.p, ldqkv, (int)T, (int)ldqkv, (int)H,
-                       EPI_STORE, 1.f, nullptr, 0, 0};
-            HIP_TRY(launch_gemm(g, s));
-        }
-        HIP_TRY(launch_qkv_post_axial(v->qkv.p, ldqkv, T, (int)v->NH, (int)v->NKV, (int)v->hd,
-                                      ly.q_norm, ly.k_norm, v->cos_t.p, v->sin_t.p, v->coord.p,
-                                      v->eps, flag, s));
-        {
-            AttnArgs a{};
-            a.q = v->qkv.p;
-            a.k = v->qkv.p + v->qd;
-            a.v = v->qkv.p + v->qd + v->kd;
-            a.out = v->attn.p;
-            a.ldq = a.ldk = a.ldv = ldqkv;
-            a.ldo = v->qd;
-            a.nh = (int)v->NH;
-            a.nkv = (int)v->NKV;
-            a.hd = (int)v->hd;
-            a.window = -1;   // vision.rs:880 sliding_window: None
-            a.scale = 1.0f;  // vision.rs:881
-            a.tiles = v->tiles.p;
-            a.n_tiles = (int)b.tiles.size();
-            a.pos = v->apos.p;
-            a.rowlen = v->rowlen.p;
-            a.tokens = T;
-            a.flag = flag;
-            HIP_TRY(launch_attention(a, s));
-        }
-        {
-            GemmArgs g{v->attn.p, v->qd, ly.w_o, v->qd, v->tmp.p, H, (int)T, (int)H, (int)v->qd,
-                       EPI_STORE, 1.f, nullptr, 0, 0};
-            HIP_TRY(launch_gemm(g, s));
-        }
-        HIP_TRY(launch_resnorm(v->tmp.p, ly.ln_post_attn, v->h.p, v->h.p, ly.ln_pre_ff, v->n.p,
-                               1.0f, T, (int)H, v->eps, flag, s));
-        {
-            GemmArgs g{v->n.p, H, ly.w_gu, H, v->act.p, v->I, (int)T, (int)(2 * v->I_pad), (int)H,
-                       EPI_GEGLU, 1.f, nullptr, 0, (int)v->I};
-            HIP_TRY(launch_gemm(g, s));
-        }
-        {
-            GemmArgs g{v->act.p, v->I, ly.w_down, v->I, v->tmp.p, H, (int)T, (int)H, (int)v->I,
-                       EPI_STORE, 1.f, nullptr, 0, 0};
-            HIP_TRY(launch_gemm(g, s));
-        }
-        const float *next = l + 1 < v->L ? v->layers[(size_t)l + 1].ln_in : nullptr;
-        HIP_TRY(launch_resnorm(v->tmp.p, ly.ln_post_ff, v->h.p, v->h.p, next,
-                               next ? v->n.p : nullptr, 1.0f, T, (int)H, v->eps, flag, s));
-        if (h_hidden)
-            HIP_TRY(hipMemcpyAsync(h_hidden + (size_t)((l + 1) * T * H), v->h.p,
-                                   (size_t)(T * H) * 4, hipMemcpyDeviceToHost, s));
+    if (b.groups.size() > 1) {
+        // the second image group runs its layers on the model's second stream
+        HIP_TRY(hipEventRecord(v->ev_fork, s));
+        HIP_TRY(hipStreamWaitEvent(v->extra, v->ev_fork, 0));
+        ST_TRY(enqueue_vis_layers(v, b, b.groups[1], v->extra, nullptr));
+        ST_TRY(enqueue_vis_layers(v, b, b.groups[0], s, nullptr));
+        HIP_TRY(hipEventRecord(v->ev_join, v->extra));
+        HIP_TRY(hipStreamWaitEvent(s, v->ev_join, 0));
+    } else {
+        ST_TRY(enqueue_vis_layers(v, b, b.groups[0], s, h_hidden));
     }
 
     // pool_patches + rms_norm_rows_unscaled + embedding projection
@@ -446,7 +514,7 @@ svl_status run_vision(svl_vision_model *v, const svl_image_patches *images, int3
                       float *d_pixels, hipStream_t s, VisBatch &b, float *out_soft,
                       float *out_hidden) {
     HIP_TRY(hipSetDevice(v->device));
-    ST_TRY(prepare_images(v, images, batch, d_pixels == nullptr, b));
+    ST_TRY(prepare_images(v, images, batch, d_pixels == nullptr, b, out_hidden != nullptr));
     if (batch == 0) return SVL_OK;
     ST_TRY(ensure_axial_tables(v, b.max_coord + 1));
     ST_TRY(ensure_vis_workspace(v, b));
@@ -597,8 +665,19 @@ svl_status svl_vision_model_create(svl_ctx *ctx, const svl_vision_config *cfg, i
         ST_TRY(up(p + "self_attn.k_norm.weight", &ly.k_norm));
     }
     HIP_TRY(hipStreamCreateWithFlags(&v->stream, hipStreamNonBlocking));
+    HIP_TRY(hipStreamCreateWithFlags(&v->extra, hipStreamNonBlocking));
+    HIP_TRY(hipEventCreateWithFlags(&v->ev_fork, hipEventDisableTiming));
+    HIP_TRY(hipEventCreateWithFlags(&v->ev_join, hipEventDisableTiming));
     HIP_TRY(hipHostMalloc((void **)&v->h_flag, sizeof(int), hipHostMallocDefault));
     *out = guard.release();
+    return SVL_OK;
+}
+
+svl_status svl_vision_model_set_stream_split(svl_vision_model *model, int groups) {
+    if (!model) return fail(SVL_USAGE, "vision model is null");
+    if (groups < 1 || groups > 2) return fail(SVL_USAGE, "image groups must be 1 or 2");
+    std::lock_guard<std::mutex> lock(model->mu);
+    model->groups = groups;
     return SVL_OK;
 }
 

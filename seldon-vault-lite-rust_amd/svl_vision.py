@@ -327,6 +327,12 @@ class VisionModel:
         except Exception:
             pass
 
+    def set_stream_split(self, groups):
+        """Image groups of a batch's encoder layers on concurrent streams (1 or
+        2; results are bit-identical either way)."""
+        g = 2 if groups is True else 1 if groups is False else int(groups)
+        _check(lib().svl_vision_model_set_stream_split(self.handle, g))
+
     def forward(self, patches: ImagePatches, capture_hidden=False) -> VisionOutput:
         """vision.rs:742-959."""
         return self.forward_batch([patches], capture_hidden)[0]

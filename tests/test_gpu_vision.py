@@ -113,6 +113,28 @@ def test_batch_is_bit_identical_to_single_calls(tower_v2):
         assert np.array_equal(again[i].pooled(), batch[len(patches) - 1 - i].pooled())
 
 
+def test_image_groups_are_bit_identical(tower_v2):
+    # Batches of two or more images and 4096 or more patches run the encoder
+    # layers as two image groups on two streams: here images 0-1 (2304 + 1296
+    # patches) against images 2-3 (2304 + 576).
+    w, gpu, om = tower_v2
+    patches = [svl_synth.image_patches(1, 48, 48, seed=61)[0],
+               svl_synth.image_patches(1, 36, 36, seed=62)[0],
+               svl_synth.image_patches(1, 48, 48, seed=63)[0],
+               svl_synth.image_patches(1, 24, 24, seed=64)[0]]
+    split = gpu.forward_batch(patches)
+    gpu.set_stream_split(1)
+    try:
+        single = gpu.forward_batch(patches)
+    finally:
+        gpu.set_stream_split(2)
+    captured = gpu.forward_batch(patches, capture_hidden=True)  # one group while capturing
+    for i in range(4):
+        assert np.array_equal(split[i].pooled(), single[i].pooled()), f"image {i}"
+        assert np.array_equal(split[i].pooled(), captured[i].pooled()), f"image {i}"
+    assert np.array_equal(gpu.forward(patches[2]).pooled(), split[2].pooled())
+
+
 def test_device_resident_matches_host(tower_v2):
     import torch
     w, gpu, om = tower_v2
