@@ -598,8 +598,9 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
         return (int64_t)((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn);
     };
     // Grids that 64x64 tiles would not cover once (a few short rows): the
-    // smallest tiles, one 16x16 (or, paired, 16x64) block per wave, so each
-    // wave's MFMA chain is K / 4 (or 4 x K / 4) instructions long.
+    // smallest tiles, one 16x16 block per wave (paired: two, the x or the y
+    // half of the pair), so each wave's MFMA chain is K / 4 (2 x K / 4)
+    // instructions long.
     const bool tiny = tiles(64, 64) < 256 && a.K % 32 == 0;
     if constexpr (paired_epi<EPI>()) {
         if (tiny) {
