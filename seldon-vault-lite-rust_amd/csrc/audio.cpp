@@ -70,6 +70,7 @@ struct svl_audio_model {
     int64_t H = 0, I = 0, L = 0, NH = 0, hd = 0, K = 0, C0 = 0, C1 = 0, chunk = 0, left = 0,
             right = 0, P = 0, text_hidden = 0, context = 0, positions = 0, H_pad = 0;
     float cap = 0.f, eps = 0.f, rw = 0.f, clip = 0.f, k_scale = 0.f;
+    bool conv_implicit = false;  // layer-1 convolution as an implicit-im2col GEMM
     std::vector<float *> allocations;
     float *w_conv0 = nullptr, *ln0 = nullptr, *w_conv1 = nullptr, *ln1 = nullptr,
           *w_in = nullptr, *w_out = nullptr, *b_out = nullptr, *w_emb = nullptr;
@@ -339,7 +340,7 @@ svl_status ensure_au_workspace(svl_audio_model *m, const AuBatch &b) {
     HIP_TRY(m->mel.ensure(F * FEATURE_SIZE));
     HIP_TRY(m->mask.ensure(F));
     HIP_TRY(m->l0.ensure(T0 * FREQ0 * m->C0));
-    HIP_TRY(m->col.ensure(T * FREQ1 * 9 * m->C0));
+    if (!m->conv_implicit) HIP_TRY(m->col.ensure(T * FREQ1 * 9 * m->C0));
     HIP_TRY(m->l1.ensure(T * FREQ1 * m->C1));
     HIP_TRY(m->h.ensure(T * m->H));
     HIP_TRY(m->n.ensure(3 * T * m->H));  // three clamped copies feed the Q/K/V projection
@@ -403,13 +404,27 @@ svl_status enqueue_audio(svl_audio_model *m, const AuBatch &b, const float *d_me
     // Subsampling (audio.rs:1136-1255).
     HIP_TRY(launch_sscp_conv0(d_mel, m->mask.p, m->rows0.p, b.T0, m->w_conv0, m->ln0, (int)m->C0,
                               m->eps, m->l0.p, flag, s));
-    // layer 1: im2col, GEMM against the [C1, 9 C0] weight, LayerNorm + ReLU
-    HIP_TRY(launch_sscp_im2col(m->l0.p, m->mask0.p, m->rows1.p, T, (int)m->C0, m->col.p, s));
+    // layer 1: the 3x3 stride-2 convolution as a GEMM against the [C1, 9 C0]
+    // weight (an implicit im2col, or im2col + GEMM), then LayerNorm + ReLU
     {
         const int64_t K = 9 * m->C0;
-        GemmArgs g{m->col.p, K, m->w_conv1, K, m->l1.p, m->C1, (int)(T * FREQ1), (int)m->C1,
-                   (int)K, EPI_STORE, 1.f, nullptr, 0, 0};
-        HIP_TRY(launch_gemm(g, s));
+        if (m->conv_implicit) {
+            GemmArgs g{m->l0.p, K, m->w_conv1, K, m->l1.p, m->C1, (int)(T * FREQ1), (int)m->C1,
+                       (int)K, EPI_STORE, 1.f, nullptr, 0, 0};
+            g.conv_rows = reinterpret_cast<const int32_t *>(m->rows1.p);
+            g.conv_mask = m->mask0.p;
+            g.conv_c0 = (int)m->C0;
+            g.conv_f0 = (int)FREQ0;
+            g.conv_f1 = (int)FREQ1;
+            g.conv_a_floats = b.T0 * FREQ0 * m->C0;
+            if (!gemm_conv_ok(g)) return fail(SVL_LIMIT, "audio subsampling too large for one launch");
+            HIP_TRY(launch_gemm_conv(g, s));
+        } else {
+            HIP_TRY(launch_sscp_im2col(m->l0.p, m->mask0.p, m->rows1.p, T, (int)m->C0, m->col.p, s));
+            GemmArgs g{m->col.p, K, m->w_conv1, K, m->l1.p, m->C1, (int)(T * FREQ1), (int)m->C1,
+                       (int)K, EPI_STORE, 1.f, nullptr, 0, 0};
+            HIP_TRY(launch_gemm(g, s));
+        }
     }
     HIP_TRY(launch_sscp_ln_relu(m->l1.p, m->ln1, (int)m->C1, T * FREQ1, m->eps, flag, s));
     {
@@ -734,7 +749,19 @@ svl_status svl_audio_model_create(svl_ctx *ctx, const svl_audio_config *cfg, int
     const std::string sp = "audio_tower.subsample_conv_projection.";
     ST_TRY(up(sp + "layer0.conv.weight", &m->w_conv0));
     ST_TRY(up(sp + "layer0.norm.weight", &m->ln0));
-    ST_TRY(up(sp + "layer1.conv.weight", &m->w_conv1));
+    // Layer-1 convolution weight [C1][C0][3][3]; the implicit-im2col GEMM
+    // (C0 % 32 == 0) takes it tap-major, [C1][3 x 3][C0].
+    ST_TRY(decode_named(by_name, sp + "layer1.conv.weight", a));
+    m->conv_implicit = m->C0 % 32 == 0;
+    if (m->conv_implicit) {
+        b2.assign(a.size(), 0.f);
+        for (int64_t o = 0; o < m->C1; ++o)
+            for (int64_t c = 0; c < m->C0; ++c)
+                for (int64_t t = 0; t < 9; ++t)
+                    b2[(size_t)((o * 9 + t) * m->C0 + c)] = a[(size_t)((o * m->C0 + c) * 9 + t)];
+        a.swap(b2);
+    }
+    ST_TRY(upload_owned(m->allocations, a.data(), a.size(), &m->w_conv1));
     ST_TRY(up(sp + "layer1.norm.weight", &m->ln1));
     ST_TRY(up(sp + "input_proj_linear.weight", &m->w_in));
     ST_TRY(up("audio_tower.output_proj.weight", &m->w_out));

@@ -119,6 +119,8 @@ hipError_t launch_sscp_conv0(const float *mel, const uint8_t *mask, const SscpRo
 }
 
 // ---- subsampling convolution 1 as im2col + GEMM ---------------------------
+// (Configurations with C0 % 32 == 0 take the implicit-im2col GEMM instead,
+// launch_gemm_conv, which reads the taps straight from the layer-0 output.)
 // col[(r * 32 + f) * 9 C0 + ic * 9 + kt * 3 + kf] = layer0 input tap, zero
 // where the tap is outside the clip, masked or outside the 64 frequencies:
 // the k order of the layer-1 weight [C1][C0][3][3], so the GEMM against it

@@ -320,7 +320,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
 // Direct-to-LDS variant; requires K % BK == 0 and 16-byte aligned rows. NS
 // LDS stages: NS - 1 slices are in flight while one is consumed. WMW waves
 // along M, 4 / WMW along N.
-template <int BM, int BN, int BK, int EPI, int MINB, int NS, int WMW>
+template <int BM, int BN, int BK, int EPI, int MINB, int NS, int WMW, bool CONV = false>
 __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m, int tiles_n) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int WNW = 4 / WMW;                // waves along N
@@ -381,19 +381,46 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     const int seg = uniform(clip_segment(p, n0));
 
     // Operand windows: [valid rows of this tile] x lda floats; reads past
-    // the last valid row return zero.
-    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)uniform(p.A + (int64_t)seg * p.a_seg + (int64_t)m0 * p.lda), (short)0,
-        uniform((int)(min(BM, M - m0) * p.lda * 4)), 0x00020000);
+    // the last valid row return zero. (Implicit im2col: the whole layer-0
+    // output, every lane's offset computed per tap.)
+    const __amdgpu_buffer_rsrc_t ra = CONV
+        ? __builtin_amdgcn_make_buffer_rsrc((void *)uniform(p.A), (short)0,
+                                            uniform((int)(p.conv_a_floats * 4)), 0x00020000)
+        : __builtin_amdgcn_make_buffer_rsrc(
+              (void *)uniform(p.A + (int64_t)seg * p.a_seg + (int64_t)m0 * p.lda), (short)0,
+              uniform((int)(min(BM, M - m0) * p.lda * 4)), 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         (void *)uniform(p.W + (int64_t)n0 * p.ldw), (short)0,
         uniform((int)(min(BN, N - n0) * p.ldw * 4)), 0x00020000);
     int a_off[A_CH], w_off[W_CH];
+    // implicit im2col: per A row of this lane, the layer-0 float offset of
+    // tap (0, 0) channel 0 and the valid kt (bits 0-2) and kf (bits 3-5)
+    int a_taps[CONV ? A_CH : 1];
 #pragma unroll
     for (int q = 0; q < A_CH; ++q) {
         const int row = (wave * A_CH + q) * RPK + lane / CPR;
         const int c = (lane % CPR) ^ ((row / RPL) % SWZ);
-        a_off[q] = (row * (int)p.lda + 4 * c) * 4;
+        if constexpr (CONV) {
+            a_off[q] = 0;
+            a_taps[q] = 0;
+            const int m = m0 + row;
+            if (m < M) {
+                const int r = m / p.conv_f1, f = m - r * p.conv_f1;
+                const int base = p.conv_rows[3 * r], t = p.conv_rows[3 * r + 1],
+                          len = p.conv_rows[3 * r + 2];
+                int bits = 0;
+#pragma unroll
+                for (int k = 0; k < 3; ++k) {
+                    const int it = 2 * t + k - 1, iff = 2 * f + k - 1;
+                    if (it >= 0 && it < len && p.conv_mask[base + it]) bits |= 1 << k;
+                    if (iff >= 0 && iff < p.conv_f0) bits |= 8 << k;
+                }
+                a_off[q] = ((base + 2 * t - 1) * p.conv_f0 + 2 * f - 1) * p.conv_c0 + 4 * c;
+                a_taps[q] = bits;
+            }
+        } else {
+            a_off[q] = (row * (int)p.lda + 4 * c) * 4;
+        }
     }
 #pragma unroll
     for (int q = 0; q < W_CH; ++q) {
@@ -404,11 +431,26 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     auto issue = [&](auto st, int k0) {
         float *as = stage_a(st);
         float *ws = stage_w(st);
+        if constexpr (CONV) {
+            // a K slice lies within one tap: k0 = tap * C0 + channel offset
+            const int tap = k0 / p.conv_c0, kt = tap / 3, kf = tap - 3 * kt;
+            const int delta = (kt * p.conv_f0 + kf) * p.conv_c0 + (k0 - tap * p.conv_c0);
 #pragma unroll
-        for (int q = 0; q < A_CH; ++q)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                ra, (__attribute__((address_space(3))) void *)&as[(wave * A_CH + q) * 256], 16,
-                a_off[q], k0 * 4, 0, 0);
+            for (int q = 0; q < A_CH; ++q) {
+                const bool ok = (a_taps[q] >> kt & 1) && (a_taps[q] >> (3 + kf) & 1);
+                // a tap outside the clip, the mask or the frequencies reads
+                // past the window, as zero
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ra, (__attribute__((address_space(3))) void *)&as[(wave * A_CH + q) * 256], 16,
+                    ok ? (a_off[q] + delta) * 4 : 0x7FFFFFF0, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < A_CH; ++q)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ra, (__attribute__((address_space(3))) void *)&as[(wave * A_CH + q) * 256], 16,
+                    a_off[q], k0 * 4, 0, 0);
+        }
 #pragma unroll
         for (int q = 0; q < W_CH; ++q)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -538,11 +580,11 @@ __global__ __launch_bounds__(256) void gemm_nt_simple(GemmArgs p) {
     }
 }
 
-template <int BM, int BN, int BK, int EPI, int MINB, int NS, int WMW = 2>
+template <int BM, int BN, int BK, int EPI, int MINB, int NS, int WMW = 2, bool CONV = false>
 static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
     const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
-    hipLaunchKernelGGL((gemm_nt_dma<BM, BN, BK, EPI, MINB, NS, WMW>), dim3(tm * tn), dim3(256), 0,
-                       s, a, tm, tn);
+    hipLaunchKernelGGL((gemm_nt_dma<BM, BN, BK, EPI, MINB, NS, WMW, CONV>), dim3(tm * tn),
+                       dim3(256), 0, s, a, tm, tn);
     return hipGetLastError();
 }
 
@@ -703,6 +745,26 @@ hipError_t launch_gemm(const GemmArgs &a, hipStream_t s) {
         case EPI_CLIP_GLU: return launch_mfma<128, 128, EPI_CLIP_GLU>(a, s);
     }
     return hipErrorInvalidValue;
+}
+
+// The implicit-im2col convolution: 128x32 tiles (the layer-1 GEMM has 8 to
+// 32 output channels) or 64x64, 32-wide K slices that each lie within one
+// tap. No column matrix is written: each lane's DMA reads its 16 bytes of the
+// layer-0 output at the tap's offset, and taps outside the input read the
+// zeros past the buffer window.
+bool gemm_conv_ok(const GemmArgs &a) {
+    return a.epi == EPI_STORE && a.conv_rows && a.conv_mask && a.conv_c0 > 0 &&
+           a.conv_c0 % 32 == 0 && a.K == 9 * a.conv_c0 && a.conv_f0 > 0 && a.conv_f1 > 0 &&
+           a.conv_a_floats > 0 && a.conv_a_floats * 4 < 0x7FFFFFF0 && a.ldw % 4 == 0 &&
+           (uintptr_t)a.A % 16 == 0 && (uintptr_t)a.W % 16 == 0 &&
+           (int64_t)128 * a.ldw * 4 < INT32_MAX;
+}
+
+hipError_t launch_gemm_conv(const GemmArgs &a, hipStream_t s) {
+    if (a.M <= 0 || a.N <= 0) return hipSuccess;
+    if (!gemm_conv_ok(a)) return hipErrorInvalidValue;
+    if (a.N <= 32) return launch_dma<128, 32, 32, EPI_STORE, 4, 2, 4, true>(a, s);
+    return launch_dma<64, 64, 32, EPI_STORE, 4, 2, 2, true>(a, s);
 }
 
 hipError_t launch_gemm_simple(const GemmArgs &a, hipStream_t s) {

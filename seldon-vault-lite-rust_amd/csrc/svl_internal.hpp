@@ -54,9 +54,25 @@ struct GemmArgs {
     // EPI_CLIP_SILU: bounds of the next clipped linear's input, applied as
     // the result is stored (the identity by default)
     float post_lo = -__builtin_huge_valf(), post_hi = __builtin_huge_valf();
+    // launch_gemm_conv: implicit im2col for the audio subsampling's layer-1
+    // 3x3 stride-2 convolution. A is the layer-0 output [rows0, conv_f0,
+    // conv_c0]; row m of the virtual A is output position (r, f) = (m /
+    // conv_f1, m % conv_f1) of layer-1 row conv_rows[r] = {base, t, len}, and
+    // its column k = tap * conv_c0 + c (tap = 3 kt + kf) holds layer-0 row
+    // base + 2 t + kt - 1, frequency 2 f + kf - 1, channel c, or zero outside
+    // the clip, on a masked row (conv_mask[base + row] == 0) or outside the
+    // frequencies. W is [N][9][conv_c0].
+    const int32_t *conv_rows = nullptr;
+    const uint8_t *conv_mask = nullptr;
+    int conv_c0 = 0, conv_f0 = 0, conv_f1 = 0;
+    int64_t conv_a_floats = 0;  // floats of the layer-0 output (A's window)
 };
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
+// True when launch_gemm_conv can take the convolution (conv_c0 % 32 == 0,
+// windows below 2 GiB); otherwise the caller runs im2col and launch_gemm.
+bool gemm_conv_ok(const GemmArgs &a);
+hipError_t launch_gemm_conv(const GemmArgs &a, hipStream_t s);
 // Plain scalar-FMA fallback for shapes the MFMA kernel does not take
 // (K % 4 != 0); same epilogues.
 hipError_t launch_gemm_simple(const GemmArgs &a, hipStream_t s);
@@ -191,6 +207,7 @@ struct SscpRow {
     int32_t t;
     int32_t len;
 };
+static_assert(sizeof(SscpRow) == 3 * sizeof(int32_t), "GemmArgs::conv_rows reads SscpRow triplets");
 
 // Mel [frames, 128] -> layer 0 [rows, 64, C0] (conv 3x3 stride 2 pad 1,
 // masked frames skipped, LayerNorm + ReLU). C0 <= 512.
