@@ -249,8 +249,20 @@ constexpr int attn_dim_split() { return HD > 256 ? HD / 256 : 1; }
 // MFMAs and HD / 4 P.V MFMAs. With OS > 1 the OS waves of a group share one
 // 16-vector group: each computes all the scores (the same instructions in the
 // same order, so the same bits), runs the same softmax, and applies P to its
-// own HD / OS dims of V. A wave's chain shrinks to HD / 4 + HD / (4 OS) MFMAs
-// per tile, and every output element is the sum it is with OS = 1.
+// own HD / OS dims of V. The scores' NP partial sums are split over the OS
+// waves (NP / OS chains each) and meet through LDS, so a wave's chain is
+// HD / (4 OS) + HD / (4 OS) MFMAs per tile, and every score and output element
+// is the sum it is with OS = 1.
+
+// Every score is the sum of NP partial dot products over consecutive blocks
+// of HD / NP dims (dims 0 .. HD / NP - 1 first), each a chain of HD / (4 NP)
+// MFMAs from zero, folded left to right: the same bits whether one wave runs
+// all NP chains or the OS waves of a group run NP / OS each and meet through
+// LDS. NP depends on the head dim only (head dims above 256 split their dims
+// over waves instead, with the partial sums of those waves folded the same
+// way).
+template <int HD>
+constexpr int attn_score_parts() { return HD == 256 ? 4 : HD == 128 ? 2 : 1; }
 
 template <int HD, int WAVES, int NS>
 constexpr int attn_min_blocks() { return HD <= 256 && WAVES == 4 && NS == 2 ? 2 : 1; }
@@ -272,6 +284,10 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES, NS>())) voi
     constexpr int HDW = HD / DS;              // head dims per wave (scores)
     constexpr int HDO = HDW / OS;             // output dims per wave
     constexpr int NKB = KT / 16;              // 16-key blocks per tile
+    constexpr int NP = DS > 1 ? 1 : attn_score_parts<HD>();  // partial sums per score
+    constexpr int PPW = NP / OS;              // partial sums per wave
+    constexpr int CPW = HDW / 16 / OS;        // 16-dim Q chunks per wave
+    constexpr int CPB = CPW / PPW;            // chunks per partial sum
     constexpr int VPW = 16 * WAVES / (DS * OS);  // query vectors per workgroup
     constexpr int SPLIT = 128 / VPW;          // workgroups per 128-vector work item
     constexpr int INSTR_PER_WAVE = KT * HD / 256 / WAVES;  // 1 KB DMA instructions per operand
@@ -279,6 +295,7 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES, NS>())) voi
     static_assert(WAVES == 1 || WAVES == 2 || WAVES == 4 || WAVES == 8, "waves");
     static_assert(WAVES % (DS * OS) == 0 && 128 % VPW == 0, "vector groups");
     static_assert(OS == 1 || (DS == 1 && HDO % 64 == 0), "output split");
+    static_assert(NP % OS == 0 && CPW % PPW == 0 && CPB >= 1, "score partial sums");
     static_assert(KT % 16 == 0 && INSTR_PER_WAVE >= 1 && (KT * HD / 256) % WAVES == 0, "key tile");
     static_assert(NS >= 2 && NS <= 4 && (NS - 2) * 2 * INSTR_PER_WAVE < 64, "pipeline depth");
     // One LDS object per stage, addressed with compile-time stage indices:
@@ -300,8 +317,8 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES, NS>())) voi
         else if constexpr (i == 2) return Vs2;
         else return Vs3;
     };
-    // partial scores of each wave (DS > 1 only)
-    __shared__ f32x4 Sx[DS > 1 ? WAVES * NKB * 64 : 1];
+    // partial scores: of each wave (DS > 1), of each group's NP blocks (OS > 1)
+    __shared__ f32x4 Sx[DS > 1 ? WAVES * NKB * 64 : OS > 1 ? WAVES / OS * NP * NKB * 64 : 1];
 
     const int wg = xcd_chunks ? xcd_chunk((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
     const AttnTile tile = p.tiles[wg / SPLIT];
@@ -319,15 +336,18 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES, NS>())) voi
     const int vq = vvalid ? v : nvec - 1;
     const int qpos = vq / G;
     const int qhead = tile.kvh * G + (vq - qpos * G);
-    const float *qrow = p.q + (int64_t)(tile.tok0 + qpos) * p.ldq + qhead * HD + dpart * HDW;
+    // this wave's score dims: block dpart of the head, and within it the
+    // OS-th part opart (the wave's NP / OS partial sums)
+    const int sdim0 = dpart * HDW + opart * 16 * CPW;
+    const float *qrow = p.q + (int64_t)(tile.tok0 + qpos) * p.ldq + qhead * HD + sdim0;
 
     // Query fragments pre-scaled by scale * log2(e): S^T comes out in log2
     // units. Fragment c holds dims 16 c + 4 (lane / 16) .. + 3 of the wave's
-    // block.
+    // score dims.
     const float scale2 = p.scale * 1.4426950408889634f;
-    f32x4 qf[HDW / 16];
+    f32x4 qf[CPW];
 #pragma unroll
-    for (int c = 0; c < HDW / 16; ++c) qf[c] = *(const f32x4 *)(qrow + 16 * c + 4 * g) * scale2;
+    for (int c = 0; c < CPW; ++c) qf[c] = *(const f32x4 *)(qrow + 16 * c + 4 * g) * scale2;
 
     f32x4 o[HDO / 16];
 #pragma unroll
@@ -404,25 +424,26 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES, NS>())) voi
 
         // S^T for keys kb * 16 + 4 (lane / 16) + r (register r of block kb)
         // and query vector lane % 16. K row kb * 16 + l16 holds dim chunk
-        // ch = 4 c + g (of the wave's dim block: ch + HDW / 4 * dpart) at
-        // slot ch ^ l16.
+        // ch = 4 c + g (of the wave's score dims: ch + sdim0 / 4) at slot
+        // ch ^ l16. Chunk c adds to partial sum c / CPB.
         // The fragments of chunk c + 1 are read while chunk c's MFMAs run,
         // and the two key blocks' chains alternate.
         const float *kb0 = kstage(st) + l16 * HD;
-        const int ch0 = dpart * (HDW / 4);
-        f32x4 s[NKB], kf[NKB];
+        const int ch0 = sdim0 / 4;
+        f32x4 sp[PPW][NKB], kf[NKB];
 #pragma unroll
         for (int kb = 0; kb < NKB; ++kb) {
-            s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < PPW; ++i) sp[i][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
             kf[kb] = *(const f32x4 *)(kb0 + kb * 16 * HD + 4 * ((ch0 + g) ^ l16));
         }
 #pragma unroll
-        for (int c = 0; c < HDW / 16; ++c) {
+        for (int c = 0; c < CPW; ++c) {
             f32x4 nf[NKB];
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) {
                 nf[kb] = kf[kb];
-                if (c + 1 < HDW / 16)
+                if (c + 1 < CPW)
                     nf[kb] = *(const f32x4 *)(kb0 + kb * 16 * HD +
                                               4 * ((ch0 + 4 * (c + 1) + g) ^ l16));
             }
@@ -432,15 +453,17 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES, NS>())) voi
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int kb = 0; kb < NKB; ++kb)
-                    s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kb][j], qf[c][j], s[kb], 0, 0, 0);
+                    sp[c / CPB][kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        kf[kb][j], qf[c][j], sp[c / CPB][kb], 0, 0, 0);
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) kf[kb] = nf[kb];
         }
+        f32x4 s[NKB];
         if constexpr (DS > 1) {
             // the partial sums of the group's waves meet in LDS; the barrier
             // at the top of the next tile keeps them until all are read
 #pragma unroll
-            for (int kb = 0; kb < NKB; ++kb) Sx[(wave * NKB + kb) * 64 + lane] = s[kb];
+            for (int kb = 0; kb < NKB; ++kb) Sx[(wave * NKB + kb) * 64 + lane] = sp[0][kb];
             __syncthreads();
             const int w0 = group * DS;
 #pragma unroll
@@ -448,6 +471,30 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES, NS>())) voi
                 f32x4 t = Sx[(w0 * NKB + kb) * 64 + lane];
 #pragma unroll
                 for (int d = 1; d < DS; ++d) t = t + Sx[((w0 + d) * NKB + kb) * 64 + lane];
+                s[kb] = t;
+            }
+        } else if constexpr (OS > 1) {
+            // the group's NP partial sums meet in LDS (same fold as below);
+            // the barrier at the top of the next tile keeps them until read
+#pragma unroll
+            for (int i = 0; i < PPW; ++i)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb)
+                    Sx[((group * NP + opart * PPW + i) * NKB + kb) * 64 + lane] = sp[i][kb];
+            __syncthreads();
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                f32x4 t = Sx[(group * NP * NKB + kb) * 64 + lane];
+#pragma unroll
+                for (int i = 1; i < NP; ++i) t = t + Sx[((group * NP + i) * NKB + kb) * 64 + lane];
+                s[kb] = t;
+            }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) {
+                f32x4 t = sp[0][kb];
+#pragma unroll
+                for (int i = 1; i < NP; ++i) t = t + sp[i][kb];
                 s[kb] = t;
             }
         }
