@@ -247,12 +247,11 @@ constexpr int attn_dim_split() { return HD > 256 ? HD / 256 : 1; }
 // Short grids (a few rows of a few hundred tokens) leave most SIMDs idle, and
 // each wave's time is its dependent MFMA work: per 16-key tile, HD / 4 score
 // MFMAs and HD / 4 P.V MFMAs. With OS > 1 the OS waves of a group share one
-// 16-vector group: each computes all the scores (the same instructions in the
-// same order, so the same bits), runs the same softmax, and applies P to its
-// own HD / OS dims of V. The scores' NP partial sums are split over the OS
-// waves (NP / OS chains each) and meet through LDS, so a wave's chain is
-// HD / (4 OS) + HD / (4 OS) MFMAs per tile, and every score and output element
-// is the sum it is with OS = 1.
+// 16-vector group: the scores' NP partial sums (below) are split over them
+// (NP / OS chains each) and meet through LDS, every wave then holds the same
+// score bits and runs the same softmax, and each applies P to its own HD / OS
+// dims of V. A wave's chain is HD / (4 OS) + HD / (4 OS) MFMAs per tile, and
+// every score and output element is the sum it is with OS = 1.
 
 // Every score is the sum of NP partial dot products over consecutive blocks
 // of HD / NP dims (dims 0 .. HD / NP - 1 first), each a chain of HD / (4 NP)
