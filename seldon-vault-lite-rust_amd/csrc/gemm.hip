@@ -488,14 +488,14 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
             issue(std::integral_constant<int, (cur + NS - 1) % NS>{}, (kt + NS - 1) * BK);
         const float *as = stage_a(st) + (wm * WTM + l16) * BK;
         const float *ws = stage_w(st) + (wn * WTN + l16) * BK;
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 16) {
+        auto frags = [&](int kk, f32x4 (&a)[TM], f32x4 (&b)[TN]) {
             const int pos = ((kk >> 2) + g) ^ sw;
-            f32x4 a[TM], b[TN];
 #pragma unroll
             for (int i = 0; i < TM; ++i) a[i] = *(const f32x4 *)(as + i * 16 * BK + 4 * pos);
 #pragma unroll
             for (int j = 0; j < TN; ++j) b[j] = *(const f32x4 *)(ws + j * 16 * BK + 4 * pos);
+        };
+        auto mfmas = [&](const f32x4 (&a)[TM], const f32x4 (&b)[TN]) {
 #pragma unroll
             for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -504,6 +504,34 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
                     for (int j = 0; j < TN; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[j][s], a[i][s],
                                                                          acc[i][j], 0, 0, 0);
+        };
+        if constexpr (TM * TN <= 2) {
+            // One or two accumulator chains per wave (the small grids, one
+            // wave per SIMD): the fragments of step kk + 16 are read while
+            // step kk's MFMAs run, so the LDS latency is not added to every
+            // step of the dependent chain.
+            f32x4 a[TM], b[TN];
+            frags(0, a, b);
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += 16) {
+                f32x4 na[TM], nb[TN];
+                if (kk + 16 < BK) frags(kk + 16, na, nb);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(a, b);
+                if (kk + 16 < BK) {
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) a[i] = na[i];
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) b[j] = nb[j];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += 16) {
+                f32x4 a[TM], b[TN];
+                frags(kk, a, b);
+                mfmas(a, b);
+            }
         }
     };
     for (int kt = 0; kt < nk; kt += NS) {
