@@ -428,6 +428,30 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
         const int c = (lane % CPR) ^ ((row / RPL) % SWZ);
         w_off[q] = (row * (int)p.ldw + 4 * c) * 4;
     }
+    // DMA instruction q of a slice: A for q < A_CH, else W (q - A_CH)
+    auto issue_one = [&](auto st, int k0, int q) {
+        float *as = stage_a(st);
+        float *ws = stage_w(st);
+        if (q < A_CH) {
+            if constexpr (CONV) {
+                const int tap = k0 / p.conv_c0, kt = tap / 3, kf = tap - 3 * kt;
+                const int delta = (kt * p.conv_f0 + kf) * p.conv_c0 + (k0 - tap * p.conv_c0);
+                const bool ok = (a_taps[q] >> kt & 1) && (a_taps[q] >> (3 + kf) & 1);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ra, (__attribute__((address_space(3))) void *)&as[(wave * A_CH + q) * 256], 16,
+                    ok ? (a_off[q] + delta) * 4 : 0x7FFFFFF0, 0, 0, 0);
+            } else {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ra, (__attribute__((address_space(3))) void *)&as[(wave * A_CH + q) * 256], 16,
+                    a_off[q], k0 * 4, 0, 0);
+            }
+        } else {
+            const int r = q - A_CH;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rw, (__attribute__((address_space(3))) void *)&ws[(wave * W_CH + r) * 256], 16,
+                w_off[r], k0 * 4, 0, 0);
+        }
+    };
     auto issue = [&](auto st, int k0) {
         float *as = stage_a(st);
         float *ws = stage_w(st);
@@ -484,8 +508,14 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
         if (kt + NS - 2 < nk) wait_vmcnt<(NS - 2) * (A_CH + W_CH)>();
         else wait_vmcnt<0>();
         __syncthreads();   // ... and every wave's; slice kt-1 is no longer read
-        if (kt + NS - 1 < nk)
-            issue(std::integral_constant<int, (cur + NS - 1) % NS>{}, (kt + NS - 1) * BK);
+        constexpr bool CHAIN = TM * TN <= 2;  // one or two accumulator chains per wave
+        // several workgroups per CU: spread the next slice's DMA issue over
+        // the steps (below)
+        constexpr bool SPREAD = CHAIN && MINB >= 2;
+        using NEXT = std::integral_constant<int, (cur + NS - 1) % NS>;
+        const bool refill = kt + NS - 1 < nk;
+        if constexpr (!SPREAD)
+            if (refill) issue(NEXT{}, (kt + NS - 1) * BK);
         const float *as = stage_a(st) + (wm * WTM + l16) * BK;
         const float *ws = stage_w(st) + (wn * WTN + l16) * BK;
         auto frags = [&](int kk, f32x4 (&a)[TM], f32x4 (&b)[TN]) {
@@ -495,21 +525,30 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
 #pragma unroll
             for (int j = 0; j < TN; ++j) b[j] = *(const f32x4 *)(ws + j * 16 * BK + 4 * pos);
         };
-        auto mfmas = [&](const f32x4 (&a)[TM], const f32x4 (&b)[TN]) {
+        auto mfmas = [&](const f32x4 (&a)[TM], const f32x4 (&b)[TN], auto &&mid) {
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
+            for (int s = 0; s < 4; ++s) {
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[j][s], a[i][s],
                                                                          acc[i][j], 0, 0, 0);
+                if (s == 0) mid();
+            }
         };
-        if constexpr (TM * TN <= 2) {
-            // One or two accumulator chains per wave (the small grids, one
-            // wave per SIMD): the fragments of step kk + 16 are read while
-            // step kk's MFMAs run, so the LDS latency is not added to every
-            // step of the dependent chain.
+        if constexpr (CHAIN) {
+            // One or two accumulator chains per wave (the small and middle
+            // grids): the fragments of step kk + 16 are read while step kk's
+            // MFMAs run, so the LDS latency is not added to every step of the
+            // dependent chain. With several workgroups per CU the next
+            // slice's DMA instructions are also spread over the steps, each
+            // issued behind an MFMA, rather than all issued before the first
+            // (each takes tens of cycles to issue, and the wave issues in
+            // order): 3 % on 64x32 tiles. With one workgroup per CU (the
+            // 32x32 and 32x64 tiles of a few short rows) that took 6.7 to
+            // 7.8 us at 128 x 768 x 768, so there the slice is issued first.
+            constexpr int NDMA = A_CH + W_CH, NSTEP = BK / 16;
             f32x4 a[TM], b[TN];
             frags(0, a, b);
 #pragma unroll
@@ -517,7 +556,15 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
                 f32x4 na[TM], nb[TN];
                 if (kk + 16 < BK) frags(kk + 16, na, nb);
                 __builtin_amdgcn_sched_barrier(0);
-                mfmas(a, b);
+                const int t = kk / 16;
+                mfmas(a, b, [&] {
+                    if (SPREAD && refill) {
+#pragma unroll
+                        for (int q = 0; q < NDMA; ++q)
+                            if (q * NSTEP / NDMA == t) issue_one(NEXT{}, (kt + NS - 1) * BK, q);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                });
                 if (kk + 16 < BK) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i) a[i] = na[i];
@@ -530,7 +577,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
             for (int kk = 0; kk < BK; kk += 16) {
                 f32x4 a[TM], b[TN];
                 frags(kk, a, b);
-                mfmas(a, b);
+                mfmas(a, b, [] {});
             }
         }
     };
