@@ -151,6 +151,29 @@ def test_long_context_batch_is_batch_invariant():
         assert np.isfinite(e).all() and abs(float(e.astype(np.float64) @ e) - 1.0) < 1e-5
 
 
+def test_longest_row_matches_oracle():
+    # A row of 8192 tokens, the most the reference accepts (text.rs:188-202),
+    # beside a short row, on a narrow two-layer model (hidden 128, 2 q heads
+    # sharing one KV head of dim 64, so the oracle finishes in seconds): the
+    # sliding layer cuts every window of the long row, the full layer scores
+    # 8192 x 8192 keys per head. One token more is LimitExceeded.
+    cfg = svl_synth.config_a(layers=2, vocab=4096)
+    cfg.update(hidden_size=128, intermediate_size=256, num_attention_heads=2,
+               num_key_value_heads=1, head_dim=64, hidden_size_per_layer_input=32,
+               embedding_dim=128)
+    w = svl_synth.weights(cfg, seed=5)
+    rows = svl_synth.token_rows(4096, [8192, 77], seed=6)
+    m = model(cfg, w)
+    got = m.forward_batch(rows)
+    ref = O.OracleTextModel(cfg, w).forward_rows(rows)
+    for i, (g_, r_) in enumerate(zip(got, ref)):
+        assert_embedding_parity(g_.normalized(), r_["normalized"], f"row {i} len {len(rows[i])}")
+    assert m.forward(rows[0]).normalized().tobytes() == got[0].normalized().tobytes()
+    with pytest.raises(S.SvlError) as e:
+        m.forward(np.concatenate([rows[0], rows[1][:1]]))
+    assert e.value.kind == "LimitExceeded"
+
+
 def test_shape_b_manifest_shape_matches_oracle():
     # 2 KV heads on sliding layers, 1 KV head of head_dim 512 on the full layer.
     cfg = svl_synth.config_b(layers=6, vocab=4096)
