@@ -459,6 +459,8 @@ def search_leg(dev, steps, cpu_sample=True):
     batch_ms = timed(lambda: ix.rank_device(dq.data_ptr(), nq, d, limit=k), steps)
     one_ms = timed(lambda: ix.rank_device(dq.data_ptr(), 1, d, limit=k), steps)
     flops = 2.0 * n * d * nq
+    # the FP64 matrix rate this device sustains on register-only MFMA chains
+    fp64_peak = dev.measure_fp64_peak()
     cpu = None
     if cpu_sample:
         from oracle import oracle as O
@@ -476,6 +478,8 @@ def search_leg(dev, steps, cpu_sample=True):
             "one_query_p50_ms": round(one_ms, 3),
             "f64_tflops_wall": round(flops / (batch_ms * 1e-3) / 1e12, 2),
             "frac_of_fp64_peak_wall": round(flops / (batch_ms * 1e-3) / 1e12 / PEAK_FP64_TFLOPS, 4),
+            "measured_fp64_mfma_tflops": round(fp64_peak, 2),
+            "frac_of_measured_fp64_wall": round(flops / (batch_ms * 1e-3) / 1e12 / fp64_peak, 4),
             "cpu_baseline": cpu, "steps": steps}
 
 

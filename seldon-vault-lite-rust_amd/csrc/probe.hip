@@ -5,7 +5,10 @@
 //    v_mfma_f32_32x32x2_f32 chains in two waves per SIMD (fewer chains or
 //    more waves leave the 16x16x4 pipe partly idle); the faster is reported;
 //  * HBM bandwidth: a copy of 1 GiB into another 1 GiB, one float4 per
-//    thread over a full grid (bytes read + bytes written per second).
+//    thread over a full grid (bytes read + bytes written per second);
+//  * FP64 matrix rate (probe_fp64_peak): eight v_mfma_f64_16x16x4f64 chains
+//    in each of four waves per SIMD (one wave per SIMD reaches three
+//    quarters of that; more chains per wave change nothing).
 // Each is timed with HIP events over several launches after a warm-up; the
 // best launch is reported.
 #include "svl_internal.hpp"
@@ -46,6 +49,24 @@ __global__ __launch_bounds__(256) void probe_mfma32_kernel(float *sink, int iter
 #pragma unroll
     for (int c = 0; c < CHAINS; ++c) s += acc[c][0] + acc[c][15];
     if (s == -1.f) sink[blockIdx.x] = s;
+}
+
+__global__ __launch_bounds__(256) void probe_mfma_f64_kernel(double *sink, int iters) {
+    typedef double f64x4 __attribute__((ext_vector_type(4)));
+    constexpr int CHAINS = 8;
+    f64x4 acc[CHAINS];
+#pragma unroll
+    for (int c = 0; c < CHAINS; ++c) acc[c] = f64x4{0.0, 0.0, 0.0, 0.0};
+    const double a = 1e-3 * (double)(threadIdx.x & 63), b = 0.5;
+    for (int i = 0; i < iters; ++i) {
+#pragma unroll
+        for (int c = 0; c < CHAINS; ++c)
+            acc[c] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[c], 0, 0, 0);
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int c = 0; c < CHAINS; ++c) s += acc[c][0] + acc[c][3];
+    if (s == -1.0) sink[blockIdx.x] = s;  // never true; keeps the chains live
 }
 
 __global__ __launch_bounds__(256) void probe_copy_kernel(const f32x4 *__restrict__ src,
@@ -121,6 +142,29 @@ hipError_t probe_peaks(double *fp32_mfma_tflops, double *hbm_copy_gbs) {
     (void)hipFree(sink);
     (void)hipFree(a);
     (void)hipFree(b);
+    (void)hipStreamDestroy(s);
+    return e;
+}
+
+hipError_t probe_fp64_peak(double *fp64_mfma_tflops) {
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    hipStream_t s = nullptr;
+    if ((e = hipStreamCreate(&s)) != hipSuccess) return e;
+    double *sink = nullptr;
+    const int iters = 1500;  // about 2 ms per launch
+    float ms = 0.f;
+    e = hipMalloc((void **)&sink, (size_t)cus * 4 * sizeof(double));
+    if (e == hipSuccess)  // four workgroups of four waves per CU: four waves per SIMD
+        e = best_ms([&] {
+            hipLaunchKernelGGL(probe_mfma_f64_kernel, dim3(cus * 4), dim3(256), 0, s, sink, iters);
+        }, 3, s, &ms);
+    if (e == hipSuccess)
+        *fp64_mfma_tflops = (double)cus * 4 * 4 * iters * 8 * (2.0 * 16 * 16 * 4) / (ms * 1e-3) / 1e12;
+    (void)hipStreamSynchronize(s);
+    (void)hipFree(sink);
     (void)hipStreamDestroy(s);
     return e;
 }

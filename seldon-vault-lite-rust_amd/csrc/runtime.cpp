@@ -1128,6 +1128,14 @@ svl_status svl_measure_peaks(svl_ctx *ctx, double *fp32_mfma_tflops, double *hbm
     return SVL_OK;
 }
 
+svl_status svl_measure_fp64_peak(svl_ctx *ctx, double *fp64_mfma_tflops) {
+    if (!ctx || !fp64_mfma_tflops) return fail(SVL_USAGE, "null argument");
+    HIP_TRY(hipSetDevice(ctx->device));
+    const hipError_t e = probe_fp64_peak(fp64_mfma_tflops);
+    if (e != hipSuccess) return fail(SVL_DEVICE, "FP64 peak probe: %s", hipGetErrorString(e));
+    return SVL_OK;
+}
+
 svl_status svl_text_embed_ids(svl_text_model *m, const uint32_t *ids, int64_t n,
                               int64_t dimension, float *out) {
     if (!m || !out) return fail(SVL_USAGE, "model and output are required");

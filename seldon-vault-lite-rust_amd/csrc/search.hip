@@ -127,6 +127,140 @@ __global__ __launch_bounds__(256) void cosine_keys_kernel(
     }
 }
 
+// The same keys on the FP64 matrix cores, for query blocks of QB = 16 NQB
+// queries (16, 32 or 64) and dimensions that are a multiple of 4.
+// v_mfma_f64_16x16x4f64 adds its four products to the accumulator one after
+// another in k order, rounding each sum (checked bit for bit on a million
+// random outputs against a chain of FMAs; the product of two floats is exact
+// in double, so only the order of the additions can matter). Instruction s of
+// a staged slice takes dims d0 + 4s .. d0 + 4s + 3 as k = 0 .. 3, so every
+// score is still the sum over d = 0, 1, ..., D - 1 in that order, bit for bit.
+//  * A operand = queries: lane l holds query l % 16 at dim 4s + l / 16; B
+//    operand = chunks: lane l holds chunk l % 16 at the same dim. Both are
+//    staged in LDS as floats (queries from a d-major float copy) and widened
+//    on read, which is exact. Accumulator register r of lane l is query
+//    l / 16 + 4 r against chunk l % 16, so one store instruction writes 16
+//    consecutive chunks (128 bytes) of four queries' key rows.
+//  * Each wave owns 16 NCB chunks of the workgroup's 64 NCB and every query
+//    of the block. The next slice's chunk and query values are loaded into
+//    registers while the current slice's MFMAs run. Registers are bounded
+//    for four waves per SIMD (the accumulators take 8 NQB NCB of them).
+//  * Dims past D inside the last slice are never read (the loop stops at the
+//    last group of 4); chunks past n and queries past nq read zeros and are
+//    not stored.
+constexpr int SEARCH_MFMA_DK = 32;
+
+template <int NQB, int NCB>
+__global__ __launch_bounds__(256, 4) void cosine_keys_mfma_kernel(
+    const float *__restrict__ V, const double *__restrict__ cnorm,
+    const float *__restrict__ Qf, int nq_pad, const double *__restrict__ qnorm, int nq,
+    int64_t n, int D, const uint8_t *__restrict__ mask, int64_t mask_stride,
+    const int64_t *__restrict__ perm, uint64_t *__restrict__ keys) {
+    constexpr int QB = 16 * NQB, CH = 64 * NCB, DK = SEARCH_MFMA_DK;
+    // row pitches (floats): 16 rows x 4 dims of a fragment read hit 64 banks
+    constexpr int VP = DK + 4;
+    constexpr int QP = QB + 16 > 48 ? QB + 16 : 48;
+    constexpr int VF4 = CH * DK / 4 / 256;              // float4 of the chunk slice per thread
+    constexpr int QN4 = DK * QB / 4;                    // float4 of the query slice
+    constexpr int QF4 = (QN4 + 255) / 256;              // ... per thread
+    static_assert(VF4 >= 1 && CH * DK / 4 % 256 == 0, "slice shape");
+    typedef double f64x4 __attribute__((ext_vector_type(4)));
+    __shared__ float vt[CH * VP];
+    __shared__ float qt[DK * QP];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int64_t c0 = (int64_t)blockIdx.x * CH;
+    const int qs = blockIdx.y * QB;
+
+    f64x4 acc[NQB][NCB];
+#pragma unroll
+    for (int i = 0; i < NQB; ++i)
+#pragma unroll
+        for (int j = 0; j < NCB; ++j) acc[i][j] = f64x4{0.0, 0.0, 0.0, 0.0};
+
+    float4 vr[VF4], qr[QF4];
+    auto load = [&](int d0) {
+#pragma unroll
+        for (int i = 0; i < VF4; ++i) {
+            const int idx = t + 256 * i, r = idx / (DK / 4), k = 4 * (idx % (DK / 4));
+            vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (c0 + r < n && d0 + k < D)
+                vr[i] = *reinterpret_cast<const float4 *>(V + (c0 + r) * D + d0 + k);
+        }
+#pragma unroll
+        for (int i = 0; i < QF4; ++i) {
+            const int idx = t + 256 * i, dd = idx / (QB / 4), q4 = 4 * (idx % (QB / 4));
+            qr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (idx < QN4 && d0 + dd < D)
+                qr[i] = *reinterpret_cast<const float4 *>(Qf + (int64_t)(d0 + dd) * nq_pad + qs + q4);
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int i = 0; i < VF4; ++i) {
+            const int idx = t + 256 * i, r = idx / (DK / 4), k = 4 * (idx % (DK / 4));
+            *reinterpret_cast<float4 *>(&vt[r * VP + k]) = vr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < QF4; ++i) {
+            const int idx = t + 256 * i, dd = idx / (QB / 4), q4 = 4 * (idx % (QB / 4));
+            if (idx < QN4) *reinterpret_cast<float4 *>(&qt[dd * QP + q4]) = qr[i];
+        }
+    };
+
+    const float *vw = vt + (wave * 16 * NCB + l16) * VP + g;
+    const float *qw = qt + g * QP + l16;
+    load(0);
+    for (int d0 = 0; d0 < D; d0 += DK) {
+        store();
+        __syncthreads();
+        if (d0 + DK < D) load(d0 + DK);
+        const int ng = min(DK, D - d0) / 4;
+        for (int s = 0; s < ng; ++s) {
+            double a[NQB], b[NCB];
+#pragma unroll
+            for (int i = 0; i < NQB; ++i) a[i] = (double)qw[4 * s * QP + 16 * i];
+#pragma unroll
+            for (int j = 0; j < NCB; ++j) b[j] = (double)vw[16 * j * VP + 4 * s];
+#pragma unroll
+            for (int i = 0; i < NQB; ++i)
+#pragma unroll
+                for (int j = 0; j < NCB; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int j = 0; j < NCB; ++j) {
+        const int64_t c = c0 + wave * 16 * NCB + 16 * j + l16;
+        if (c >= n) continue;
+        const double cn = cnorm[c];
+        const int64_t orig = mask ? perm[c] : 0;
+#pragma unroll
+        for (int i = 0; i < NQB; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int q = qs + 16 * i + g + 4 * r;
+                if (q >= nq) continue;
+                uint64_t key = ~0ull;
+                if (!mask || mask[(int64_t)q * mask_stride + orig])
+                    key = descending_key(acc[i][j][r] / (qnorm[q] * cn));
+                keys[(int64_t)q * n + c] = key;
+            }
+    }
+}
+
+// Queries as floats, d-major (Qf[d * nq_pad + q], zero padding): the query
+// operand of the matrix-core kernel, staged per slice with float4 loads.
+__global__ __launch_bounds__(256) void queries_dmajor_kernel(const float *Q, int nq, int D,
+                                                             int nq_pad, float *Qf) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)D * nq_pad) return;
+    const int d = (int)(i / nq_pad), q = (int)(i % nq_pad);
+    Qf[i] = q < nq ? Q[(int64_t)q * D + d] : 0.f;
+}
+
 // One workgroup per query: the row is staged in LDS with coalesced loads,
 // then one lane accumulates the squared norm in d order (vector.rs:33-40).
 __global__ __launch_bounds__(256) void query_norm_kernel(const float *Q, int nq, int D,
@@ -200,10 +334,28 @@ hipError_t launch_cosine_keys(const float *V, const double *cnorm, const float *
     const int qb = cosine_query_block(nq);
     const int nq_pad = (nq + qb - 1) / qb * qb;
     const int64_t total = (int64_t)D * nq_pad;
+    const bool vec4 = D % 4 == 0;
+    if (vec4 && qb >= 16) {
+        // FP64 matrix cores: 128 chunks per workgroup, the whole query block;
+        // the queries as floats, d-major, in the first half of Qd's space
+        float *Qf = reinterpret_cast<float *>(Qd);
+        hipLaunchKernelGGL(queries_dmajor_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                           0, s, Q, nq, D, nq_pad, Qf);
+        const dim3 grid((unsigned)((n + 127) / 128), (unsigned)(nq_pad / qb));
+        if (qb == 16)
+            hipLaunchKernelGGL((cosine_keys_mfma_kernel<1, 2>), grid, dim3(256), 0, s, V, cnorm,
+                               Qf, nq_pad, qnorm, nq, n, D, mask, mask_stride, perm, keys);
+        else if (qb == 32)
+            hipLaunchKernelGGL((cosine_keys_mfma_kernel<2, 2>), grid, dim3(256), 0, s, V, cnorm,
+                               Qf, nq_pad, qnorm, nq, n, D, mask, mask_stride, perm, keys);
+        else
+            hipLaunchKernelGGL((cosine_keys_mfma_kernel<4, 2>), grid, dim3(256), 0, s, V, cnorm,
+                               Qf, nq_pad, qnorm, nq, n, D, mask, mask_stride, perm, keys);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(queries_f64_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                        Q, nq, D, nq_pad, Qd);
-    const bool vec4 = D % 4 == 0;
-#define COS_LAUNCH(QB, QW, CPL)                                                                \
+#define COS_LAUNCH(QB, QW, CPL)                                                               \
     do {                                                                                      \
         constexpr int CH = 64 * CPL * 4 / (QB / QW);                                          \
         const dim3 grid((unsigned)((n + CH - 1) / CH), (unsigned)(nq_pad / QB));              \

@@ -155,6 +155,7 @@ hipError_t launch_noalloc_attn_setup(void *base, int seq, int per_head, int bv, 
 // Measured FP32 MFMA rate (register-only chains on every SIMD) and HBM copy
 // bandwidth of the current device (probe.hip).
 hipError_t probe_peaks(double *fp32_mfma_tflops, double *hbm_copy_gbs);
+hipError_t probe_fp64_peak(double *fp64_mfma_tflops);
 
 // Per row r of [offsets[r], offsets[r+1]): pos[t] = t - offsets[r] and
 // rowlen[t] = offsets[r+1] - offsets[r] (rowlen may be null).

@@ -114,7 +114,7 @@ EXPORTED = [
     "svl_text_embed_texts", "svl_vector_index_create", "svl_vector_index_destroy",
     "svl_vector_index_size", "svl_vector_index_dimension", "svl_vector_rank",
     "svl_vector_rank_device", "svl_tensor_to_f32", "svl_bidirectional_attention_noalloc",
-    "svl_measure_peaks",
+    "svl_measure_peaks", "svl_measure_fp64_peak",
 ]
 
 _lib = None
@@ -167,6 +167,7 @@ def lib():
         L.svl_tensor_to_f32.argtypes = [ctypes.POINTER(_TensorView), vp, i64]
         L.svl_measure_peaks.argtypes = [vp, ctypes.POINTER(ctypes.c_double),
                                         ctypes.POINTER(ctypes.c_double)]
+        L.svl_measure_fp64_peak.argtypes = [vp, ctypes.POINTER(ctypes.c_double)]
         L.svl_text_model_set_kernel_timing.argtypes = [vp, ctypes.c_int]
         L.svl_text_model_set_stream_split.argtypes = [vp, ctypes.c_int]
         L.svl_text_model_kernel_stats.argtypes = [vp, vp, vp, vp]
@@ -516,6 +517,12 @@ class Device:
         t, b = ctypes.c_double(), ctypes.c_double()
         _check(lib().svl_measure_peaks(self.handle, ctypes.byref(t), ctypes.byref(b)))
         return t.value, b.value
+
+    def measure_fp64_peak(self):
+        """FP64 MFMA TFLOP/s measured on this device."""
+        t = ctypes.c_double()
+        _check(lib().svl_measure_fp64_peak(self.handle, ctypes.byref(t)))
+        return t.value
 
 
 def tensor_views(weights: dict):
