@@ -162,7 +162,7 @@ svl_status svl_tensor_to_f32(const svl_tensor_view *tensor, float *out, int64_t 
 svl_status svl_measure_peaks(svl_ctx *ctx, double *fp32_mfma_tflops, double *hbm_copy_gbs);
 /* No counterpart in the reference (a measurement aid): the device's FP64
  * matrix rate from register-only v_mfma_f64_16x16x4f64 chains in four waves
- * on every SIMD; best of a few timed launches. Takes a few milliseconds. */
+ * on every SIMD; best of three timed launches of about 12 ms each. */
 svl_status svl_measure_fp64_peak(svl_ctx *ctx, double *fp64_mfma_tflops);
 
 /* Batches of 4096 tokens or more run as `groups` groups of rows (1..4,

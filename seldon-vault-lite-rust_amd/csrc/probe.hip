@@ -58,10 +58,16 @@ __global__ __launch_bounds__(256) void probe_mfma_f64_kernel(double *sink, int i
 #pragma unroll
     for (int c = 0; c < CHAINS; ++c) acc[c] = f64x4{0.0, 0.0, 0.0, 0.0};
     const double a = 1e-3 * (double)(threadIdx.x & 63), b = 0.5;
-    for (int i = 0; i < iters; ++i) {
+    // 16 steps per trip: the compiler moves the accumulators between vector
+    // and accumulation registers once per trip, which with one step per trip
+    // cost more than the MFMAs (the MFMA intrinsic is convergent, so the loop
+    // is not unrolled for us)
+    for (int i = 0; i < iters; i += 16) {
 #pragma unroll
-        for (int c = 0; c < CHAINS; ++c)
-            acc[c] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[c], 0, 0, 0);
+        for (int u = 0; u < 16; ++u)
+#pragma unroll
+            for (int c = 0; c < CHAINS; ++c)
+                acc[c] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[c], 0, 0, 0);
     }
     double s = 0.0;
 #pragma unroll
@@ -154,7 +160,8 @@ hipError_t probe_fp64_peak(double *fp64_mfma_tflops) {
     hipStream_t s = nullptr;
     if ((e = hipStreamCreate(&s)) != hipSuccess) return e;
     double *sink = nullptr;
-    const int iters = 1500;  // about 2 ms per launch
+    const int iters = 12800;  // a multiple of 16; about 12 ms per launch (shorter launches
+                              // measured well below the sustained rate)
     float ms = 0.f;
     e = hipMalloc((void **)&sink, (size_t)cus * 4 * sizeof(double));
     if (e == hipSuccess)  // four workgroups of four waves per CU: four waves per SIMD

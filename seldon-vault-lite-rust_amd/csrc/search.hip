@@ -9,11 +9,12 @@
 // computed in the reference's order on the host.
 //
 // Layout: the chunk matrix V [n, D] (rows in ascending chunk-id order) is
-// streamed once per block of QB queries. Each step stages a slice of 32
-// dimensions of the workgroup's chunks in LDS (padded rows, conflict-free
-// column reads); every lane then runs 32 FMAs per query it serves, whose
-// query operands are uniform loads from a d-major double copy of the queries
-// (scalar registers, no LDS traffic).
+// streamed once per block of QB queries, a slice of 32 dimensions of the
+// workgroup's chunks at a time through LDS. Blocks of 16 to 64 queries run on
+// the FP64 matrix cores (cosine_keys_mfma_kernel, whose instructions add their
+// four products in order); other counts run one lane per (query, chunk) pair
+// with 32 FMAs per slice, whose query operands are uniform loads from a
+// d-major double copy of the queries (cosine_keys_kernel).
 //
 // Ranking: scores become 64-bit keys ordered like f64::total_cmp reversed
 // (ascending key = descending score); masked-out chunks get the largest key.
