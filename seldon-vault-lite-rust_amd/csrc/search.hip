@@ -75,19 +75,32 @@ __global__ __launch_bounds__(256) void cosine_keys_kernel(
     for (int i = 0; i < CPL; ++i)
 #pragma unroll
         for (int j = 0; j < QW; ++j) acc[i][j] = 0.0;
+    // D % 4 == 0: the slice is loaded as float4, 8 lanes per row (128
+    // contiguous bytes of one chunk per 8 lanes), into registers one slice
+    // ahead, so the next slice's loads are in flight while this one's FMAs run
+    constexpr int NPF = CH * (SEARCH_DK / 4) / 256;
+    static_assert(!VEC4 || CH * (SEARCH_DK / 4) % 256 == 0, "slice tiling");
+    float4 pf[VEC4 ? NPF : 1];
+    auto prefetch = [&](int d0) {
+#pragma unroll
+        for (int j = 0; j < NPF; ++j) {
+            const int i = t + 256 * j, r = i / (SEARCH_DK / 4), k = 4 * (i % (SEARCH_DK / 4));
+            pf[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (c0 + r < n && d0 + k < D)
+                pf[j] = *reinterpret_cast<const float4 *>(V + (c0 + r) * D + d0 + k);
+        }
+    };
+    if (VEC4) prefetch(0);
     for (int d0 = 0; d0 < D; d0 += SEARCH_DK) {
         const int dk = min(SEARCH_DK, D - d0);
         if (VEC4) {
-            // 8 lanes per row: 128 contiguous bytes of one chunk per 8 lanes
-            for (int i = t; i < CH * (SEARCH_DK / 4); i += 256) {
-                const int r = i / (SEARCH_DK / 4), k = 4 * (i % (SEARCH_DK / 4));
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (c0 + r < n && k < dk)
-                    v = *reinterpret_cast<const float4 *>(V + (c0 + r) * D + d0 + k);
-                vt[r][k] = v.x;
-                vt[r][k + 1] = v.y;
-                vt[r][k + 2] = v.z;
-                vt[r][k + 3] = v.w;
+#pragma unroll
+            for (int j = 0; j < NPF; ++j) {
+                const int i = t + 256 * j, r = i / (SEARCH_DK / 4), k = 4 * (i % (SEARCH_DK / 4));
+                vt[r][k] = pf[j].x;
+                vt[r][k + 1] = pf[j].y;
+                vt[r][k + 2] = pf[j].z;
+                vt[r][k + 3] = pf[j].w;
             }
         } else {
             for (int i = t; i < CH * SEARCH_DK; i += 256) {
@@ -98,6 +111,7 @@ __global__ __launch_bounds__(256) void cosine_keys_kernel(
             }
         }
         __syncthreads();
+        if (VEC4 && d0 + SEARCH_DK < D) prefetch(d0 + SEARCH_DK);
         const double *qrow = Qd + (int64_t)d0 * nq_pad + qs;
         for (int k = 0; k < dk; ++k) {
             const double *qk = qrow + (int64_t)k * nq_pad;
