@@ -9,8 +9,9 @@ Cases: the reference's unit tests; a ragged dimension (not a multiple of the
 tile; exact score ties broken by chunk id; per-query and shared filters;
 every query-block width (1, 4, 8, 16, 32, 64 and tails), dimensions that are
 and are not a multiple of 4 (vector and scalar staging); pagination slices and
-the full ranking; queries already in HBM; a 200k x 768 index; the error
-taxonomy."""
+the full ranking; queries already in HBM; a 200k x 768 index, on which blocks
+of 16-64 queries (FP64 matrix cores) equal single queries (vector FMAs) bit for
+bit; the error taxonomy."""
 import math
 
 import numpy as np
@@ -99,6 +100,27 @@ def test_device_queries_and_large_index():
         check_query(ix, emb, ids, qs[q], host[q], limit=100, label=f"200k query {q}")
     deep = ix.rank(qs[:1], offset=150_000, limit=1000)
     check_query(ix, emb, ids, qs[0], deep[0], offset=150_000, limit=1000, label="deep page")
+
+
+def test_matrix_core_blocks_equal_single_queries_at_scale():
+    """Blocks of 16, 32 and 64 queries take the FP64 matrix-core score kernel
+    and single queries the vector-FMA kernel. Both sum in dimension order, so
+    on a 200k x 768 index every ranking and every score bit must agree; three
+    queries are also checked against the oracle."""
+    n, d = 200_000, 768
+    emb, ids = corpus(n, d, seed=31)
+    ix = V.VectorIndex(emb, ids)
+    rng = np.random.default_rng(32)
+    qs = rng.standard_normal((64, d)).astype(np.float32)
+    single = [ix.rank(qs[q:q + 1], limit=50)[0] for q in range(64)]
+    for nq in (16, 32, 64):
+        block = ix.rank(qs[:nq], limit=50)
+        for q in range(nq):
+            assert np.array_equal(block[q][0], single[q][0]), f"{nq}-query block, query {q}"
+            assert np.array_equal(block[q][1].view(np.uint64), single[q][1].view(np.uint64)), \
+                f"{nq}-query block, query {q} score bits"
+    for q in (0, 17, 63):
+        check_query(ix, emb, ids, qs[q], single[q], limit=50, label=f"200k query {q}")
 
 
 def test_error_taxonomy():
