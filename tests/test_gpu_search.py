@@ -123,6 +123,25 @@ def test_matrix_core_blocks_equal_single_queries_at_scale():
         check_query(ix, emb, ids, qs[q], single[q], limit=50, label=f"200k query {q}")
 
 
+def test_concurrent_calls_equal_serial_calls():
+    """Calls on one index from several threads (the reference's server runs
+    searches concurrently) are serialised by the index and give the serial
+    results bit for bit, across the vector-FMA and matrix-core paths."""
+    from concurrent.futures import ThreadPoolExecutor
+    n, d = 20_000, 128
+    emb, ids = corpus(n, d, seed=41)
+    ix = V.VectorIndex(emb, ids)
+    rng = np.random.default_rng(42)
+    batches = [rng.standard_normal((nq, d)).astype(np.float32) for nq in (1, 16, 3, 64, 33, 8)]
+    serial = [ix.rank(b, limit=20) for b in batches]
+    with ThreadPoolExecutor(max_workers=6) as ex:
+        threaded = list(ex.map(lambda b: ix.rank(b, limit=20), batches * 3))
+    for i, got in enumerate(threaded):
+        want = serial[i % len(batches)]
+        for (gi, gs), (wi, ws) in zip(got, want):
+            assert np.array_equal(gi, wi) and np.array_equal(gs.view(np.uint64), ws.view(np.uint64))
+
+
 def test_error_taxonomy():
     import torch
     emb = np.array([[1, 0], [0, 0], [0, 1]], np.float32)    # chunk 2 has a zero norm
