@@ -424,38 +424,50 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES, NS>())) voi
         // S^T for keys kb * 16 + 4 (lane / 16) + r (register r of block kb)
         // and query vector lane % 16. K row kb * 16 + l16 holds dim chunk
         // ch = 4 c + g (of the wave's score dims: ch + sdim0 / 4) at slot
-        // ch ^ l16. Chunk c adds to partial sum c / CPB.
-        // The fragments of chunk c + 1 are read while chunk c's MFMAs run,
-        // and the two key blocks' chains alternate.
+        // ch ^ l16. Chunk c adds to partial sum c / CPB. The PPW partial sums
+        // advance together: step i runs chunk p * CPB + i of every partial
+        // sum p, so consecutive MFMAs feed different accumulators, while each
+        // partial sum still takes its chunks, and each chunk its four k, in
+        // the same order (the same bits as running the sums one after
+        // another). The fragments of step i + 1 are read while step i's MFMAs
+        // run, and the key blocks' chains alternate.
         const float *kb0 = kstage(st) + l16 * HD;
         const int ch0 = sdim0 / 4;
-        f32x4 sp[PPW][NKB], kf[NKB];
+        auto kfrag = [&](int c, int kb) {
+            return *(const f32x4 *)(kb0 + kb * 16 * HD + 4 * ((ch0 + 4 * c + g) ^ l16));
+        };
+        f32x4 sp[PPW][NKB], kf[PPW][NKB];
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-#pragma unroll
-            for (int i = 0; i < PPW; ++i) sp[i][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            kf[kb] = *(const f32x4 *)(kb0 + kb * 16 * HD + 4 * ((ch0 + g) ^ l16));
-        }
-#pragma unroll
-        for (int c = 0; c < CPW; ++c) {
-            f32x4 nf[NKB];
+        for (int p = 0; p < PPW; ++p)
 #pragma unroll
             for (int kb = 0; kb < NKB; ++kb) {
-                nf[kb] = kf[kb];
-                if (c + 1 < CPW)
-                    nf[kb] = *(const f32x4 *)(kb0 + kb * 16 * HD +
-                                              4 * ((ch0 + 4 * (c + 1) + g) ^ l16));
+                sp[p][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                kf[p][kb] = kfrag(p * CPB, kb);
             }
-            // keep the reads of chunk c + 1 ahead of chunk c's MFMAs
+#pragma unroll
+        for (int i = 0; i < CPB; ++i) {
+            f32x4 nf[PPW][NKB];
+#pragma unroll
+            for (int p = 0; p < PPW; ++p)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) {
+                    nf[p][kb] = kf[p][kb];
+                    if (i + 1 < CPB) nf[p][kb] = kfrag(p * CPB + i + 1, kb);
+                }
+            // keep the reads of step i + 1 ahead of step i's MFMAs
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int kb = 0; kb < NKB; ++kb)
-                    sp[c / CPB][kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                        kf[kb][j], qf[c][j], sp[c / CPB][kb], 0, 0, 0);
+                for (int p = 0; p < PPW; ++p)
 #pragma unroll
-            for (int kb = 0; kb < NKB; ++kb) kf[kb] = nf[kb];
+                    for (int kb = 0; kb < NKB; ++kb)
+                        sp[p][kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                            kf[p][kb][j], qf[p * CPB + i][j], sp[p][kb], 0, 0, 0);
+#pragma unroll
+            for (int p = 0; p < PPW; ++p)
+#pragma unroll
+                for (int kb = 0; kb < NKB; ++kb) kf[p][kb] = nf[p][kb];
         }
         f32x4 s[NKB];
         if constexpr (DS > 1) {
