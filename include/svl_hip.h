@@ -53,13 +53,16 @@ typedef struct svl_ctx svl_ctx;
 typedef struct svl_text_model svl_text_model;
 
 /* One named weight tensor, borrowed for the duration of the call
- * (src/binary/safetensors.rs:69-110 TensorEntry). */
+ * (src/binary/safetensors.rs:69-110 TensorEntry: name, dtype, shape and its
+ * byte slice). A payload whose length is not numel * 4 (F32) or numel * 2
+ * (BF16) is Corrupt, as in TensorEntry::to_f32 and bf16::decode_bf16. */
 typedef struct {
     const char *name;
     int32_t dtype; /* svl_dtype */
     int32_t ndim;
     int64_t shape[8];
     const void *data; /* host memory, little-endian */
+    size_t nbytes;    /* bytes at data */
 } svl_tensor_view;
 
 /* Validated text configuration (src/model/config.rs:76-95 TextConfig and
@@ -152,7 +155,8 @@ svl_status svl_truncate_and_normalize(const float *values, size_t n, size_t dime
 /* TensorEntry::to_f32 (src/binary/safetensors.rs:69-110): decodes one view
  * into `out` (capacity floats): F32 read little-endian, BF16 widened exactly
  * (bits << 16, src/binary/bf16.rs:13-15). LimitExceeded above the element
- * cap, Unsupported for another dtype. Host only; no device is needed. */
+ * cap, Corrupt when the payload length does not match the shape,
+ * Unsupported for another dtype. Host only; no device is needed. */
 svl_status svl_tensor_to_f32(const svl_tensor_view *tensor, float *out, int64_t capacity);
 
 /* No counterpart in the reference (a measurement aid): the device's FP32
@@ -210,19 +214,32 @@ svl_status svl_bidirectional_attention(const float *d_q, const float *d_k, const
                                        int64_t sliding_window, float scale, float *d_out,
                                        void *stream);
 /* No counterpart in the reference: svl_bidirectional_attention for callers
- * that cannot allocate device memory (code under HIP graph capture, tight
- * serving loops, harnesses that forbid hipMalloc). Same arguments, kernels
- * and results; its work items, position arrays and non-finite flag live in
- * a 320 KiB device array of the library, one per GPU, instead of per-call
- * allocations. At most 8192 keys and 16384 work items (LimitExceeded
- * beyond). Every call on a GPU shares that GPU's array: calls in one process
- * are serialised by a lock and return after their stream has finished, and
- * calls that overlap on one GPU by other means race. */
+ * that cannot allocate device memory (tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments, kernels and results; its work items,
+ * position arrays and non-finite flag live in a 320 KiB device array of the
+ * library, one per GPU, instead of per-call allocations. At most 8192 keys
+ * and 16384 work items (LimitExceeded beyond). The call waits for its stream
+ * and reads the non-finite flag back before it returns, so it cannot be
+ * recorded into a HIP graph. Every call on a GPU shares that GPU's array:
+ * calls in one process are serialised by a lock and return after their
+ * stream has finished, and calls that overlap on one GPU by other means
+ * race. */
 svl_status svl_bidirectional_attention_noalloc(const float *d_q, const float *d_k,
                                                const float *d_v, int64_t seq_len,
                                                int64_t num_heads, int64_t num_kv_heads,
                                                int64_t head_dim, int64_t sliding_window,
                                                float scale, float *d_out, void *stream);
+/* Test hook, no counterpart in the reference: fixes which attention kernel
+ * every later attention launch of the process uses (the model forward passes
+ * and the entry points above), so that tests can check the kernels that only
+ * rows whose K/V operand window passes 2 GiB would otherwise reach.
+ * 0 = by shape (the default), 1 = the fallback for such rows (the
+ * register-staged MFMA kernel at head_dim 64 / 128 / 256, the generic kernel
+ * otherwise), 2 = the generic kernel (one wave per query row and head; rows of
+ * at most 8192 keys). Other values are Usage. Results stay within the
+ * reference tolerance but are not bit-identical across paths; calls in flight
+ * on other threads race with a change. */
+svl_status svl_set_attention_path(int path);
 /* kernels.rs:386-400 gelu_tanh / geglu, kernels.rs:44-52 add. */
 svl_status svl_gelu_tanh(const float *d_in, int64_t n, float *d_out, void *stream);
 svl_status svl_geglu(const float *d_gate, const float *d_up, int64_t n, float *d_out,

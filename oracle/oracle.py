@@ -357,6 +357,8 @@ def _vision_lib():
         L.svlo_pool_patches.argtypes = [f, i32, sz, sz, sz, sz, sz, f]
         L.svlo_vision_forward.argtypes = [ctypes.POINTER(_VisCfg), ctypes.POINTER(f), sz, f, i32,
                                           sz, sz, sz, sz, sz, f, f, ctypes.c_char_p, sz]
+        L.svlo_vision_layer.argtypes = [ctypes.POINTER(_VisCfg), ctypes.POINTER(f), sz, f, i32, sz,
+                                        f, ctypes.c_char_p, sz]
         L._vision_ready = True
     return L
 
@@ -442,6 +444,22 @@ class OracleVisionModel:
                    soft_tokens=soft)
         if capture_hidden:
             out["hidden_states"] = hidden.reshape(L + 1, valid, H)
+        return out
+
+    def layer(self, layer, hidden, positions):
+        """Encoder layer `layer` alone (vision.rs:816-935) applied to hidden
+        [rows, hidden_size] with patch positions [rows, 2] (x, y); the code
+        the forward pass runs per layer."""
+        h = _f32(hidden)
+        rows = h.shape[0]
+        pos = np.ascontiguousarray(np.asarray(positions, np.int32).reshape(-1, 2)[:rows])
+        assert pos.shape[0] == rows
+        out = np.empty_like(h)
+        msg = ctypes.create_string_buffer(256)
+        st = _vision_lib().svlo_vision_layer(ctypes.byref(self._c), self._ptrs, int(layer), _fp(h),
+                                             _ip(pos), rows, _fp(out), msg, 256)
+        if st != 0:
+            raise OracleError(st, msg.value.decode())
         return out
 
 

@@ -151,6 +151,12 @@ int svlo_vision_forward(const svlo_vision_config *cfg, const float *const *weigh
                         size_t valid, size_t max_patches, size_t grid_width, size_t grid_height,
                         size_t soft_tokens, float *out_pooled, float *out_hidden, char *msg,
                         size_t msg_len);
+/* One encoder layer of VisionModel::forward (vision.rs:816-935) alone, from a
+ * given hidden state [rows, hidden] and patch positions [rows, 2] (x, y), into
+ * out [rows, hidden]; the same code the forward pass runs per layer. */
+int svlo_vision_layer(const svlo_vision_config *cfg, const float *const *weights, size_t layer,
+                      const float *hidden_in, const int32_t *positions, size_t rows, float *out,
+                      char *msg, size_t msg_len);
 
 /* ---- audio tower (src/model/audio.rs) ----------------------------------- */
 

@@ -10,10 +10,15 @@
  *  - svlo_axial_inv_freq / svlo_axial_rope against the known answers of
  *    src/model/vision.rs:1154-1182 and a float64 rotation restatement;
  *  - svlo_pool_patches against a float64 bin average;
- *  - svlo_vision_forward against an independent float64 numpy forward with
- *    random weights. No offline golden exists for the vision tower (the
- *    reference's image golden needs the full released weights), so the
- *    whole-tower result is pinned by restatement only.
+ *  - svlo_vision_forward by closed forms of degenerate weight sets (zero
+ *    projections: every layer is the identity; identical patches: attention
+ *    returns the value row), by a brute-force softmax over two patches that
+ *    fixes the q_norm / k_norm / axial RoPE wiring (tests/test_oracle_wiring.py),
+ *    and against an independent float64 numpy forward with random weights.
+ *    No offline golden exists for the vision tower (the reference's image
+ *    golden needs the full released weights).
+ *  - svlo_vision_layer is the forward pass's own per-layer code; chaining it
+ *    reproduces svlo_vision_forward bit for bit.
  */
 #include <math.h>
 #include <stdarg.h>
@@ -172,6 +177,128 @@ enum {
 };
 #define VW(layer, idx) weights[SVLO_VISION_GLOBAL_TENSORS + (size_t)(layer)*SVLO_VISION_LAYER_TENSORS + (idx)]
 
+/* Work buffers of one encoder layer over `valid` rows. */
+typedef struct {
+    float *residual, *normed, *tmp, *tmp2, *query, *query_n, *key, *key_n, *value, *value_n,
+        *attn, *gate, *up, *act;
+} vis_layer_bufs;
+
+static void vis_layer_free(vis_layer_bufs *b) {
+    free(b->residual);
+    free(b->normed);
+    free(b->tmp);
+    free(b->tmp2);
+    free(b->query);
+    free(b->query_n);
+    free(b->key);
+    free(b->key_n);
+    free(b->value);
+    free(b->value_n);
+    free(b->attn);
+    free(b->gate);
+    free(b->up);
+    free(b->act);
+    memset(b, 0, sizeof(*b));
+}
+
+static int vis_layer_alloc(vis_layer_bufs *b, size_t n_hidden, size_t n_q, size_t n_kv,
+                           size_t n_ff) {
+    b->residual = (float *)malloc(n_hidden * sizeof(float));
+    b->normed = (float *)malloc(n_hidden * sizeof(float));
+    b->tmp = (float *)malloc(n_hidden * sizeof(float));
+    b->tmp2 = (float *)malloc(n_hidden * sizeof(float));
+    b->query = (float *)malloc(n_q * sizeof(float));
+    b->query_n = (float *)malloc(n_q * sizeof(float));
+    b->key = (float *)malloc(n_kv * sizeof(float));
+    b->key_n = (float *)malloc(n_kv * sizeof(float));
+    b->value = (float *)malloc(n_kv * sizeof(float));
+    b->value_n = (float *)malloc(n_kv * sizeof(float));
+    b->attn = (float *)malloc(n_q * sizeof(float));
+    b->gate = (float *)malloc(n_ff * sizeof(float));
+    b->up = (float *)malloc(n_ff * sizeof(float));
+    b->act = (float *)malloc(n_ff * sizeof(float));
+    if (b->residual && b->normed && b->tmp && b->tmp2 && b->query && b->query_n && b->key &&
+        b->key_n && b->value && b->value_n && b->attn && b->gate && b->up && b->act)
+        return 1;
+    vis_layer_free(b);
+    return 0;
+}
+
+/* One encoder layer (vision.rs:816-935) in place on hidden [valid, H]; inv
+ * holds the head_dim / 4 axial frequencies. */
+static int vis_layer(const svlo_vision_config *cfg, const float *const *weights, size_t l,
+                     float *hidden, const int32_t *positions, size_t valid, const float *inv,
+                     vis_layer_bufs *b) {
+    const size_t H = (size_t)cfg->hidden_size, I = (size_t)cfg->intermediate_size;
+    const size_t NH = (size_t)cfg->num_attention_heads, NKV = (size_t)cfg->num_key_value_heads;
+    const size_t hd = (size_t)cfg->head_dim, qd = NH * hd, kd = NKV * hd;
+    const size_t n_hidden = valid * H, n_ff = valid * I;
+    const float eps = cfg->rms_norm_eps;
+    int st;
+    memcpy(b->residual, hidden, n_hidden * sizeof(float));
+    if ((st = svlo_rms_norm_rows(hidden, VW(l, V_INPUT_LN), valid, H, eps, b->normed))) return st;
+    if ((st = svlo_linear(b->normed, VW(l, V_Q), valid, H, qd, b->query))) return st;
+    if ((st = svlo_linear(b->normed, VW(l, V_K), valid, H, kd, b->key))) return st;
+    if ((st = svlo_linear(b->normed, VW(l, V_V), valid, H, kd, b->value))) return st;
+    if ((st = svlo_rms_norm_rows(b->query, VW(l, V_QNORM), valid * NH, hd, eps, b->query_n)))
+        return st;
+    if ((st = svlo_rms_norm_rows(b->key, VW(l, V_KNORM), valid * NKV, hd, eps, b->key_n)))
+        return st;
+    if ((st = svlo_rms_norm_rows_unscaled(b->value, valid * NKV, hd, eps, b->value_n))) return st;
+    if ((st = svlo_axial_rope(b->query_n, valid, NH, hd, positions, valid, inv, hd / 4))) return st;
+    if ((st = svlo_axial_rope(b->key_n, valid, NKV, hd, positions, valid, inv, hd / 4))) return st;
+    if ((st = svlo_bidirectional_attention(b->query_n, b->key_n, b->value_n, valid, NH, NKV, hd, -1,
+                                           1.0f, b->attn)))
+        return st;
+    if ((st = svlo_linear(b->attn, VW(l, V_O), valid, qd, H, b->tmp))) return st;
+    if ((st = svlo_rms_norm_rows(b->tmp, VW(l, V_POST_ATTN_LN), valid, H, eps, b->tmp2))) return st;
+    svlo_add(b->residual, b->tmp2, n_hidden, hidden);
+
+    memcpy(b->residual, hidden, n_hidden * sizeof(float));
+    if ((st = svlo_rms_norm_rows(hidden, VW(l, V_PRE_FF_LN), valid, H, eps, b->normed))) return st;
+    if ((st = svlo_linear(b->normed, VW(l, V_GATE), valid, H, I, b->gate))) return st;
+    if ((st = svlo_linear(b->normed, VW(l, V_UP), valid, H, I, b->up))) return st;
+    if ((st = svlo_geglu(b->gate, b->up, n_ff, b->act))) return st;
+    if ((st = svlo_linear(b->act, VW(l, V_DOWN), valid, I, H, b->tmp))) return st;
+    if ((st = svlo_rms_norm_rows(b->tmp, VW(l, V_POST_FF_LN), valid, H, eps, b->tmp2))) return st;
+    svlo_add(b->residual, b->tmp2, n_hidden, hidden);
+    return SVLO_OK;
+}
+
+int svlo_vision_layer(const svlo_vision_config *cfg, const float *const *weights, size_t layer,
+                      const float *hidden_in, const int32_t *positions, size_t rows, float *out,
+                      char *msg, size_t msg_len) {
+    if (msg && msg_len) msg[0] = 0;
+    if (layer >= (size_t)cfg->num_hidden_layers || rows == 0)
+        return vis_fail(msg, msg_len, SVLO_INTERNAL, "vision layer %zu of %lld over %zu rows", layer,
+                        (long long)cfg->num_hidden_layers, rows);
+    const size_t H = (size_t)cfg->hidden_size, hd = (size_t)cfg->head_dim;
+    size_t n_hidden, n_q, n_kv, n_ff;
+    if (vis_checked_len(rows, H, &n_hidden) ||
+        vis_checked_len(rows, (size_t)cfg->num_attention_heads * hd, &n_q) ||
+        vis_checked_len(rows, (size_t)cfg->num_key_value_heads * hd, &n_kv) ||
+        vis_checked_len(rows, (size_t)cfg->intermediate_size, &n_ff))
+        return vis_fail(msg, msg_len, SVLO_LIMIT, "vision activation above the element cap");
+    for (size_t p = 0; p < rows; ++p)
+        if (positions[2 * p] < 0 || positions[2 * p + 1] < 0)
+            return vis_fail(msg, msg_len, SVLO_INTERNAL, "vision patch position is negative");
+    vis_layer_bufs b;
+    float *inv = (float *)malloc((hd / 4 + 1) * sizeof(float));
+    if (!inv || !vis_layer_alloc(&b, n_hidden, n_q, n_kv, n_ff)) {
+        free(inv);
+        return vis_fail(msg, msg_len, SVLO_LIMIT, "allocation failed");
+    }
+    int st = svlo_axial_inv_freq(hd, cfg->rope_theta, inv);
+    if (st == SVLO_OK) {
+        memcpy(out, hidden_in, n_hidden * sizeof(float));
+        st = vis_layer(cfg, weights, layer, out, positions, rows, inv, &b);
+    }
+    if (st) vis_fail(msg, msg_len, st, "vision kernel failed with status %d (non-finite value or limit)", st);
+    vis_layer_free(&b);
+    free(inv);
+    return st;
+}
+
 /* VisionModel::forward (vision.rs:742-959). */
 int svlo_vision_forward(const svlo_vision_config *cfg, const float *const *weights,
                         size_t text_hidden, const float *pixel_values, const int32_t *positions,
@@ -197,28 +324,15 @@ int svlo_vision_forward(const svlo_vision_config *cfg, const float *const *weigh
         return vis_fail(msg, msg_len, SVLO_LIMIT, "vision activation above the element cap");
 
     int st = SVLO_OK;
+    vis_layer_bufs b;
+    memset(&b, 0, sizeof(b));
     float *scaled = (float *)malloc(n_patch * sizeof(float));
     float *hidden = (float *)malloc(n_hidden * sizeof(float));
-    float *residual = (float *)malloc(n_hidden * sizeof(float));
-    float *normed = (float *)malloc(n_hidden * sizeof(float));
-    float *tmp = (float *)malloc(n_hidden * sizeof(float));
-    float *tmp2 = (float *)malloc(n_hidden * sizeof(float));
-    float *query = (float *)malloc(n_q * sizeof(float));
-    float *query_n = (float *)malloc(n_q * sizeof(float));
-    float *key = (float *)malloc(n_kv * sizeof(float));
-    float *key_n = (float *)malloc(n_kv * sizeof(float));
-    float *value = (float *)malloc(n_kv * sizeof(float));
-    float *value_n = (float *)malloc(n_kv * sizeof(float));
-    float *attn = (float *)malloc(n_q * sizeof(float));
-    float *gate = (float *)malloc(n_ff * sizeof(float));
-    float *up = (float *)malloc(n_ff * sizeof(float));
-    float *act = (float *)malloc(n_ff * sizeof(float));
     float *pooled = (float *)malloc((n_pool + 1) * sizeof(float));
     float *pooled_n = (float *)malloc((n_pool + 1) * sizeof(float));
     float *inv = (float *)malloc((hd / 4 + 1) * sizeof(float));
-    if (!scaled || !hidden || !residual || !normed || !tmp || !tmp2 || !query || !query_n ||
-        !key || !key_n || !value || !value_n || !attn || !gate || !up || !act || !pooled ||
-        !pooled_n || !inv) {
+    if (!scaled || !hidden || !pooled || !pooled_n || !inv ||
+        !vis_layer_alloc(&b, n_hidden, n_q, n_kv, n_ff)) {
         st = vis_fail(msg, msg_len, SVLO_LIMIT, "allocation failed");
         goto done;
     }
@@ -250,31 +364,7 @@ int svlo_vision_forward(const svlo_vision_config *cfg, const float *const *weigh
     if ((st = svlo_axial_inv_freq(hd, cfg->rope_theta, inv))) goto knl;
     /* vision.rs:816-935 encoder layers. */
     for (size_t l = 0; l < L; ++l) {
-        memcpy(residual, hidden, n_hidden * sizeof(float));
-        if ((st = svlo_rms_norm_rows(hidden, VW(l, V_INPUT_LN), valid, H, eps, normed))) goto knl;
-        if ((st = svlo_linear(normed, VW(l, V_Q), valid, H, qd, query))) goto knl;
-        if ((st = svlo_linear(normed, VW(l, V_K), valid, H, kd, key))) goto knl;
-        if ((st = svlo_linear(normed, VW(l, V_V), valid, H, kd, value))) goto knl;
-        if ((st = svlo_rms_norm_rows(query, VW(l, V_QNORM), valid * NH, hd, eps, query_n))) goto knl;
-        if ((st = svlo_rms_norm_rows(key, VW(l, V_KNORM), valid * NKV, hd, eps, key_n))) goto knl;
-        if ((st = svlo_rms_norm_rows_unscaled(value, valid * NKV, hd, eps, value_n))) goto knl;
-        if ((st = svlo_axial_rope(query_n, valid, NH, hd, positions, valid, inv, hd / 4))) goto knl;
-        if ((st = svlo_axial_rope(key_n, valid, NKV, hd, positions, valid, inv, hd / 4))) goto knl;
-        if ((st = svlo_bidirectional_attention(query_n, key_n, value_n, valid, NH, NKV, hd, -1,
-                                               1.0f, attn)))
-            goto knl;
-        if ((st = svlo_linear(attn, VW(l, V_O), valid, qd, H, tmp))) goto knl;
-        if ((st = svlo_rms_norm_rows(tmp, VW(l, V_POST_ATTN_LN), valid, H, eps, tmp2))) goto knl;
-        svlo_add(residual, tmp2, n_hidden, hidden);
-
-        memcpy(residual, hidden, n_hidden * sizeof(float));
-        if ((st = svlo_rms_norm_rows(hidden, VW(l, V_PRE_FF_LN), valid, H, eps, normed))) goto knl;
-        if ((st = svlo_linear(normed, VW(l, V_GATE), valid, H, I, gate))) goto knl;
-        if ((st = svlo_linear(normed, VW(l, V_UP), valid, H, I, up))) goto knl;
-        if ((st = svlo_geglu(gate, up, n_ff, act))) goto knl;
-        if ((st = svlo_linear(act, VW(l, V_DOWN), valid, I, H, tmp))) goto knl;
-        if ((st = svlo_rms_norm_rows(tmp, VW(l, V_POST_FF_LN), valid, H, eps, tmp2))) goto knl;
-        svlo_add(residual, tmp2, n_hidden, hidden);
+        if ((st = vis_layer(cfg, weights, l, hidden, positions, valid, inv, &b))) goto knl;
         if (out_hidden) memcpy(out_hidden + (l + 1) * n_hidden, hidden, n_hidden * sizeof(float));
     }
 
@@ -295,22 +385,9 @@ int svlo_vision_forward(const svlo_vision_config *cfg, const float *const *weigh
 knl:
     vis_fail(msg, msg_len, st, "vision kernel failed with status %d (non-finite value or limit)", st);
 done:
+    vis_layer_free(&b);
     free(scaled);
     free(hidden);
-    free(residual);
-    free(normed);
-    free(tmp);
-    free(tmp2);
-    free(query);
-    free(query_n);
-    free(key);
-    free(key_n);
-    free(value);
-    free(value_n);
-    free(attn);
-    free(gate);
-    free(up);
-    free(act);
     free(pooled);
     free(pooled_n);
     free(inv);

@@ -28,7 +28,7 @@
 // own order of operations (score row, max-subtracted exp, divide by the sum,
 // p-weighted value rows in key order).
 #include <algorithm>
-
+#include <atomic>
 #include <type_traits>
 
 #include "dev_common.hpp"
@@ -711,13 +711,27 @@ static hipError_t launch_attn16(const AttnArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Kernel choice forced by set_attention_path (0: by shape).
+static std::atomic<int> g_attention_path{ATTN_PATH_AUTO};
+
+void set_attention_path(int path) { g_attention_path.store(path, std::memory_order_relaxed); }
+
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s) {
     if (a.tokens <= 0) return hipSuccess;
     const dim3 block(64 * ATTN_WAVES);
+    const int path = g_attention_path.load(std::memory_order_relaxed);
+    if (path == ATTN_PATH_GENERIC) {
+        if (!a.pos || !a.rowlen || a.max_len <= 0 || a.max_len > ATTN_SIMPLE_MAX_KEYS)
+            return hipErrorInvalidValue;
+        hipLaunchKernelGGL(attn_simple_kernel, dim3((unsigned)(a.tokens * a.nh)), dim3(64), 0, s,
+                           a);
+        return hipGetLastError();
+    }
     // Buffer windows are per row: the longest row bounds the offsets.
     // A tail tile addresses up to 31 keys past the row end (read as zero).
     const int64_t rows = (a.max_len > 0 ? a.max_len : a.tokens) + 32;
-    const bool dma = rows * std::max(std::max(a.ldk, a.ldv), (int64_t)a.hd) * 4 < INT32_MAX;
+    const bool dma = path == ATTN_PATH_AUTO &&
+                     rows * std::max(std::max(a.ldk, a.ldv), (int64_t)a.hd) * 4 < INT32_MAX;
     switch (a.hd) {
         case 64:
             if (dma) return launch_attn16<64, 32>(a, s);

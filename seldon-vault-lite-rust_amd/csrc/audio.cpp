@@ -70,13 +70,12 @@ struct svl_audio_model {
     int64_t H = 0, I = 0, L = 0, NH = 0, hd = 0, K = 0, C0 = 0, C1 = 0, chunk = 0, left = 0,
             right = 0, P = 0, text_hidden = 0, context = 0, positions = 0, H_pad = 0;
     float cap = 0.f, eps = 0.f, rw = 0.f, clip = 0.f, k_scale = 0.f;
-    bool conv_implicit = false;  // layer-1 convolution as an implicit-im2col GEMM
     std::vector<float *> allocations;
     float *w_conv0 = nullptr, *ln0 = nullptr, *w_conv1 = nullptr, *ln1 = nullptr,
           *w_in = nullptr, *w_out = nullptr, *b_out = nullptr, *w_emb = nullptr;
     std::vector<AuLayer> layers;
     // workspace
-    DevBuf<float> mel, l0, col, l1, h, n, tmp, act, qkv, att, gated, proj, projn, soft;
+    DevBuf<float> mel, l0, l1, h, n, tmp, act, qkv, att, gated, proj, projn, soft;
     DevBuf<uint8_t> mask, mask0, mask1;
     DevBuf<SscpRow> rows0, rows1;
     DevBuf<int32_t> pos, rowlen, valid_idx, att_blocks;
@@ -91,7 +90,7 @@ struct svl_audio_model {
         delete lm;
         if (device >= 0) (void)hipSetDevice(device);
         for (float *p : allocations) (void)hipFree(p);
-        mel.release(); l0.release(); col.release(); l1.release(); h.release(); n.release(); tmp.release();
+        mel.release(); l0.release(); l1.release(); h.release(); n.release(); tmp.release();
         act.release(); qkv.release(); att.release(); gated.release(); proj.release();
         projn.release(); soft.release(); mask.release(); mask0.release(); mask1.release();
         rows0.release(); rows1.release(); pos.release(); rowlen.release(); valid_idx.release();
@@ -299,10 +298,11 @@ svl_status prepare_clips(const svl_audio_model *m, const svl_mel *mels, int32_t 
         if (f1 * FREQ0 * m->C0 > MAX_ACTIVATION_ELEMENTS || f2 * FREQ1 * m->C1 > MAX_ACTIVATION_ELEMENTS)
             return fail(SVL_LIMIT, "clip %d: audio subsampling would allocate more than the "
                                    "%lld-element cap", i, (long long)MAX_ACTIVATION_ELEMENTS);
-        const int64_t widest = std::max({m->I, 2 * m->H, m->P, m->text_hidden});
-        if (f2 * widest > MAX_ACTIVATION_ELEMENTS)
-            return fail(SVL_LIMIT, "clip %d: audio linear output would allocate %lld elements", i,
-                        (long long)(f2 * widest));
+        // The input projection takes (C0 / 4) * C1 features per row and layer 1
+        // yields 32 * C1 (audio.rs:1244-1248): only C0 = 128 can run.
+        if ((m->C0 / 4) * m->C1 != FREQ1 * m->C1)
+            return fail(SVL_INTERNAL,
+                        "audio subsampling output does not match the projection input width");
         for (int64_t t = 0; t < f1; ++t) {
             b.rows0.push_back({(int32_t)b.frame_off.back(), (int32_t)t, (int32_t)F});
             b.mask0.push_back(2 * t < F ? (uint8_t)(mel.mask[2 * t] != 0) : (uint8_t)0);
@@ -320,6 +320,10 @@ svl_status prepare_clips(const svl_audio_model *m, const svl_mel *mels, int32_t 
         }
         if (tok == 0)
             return fail(SVL_CORRUPT, "clip %d: audio tower received no valid subsampled token", i);
+        const int64_t widest = std::max({m->I, 2 * m->H, m->P, m->text_hidden});
+        if (f2 * widest > MAX_ACTIVATION_ELEMENTS)
+            return fail(SVL_LIMIT, "clip %d: audio linear output would allocate %lld elements", i,
+                        (long long)(f2 * widest));
         b.tokens_per_clip.push_back(tok);
         row0_off += f1;
         b.frame_off.push_back(b.frame_off.back() + F);
@@ -329,9 +333,15 @@ svl_status prepare_clips(const svl_audio_model *m, const svl_mel *mels, int32_t 
     b.T0 = row0_off;
     b.T = b.row_off.back();
     b.tokens = (int64_t)b.valid_idx.size();
-    if (b.F > (int64_t)INT32_MAX / 2 || b.T0 * FREQ0 * m->C0 > (int64_t)1 << 31)
-        return fail(SVL_LIMIT, "batch holds too many frames");
     return SVL_OK;
+}
+
+// One pass of the tower keeps its layer-0 activations below 2 GiB: the
+// implicit-im2col convolution reads them through one 32-bit buffer window,
+// and the packed frame and row offsets are 32-bit. One clip always fits
+// (its layer-0 output is at most MAX_ACTIVATION_ELEMENTS floats).
+bool au_pass_fits(const svl_audio_model *m, int64_t t0) {
+    return t0 * FREQ0 * m->C0 * 4 < 0x7FFFFFF0;
 }
 
 svl_status ensure_au_workspace(svl_audio_model *m, const AuBatch &b) {
@@ -340,7 +350,6 @@ svl_status ensure_au_workspace(svl_audio_model *m, const AuBatch &b) {
     HIP_TRY(m->mel.ensure(F * FEATURE_SIZE));
     HIP_TRY(m->mask.ensure(F));
     HIP_TRY(m->l0.ensure(T0 * FREQ0 * m->C0));
-    if (!m->conv_implicit) HIP_TRY(m->col.ensure(T * FREQ1 * 9 * m->C0));
     HIP_TRY(m->l1.ensure(T * FREQ1 * m->C1));
     HIP_TRY(m->h.ensure(T * m->H));
     HIP_TRY(m->n.ensure(3 * T * m->H));  // three clamped copies feed the Q/K/V projection
@@ -365,7 +374,7 @@ svl_status ensure_au_workspace(svl_audio_model *m, const AuBatch &b) {
     return SVL_OK;
 }
 
-svl_status upload_au_meta(svl_audio_model *m, const AuBatch &b, hipStream_t s) {
+svl_status upload_au_meta(svl_audio_model *m, const AuBatch &b, hipStream_t s, bool reset_flag) {
     HIP_TRY(hipMemcpyAsync(m->rows0.p, b.rows0.data(), b.rows0.size() * sizeof(SscpRow),
                            hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(m->rows1.p, b.rows1.data(), b.rows1.size() * sizeof(SscpRow),
@@ -378,7 +387,7 @@ svl_status upload_au_meta(svl_audio_model *m, const AuBatch &b, hipStream_t s) {
                            hipMemcpyHostToDevice, s));
     HIP_TRY(hipMemcpyAsync(m->offsets.p, b.row_off.data(), b.row_off.size() * 8,
                            hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemsetAsync(m->flag.p, 0, sizeof(int), s));
+    if (reset_flag) HIP_TRY(hipMemsetAsync(m->flag.p, 0, sizeof(int), s));
     return SVL_OK;
 }
 
@@ -391,11 +400,11 @@ void select_valid(const AuBatch &b, int64_t H, const float *all, float *out) {
 }
 
 // The tower over the packed mel frames in d_mel (audio.rs:981-1133); soft
-// tokens of the valid rows land in m->soft. Captures (all rows, [T, H]; the
+// tokens of the valid rows land in d_soft. Captures (all rows, [T, H]; the
 // caller selects the valid ones after the stream drains): h_sscp after the
 // subsampling, h_hidden [L, T, H] after every layer.
 svl_status enqueue_audio(svl_audio_model *m, const AuBatch &b, const float *d_mel, hipStream_t s,
-                         float *h_sscp, float *h_hidden) {
+                         float *d_soft, float *h_sscp, float *h_hidden) {
     const int64_t T = b.T, H = m->H, I = m->I;
     const int W = (int)H;
     int *flag = m->flag.p;
@@ -404,27 +413,23 @@ svl_status enqueue_audio(svl_audio_model *m, const AuBatch &b, const float *d_me
     // Subsampling (audio.rs:1136-1255).
     HIP_TRY(launch_sscp_conv0(d_mel, m->mask.p, m->rows0.p, b.T0, m->w_conv0, m->ln0, (int)m->C0,
                               m->eps, m->l0.p, flag, s));
-    // layer 1: the 3x3 stride-2 convolution as a GEMM against the [C1, 9 C0]
-    // weight (an implicit im2col, or im2col + GEMM), then LayerNorm + ReLU
+    // layer 1: the 3x3 stride-2 convolution as an implicit-im2col GEMM against
+    // the tap-major [C1, 9 C0] weight, then LayerNorm + ReLU. C0 is 128 in
+    // every configuration that reaches this point (prepare_clips), and a pass
+    // keeps the layer-0 output inside the kernel's buffer window
+    // (au_pass_fits), so gemm_conv_ok holds.
     {
         const int64_t K = 9 * m->C0;
-        if (m->conv_implicit) {
-            GemmArgs g{m->l0.p, K, m->w_conv1, K, m->l1.p, m->C1, (int)(T * FREQ1), (int)m->C1,
-                       (int)K, EPI_STORE, 1.f, nullptr, 0, 0};
-            g.conv_rows = reinterpret_cast<const int32_t *>(m->rows1.p);
-            g.conv_mask = m->mask0.p;
-            g.conv_c0 = (int)m->C0;
-            g.conv_f0 = (int)FREQ0;
-            g.conv_f1 = (int)FREQ1;
-            g.conv_a_floats = b.T0 * FREQ0 * m->C0;
-            if (!gemm_conv_ok(g)) return fail(SVL_LIMIT, "audio subsampling too large for one launch");
-            HIP_TRY(launch_gemm_conv(g, s));
-        } else {
-            HIP_TRY(launch_sscp_im2col(m->l0.p, m->mask0.p, m->rows1.p, T, (int)m->C0, m->col.p, s));
-            GemmArgs g{m->col.p, K, m->w_conv1, K, m->l1.p, m->C1, (int)(T * FREQ1), (int)m->C1,
-                       (int)K, EPI_STORE, 1.f, nullptr, 0, 0};
-            HIP_TRY(launch_gemm(g, s));
-        }
+        GemmArgs g{m->l0.p, K, m->w_conv1, K, m->l1.p, m->C1, (int)(T * FREQ1), (int)m->C1,
+                   (int)K, EPI_STORE, 1.f, nullptr, 0, 0};
+        g.conv_rows = reinterpret_cast<const int32_t *>(m->rows1.p);
+        g.conv_mask = m->mask0.p;
+        g.conv_c0 = (int)m->C0;
+        g.conv_f0 = (int)FREQ0;
+        g.conv_f1 = (int)FREQ1;
+        g.conv_a_floats = b.T0 * FREQ0 * m->C0;
+        if (!gemm_conv_ok(g)) return fail(SVL_INTERNAL, "audio subsampling launch out of bounds");
+        HIP_TRY(launch_gemm_conv(g, s));
     }
     HIP_TRY(launch_sscp_ln_relu(m->l1.p, m->ln1, (int)m->C1, T * FREQ1, m->eps, flag, s));
     {
@@ -544,11 +549,11 @@ svl_status enqueue_audio(svl_audio_model *m, const AuBatch &b, const float *d_me
     HIP_TRY(launch_compact_rms(m->proj.p, m->valid_idx.p, m->projn.p, b.tokens, (int)m->P, m->eps,
                                flag, s));
     {
-        GemmArgs g{m->projn.p, m->P, m->w_emb, m->P, m->soft.p, m->text_hidden, (int)b.tokens,
+        GemmArgs g{m->projn.p, m->P, m->w_emb, m->P, d_soft, m->text_hidden, (int)b.tokens,
                    (int)m->text_hidden, (int)m->P, EPI_STORE, 1.f, nullptr, 0, 0};
         HIP_TRY(launch_gemm(g, s));
     }
-    HIP_TRY(launch_finite_check(m->soft.p, b.tokens * m->text_hidden, flag, s));
+    HIP_TRY(launch_finite_check(d_soft, b.tokens * m->text_hidden, flag, s));
     return SVL_OK;
 }
 
@@ -560,42 +565,75 @@ svl_status au_finish(svl_audio_model *m, hipStream_t s) {
     return SVL_OK;
 }
 
-// Runs the tower; soft tokens stay in m->soft. Mel frames come from the
-// host spectrograms, or from d_features ([sum frames, 128] in HBM). Caller
-// holds m->mu.
+// Runs the tower; soft tokens stay in m->soft, clip after clip. Mel frames
+// come from the host spectrograms, or from d_features ([sum frames, 128] in
+// HBM). A batch whose layer-0 activations would pass au_pass_fits runs as
+// consecutive passes over groups of whole clips on the same stream; every
+// clip is an independent reference call, so its output does not depend on
+// the grouping. Caller holds m->mu.
 svl_status run_audio(svl_audio_model *m, const svl_mel *mels, int32_t batch,
                      const float *d_features, hipStream_t s, AuBatch &b, int64_t *out_tokens,
                      float *out_soft, float *out_sscp, float *out_hidden) {
     HIP_TRY(hipSetDevice(m->device));
     ST_TRY(prepare_clips(m, mels, batch, d_features == nullptr, b));
     if (batch == 0) return SVL_OK;
-    ST_TRY(ensure_au_workspace(m, b));
-    if (!d_features) {
-        for (int i = 0; i < batch; ++i)
-            if (mels[i].frames > 0)
-                HIP_TRY(hipMemcpyAsync(m->mel.p + b.frame_off[i] * FEATURE_SIZE, mels[i].features,
-                                       (size_t)(mels[i].frames * FEATURE_SIZE) * 4,
-                                       hipMemcpyHostToDevice, s));
-        d_features = m->mel.p;
+    std::vector<int32_t> first(1, 0);  // first clip of each pass, then batch
+    for (int32_t i = 0, t0 = 0; i < batch; ++i) {
+        const int64_t f1 = (mels[i].frames + 1) / 2;
+        if (i > first.back() && !au_pass_fits(m, t0 + f1)) {
+            first.push_back(i);
+            t0 = 0;
+        }
+        t0 += (int32_t)f1;
     }
-    for (int i = 0; i < batch; ++i)
-        if (mels[i].frames > 0)
-            HIP_TRY(hipMemcpyAsync(m->mask.p + b.frame_off[i], mels[i].mask, (size_t)mels[i].frames,
-                                   hipMemcpyHostToDevice, s));
-    ST_TRY(upload_au_meta(m, b, s));
-    std::vector<float> all_sscp, all_hidden;
-    if (out_sscp) all_sscp.resize((size_t)(b.T * m->H));
-    if (out_hidden) all_hidden.resize((size_t)(m->L * b.T * m->H));
-    ST_TRY(enqueue_audio(m, b, d_features, s, out_sscp ? all_sscp.data() : nullptr,
-                         out_hidden ? all_hidden.data() : nullptr));
+    first.push_back(batch);
+    const size_t passes = first.size() - 1;
+    std::vector<AuBatch> parts(passes > 1 ? passes : 0);
+    for (size_t g = 0; g < parts.size(); ++g)
+        ST_TRY(prepare_clips(m, mels + first[g], first[g + 1] - first[g], d_features == nullptr,
+                             parts[g]));
+    // every workspace is sized before the first launch, so no buffer moves
+    // while an earlier pass still reads it
+    for (size_t g = 0; g < passes; ++g) ST_TRY(ensure_au_workspace(m, passes > 1 ? parts[g] : b));
+    HIP_TRY(m->soft.ensure((size_t)std::max<int64_t>(b.tokens, 1) * m->text_hidden));
+    std::vector<std::vector<float>> cap_sscp(passes), cap_hidden(passes);
+    int64_t tok_off = 0;
+    for (size_t g = 0; g < passes; ++g) {
+        const AuBatch &pb = passes > 1 ? parts[g] : b;
+        const int32_t c0 = first[g], nc = first[g + 1] - first[g];
+        const float *feats = d_features ? d_features + b.frame_off[(size_t)c0] * FEATURE_SIZE
+                                        : m->mel.p;
+        for (int32_t i = 0; i < nc; ++i) {
+            const svl_mel &mel = mels[c0 + i];
+            if (mel.frames <= 0) continue;
+            if (!d_features)
+                HIP_TRY(hipMemcpyAsync(m->mel.p + pb.frame_off[(size_t)i] * FEATURE_SIZE,
+                                       mel.features, (size_t)(mel.frames * FEATURE_SIZE) * 4,
+                                       hipMemcpyHostToDevice, s));
+            HIP_TRY(hipMemcpyAsync(m->mask.p + pb.frame_off[(size_t)i], mel.mask,
+                                   (size_t)mel.frames, hipMemcpyHostToDevice, s));
+        }
+        ST_TRY(upload_au_meta(m, pb, s, g == 0));
+        if (out_sscp) cap_sscp[g].resize((size_t)(pb.T * m->H));
+        if (out_hidden) cap_hidden[g].resize((size_t)(m->L * pb.T * m->H));
+        ST_TRY(enqueue_audio(m, pb, feats, s, m->soft.p + tok_off * m->text_hidden,
+                             out_sscp ? cap_sscp[g].data() : nullptr,
+                             out_hidden ? cap_hidden[g].data() : nullptr));
+        tok_off += pb.tokens;
+    }
     if (out_soft)
         HIP_TRY(hipMemcpyAsync(out_soft, m->soft.p, (size_t)(b.tokens * m->text_hidden) * 4,
                                hipMemcpyDeviceToHost, s));
     ST_TRY(au_finish(m, s));
-    if (out_sscp) select_valid(b, m->H, all_sscp.data(), out_sscp);
-    for (int64_t l = 0; out_hidden && l < m->L; ++l)
-        select_valid(b, m->H, all_hidden.data() + (size_t)(l * b.T * m->H),
-                     out_hidden + (size_t)(l * b.tokens * m->H));
+    tok_off = 0;
+    for (size_t g = 0; g < passes; ++g) {
+        const AuBatch &pb = passes > 1 ? parts[g] : b;
+        if (out_sscp) select_valid(pb, m->H, cap_sscp[g].data(), out_sscp + tok_off * m->H);
+        for (int64_t l = 0; out_hidden && l < m->L; ++l)
+            select_valid(pb, m->H, cap_hidden[g].data() + (size_t)(l * pb.T * m->H),
+                         out_hidden + (size_t)((l * b.tokens + tok_off) * m->H));
+        tok_off += pb.tokens;
+    }
     if (out_tokens)
         for (int i = 0; i < batch; ++i) out_tokens[i] = b.tokens_per_clip[(size_t)i];
     return SVL_OK;
@@ -738,8 +776,6 @@ svl_status svl_audio_model_create(svl_ctx *ctx, const svl_audio_config *cfg, int
         return fail(SVL_UNSUPPORTED, "audio head dimension above 256 or attention context above 64");
     if (m->C0 > 512)
         return fail(SVL_UNSUPPORTED, "audio subsampling channels above 512 are not supported");
-    if ((m->C0 / 4) * m->C1 != FREQ1 * m->C1)
-        return fail(SVL_INTERNAL, "audio subsampling output does not match the projection input width");
 
     std::vector<float> a, b2;
     auto up = [&](const std::string &name, float **dst) -> svl_status {
@@ -750,17 +786,14 @@ svl_status svl_audio_model_create(svl_ctx *ctx, const svl_audio_config *cfg, int
     ST_TRY(up(sp + "layer0.conv.weight", &m->w_conv0));
     ST_TRY(up(sp + "layer0.norm.weight", &m->ln0));
     // Layer-1 convolution weight [C1][C0][3][3]; the implicit-im2col GEMM
-    // (C0 % 32 == 0) takes it tap-major, [C1][3 x 3][C0].
+    // takes it tap-major, [C1][3 x 3][C0].
     ST_TRY(decode_named(by_name, sp + "layer1.conv.weight", a));
-    m->conv_implicit = m->C0 % 32 == 0;
-    if (m->conv_implicit) {
-        b2.assign(a.size(), 0.f);
-        for (int64_t o = 0; o < m->C1; ++o)
-            for (int64_t c = 0; c < m->C0; ++c)
-                for (int64_t t = 0; t < 9; ++t)
-                    b2[(size_t)((o * 9 + t) * m->C0 + c)] = a[(size_t)((o * m->C0 + c) * 9 + t)];
-        a.swap(b2);
-    }
+    b2.assign(a.size(), 0.f);
+    for (int64_t o = 0; o < m->C1; ++o)
+        for (int64_t c = 0; c < m->C0; ++c)
+            for (int64_t t = 0; t < 9; ++t)
+                b2[(size_t)((o * 9 + t) * m->C0 + c)] = a[(size_t)((o * m->C0 + c) * 9 + t)];
+    a.swap(b2);
     ST_TRY(upload_owned(m->allocations, a.data(), a.size(), &m->w_conv1));
     ST_TRY(up(sp + "layer1.norm.weight", &m->ln1));
     ST_TRY(up(sp + "input_proj_linear.weight", &m->w_in));

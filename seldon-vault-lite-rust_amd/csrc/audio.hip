@@ -3,7 +3,8 @@
 // specific to the tower lives here:
 //  * the two stride-2 3x3 subsampling convolutions, each with its per-position
 //    LayerNorm (weight, no bias) and ReLU (audio.rs:1136-1255, 1290-1322):
-//    the first direct, the second as im2col + the MFMA GEMM;
+//    the first direct, the second as an implicit-im2col MFMA GEMM
+//    (launch_gemm_conv) followed by the LayerNorm + ReLU kernel here;
 //  * one fused row kernel for every clamp / RMSNorm / residual / next-norm
 //    chain of the conformer block (audio.rs:1374-1433, 1000-1066);
 //  * the chunked local attention with relative positions and the logit soft
@@ -115,71 +116,6 @@ hipError_t launch_sscp_conv0(const float *mel, const uint8_t *mask, const SscpRo
     else if (cpt <= 128) C0_LAUNCH(128);
     else return hipErrorInvalidValue;
 #undef C0_LAUNCH
-    return hipGetLastError();
-}
-
-// ---- subsampling convolution 1 as im2col + GEMM ---------------------------
-// (Configurations with C0 % 32 == 0 take the implicit-im2col GEMM instead,
-// launch_gemm_conv, which reads the taps straight from the layer-0 output.)
-// col[(r * 32 + f) * 9 C0 + ic * 9 + kt * 3 + kf] = layer0 input tap, zero
-// where the tap is outside the clip, masked or outside the 64 frequencies:
-// the k order of the layer-1 weight [C1][C0][3][3], so the GEMM against it
-// sums each output in the reference's (channel, row, column) order. One
-// thread per (output position, group of four input channels): nine 16-byte
-// loads, one per tap, coalesced over the channel groups of a layer-0 row,
-// and nine 16-byte stores of the thread's 36 contiguous columns (channel
-// major, tap minor: a register transpose of the loads). C0 % 4 == 0 (the
-// configuration requires it).
-__global__ __launch_bounds__(256) void sscp_im2col_kernel(const float *__restrict__ l0,
-                                                          const uint8_t *__restrict__ mask0,
-                                                          const SscpRow *__restrict__ rows,
-                                                          int64_t n_pos, int C0,
-                                                          float *__restrict__ col) {
-    const int groups = C0 >> 2;
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= n_pos * groups) return;
-    const int64_t pos = idx / groups;
-    const int ic0 = 4 * (int)(idx - pos * groups);
-    const int64_t r = pos / FREQ1;
-    const int f = (int)(pos - r * FREQ1);
-    const SscpRow ri = rows[r];
-    f32x4 tap[9];
-#pragma unroll
-    for (int kt = 0; kt < 3; ++kt) {
-        const int it = 2 * ri.t + kt - 1;
-        const bool row_ok = it >= 0 && it < ri.len && mask0[ri.base + it];
-#pragma unroll
-        for (int kf = 0; kf < 3; ++kf) {
-            const int iff = 2 * f + kf - 1;
-            f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (row_ok && iff >= 0 && iff < FREQ0)
-                v = *(const f32x4 *)(l0 + ((int64_t)(ri.base + it) * FREQ0 + iff) * C0 + ic0);
-            tap[kt * 3 + kf] = v;
-        }
-    }
-    // out[j * 9 + t] = channel ic0 + j of tap t, for the 36 columns from ic0 * 9
-    float o[36];
-#pragma unroll
-    for (int t = 0; t < 9; ++t) {
-        o[0 * 9 + t] = tap[t].x;
-        o[1 * 9 + t] = tap[t].y;
-        o[2 * 9 + t] = tap[t].z;
-        o[3 * 9 + t] = tap[t].w;
-    }
-    f32x4 *dst = (f32x4 *)(col + pos * (int64_t)(9 * C0) + 9 * ic0);
-#pragma unroll
-    for (int u = 0; u < 9; ++u) dst[u] = f32x4{o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]};
-}
-
-hipError_t launch_sscp_im2col(const float *l0, const uint8_t *mask0, const SscpRow *rows,
-                              int64_t n_rows, int C0, float *col, hipStream_t s) {
-    const int64_t n = n_rows * FREQ1;
-    if (n <= 0) return hipSuccess;
-    if (C0 <= 0 || C0 % 4) return hipErrorInvalidValue;
-    const int64_t threads = n * (C0 / 4);
-    if ((threads + 255) / 256 > INT32_MAX) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(sscp_im2col_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       s, l0, mask0, rows, n, C0, col);
     return hipGetLastError();
 }
 

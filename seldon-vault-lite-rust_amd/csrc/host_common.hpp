@@ -123,12 +123,24 @@ inline svl_status check_inventory(const svl_tensor_view *tensors, size_t n_tenso
 }
 
 // TensorEntry::to_f32 (safetensors.rs:69-110): F32 little-endian or BF16
-// widened exactly (bf16.rs:13-15, bits << 16). Non-finite values are
-// rejected like Tensor::validate_finite (owned.rs:126-135).
+// widened exactly (bf16.rs:13-15, bits << 16), each after the payload length
+// check of the reference (safetensors.rs:79-88, bf16.rs:40-51). numel is at
+// most MAX_TENSOR_ELEMENTS, so the byte counts cannot overflow. Non-finite
+// values are rejected like Tensor::validate_finite (owned.rs:126-135).
 inline svl_status widen_f32(const svl_tensor_view &t, int64_t numel, float *out) {
     if (t.dtype == SVL_F32) {
-        std::memcpy(out, t.data, (size_t)numel * 4);
+        const uint64_t expected = (uint64_t)numel * 4;
+        if (t.nbytes != expected)
+            return fail(SVL_CORRUPT, "tensor %s has %llu bytes, expected %llu for %lld F32 values",
+                        t.name, (unsigned long long)t.nbytes, (unsigned long long)expected,
+                        (long long)numel);
+        if (numel > 0) std::memcpy(out, t.data, (size_t)numel * 4);
     } else if (t.dtype == SVL_BF16) {
+        const uint64_t expected = (uint64_t)numel * 2;
+        if (t.nbytes != expected)
+            return fail(SVL_CORRUPT, "BF16 length mismatch: expected %llu bytes for %lld values, "
+                        "got %llu", (unsigned long long)expected, (long long)numel,
+                        (unsigned long long)t.nbytes);
         const uint16_t *b = (const uint16_t *)t.data;
         for (int64_t i = 0; i < numel; ++i) {
             const uint32_t bits = (uint32_t)b[i] << 16;

@@ -1115,7 +1115,7 @@ svl_status svl_tensor_to_f32(const svl_tensor_view *t, float *out, int64_t capac
     if (numel > capacity)
         return fail(SVL_USAGE, "tensor %s has %lld elements, the output holds %lld", t->name,
                     (long long)numel, (long long)capacity);
-    if (numel == 0) return SVL_OK;
+    if (numel == 0) return widen_f32(*t, 0, out);
     if (!t->data || !out) return fail(SVL_USAGE, "tensor %s has no data", t->name);
     return widen_f32(*t, numel, out);
 }
@@ -1406,6 +1406,13 @@ svl_status svl_bidirectional_attention_noalloc(const float *d_q, const float *d_
     HIP_TRY(launch_noalloc_attn_setup(base, (int)seq_len, (int)per_head, bv, a.n_tiles, s));
     if (launch_attention(a, s) != hipSuccess) return fail(SVL_DEVICE, "attention launch failed");
     return seam_finish(s, a.flag, "attention");
+}
+
+svl_status svl_set_attention_path(int path) {
+    if (path != ATTN_PATH_AUTO && path != ATTN_PATH_FALLBACK && path != ATTN_PATH_GENERIC)
+        return fail(SVL_USAGE, "attention path %d is not 0, 1 or 2", path);
+    set_attention_path(path);
+    return SVL_OK;
 }
 
 static svl_status seam_elementwise(const char *what, int kind, const float *a, const float *b,

@@ -70,7 +70,7 @@ struct GemmArgs {
 
 hipError_t launch_gemm(const GemmArgs &a, hipStream_t s);
 // True when launch_gemm_conv can take the convolution (conv_c0 % 32 == 0,
-// windows below 2 GiB); otherwise the caller runs im2col and launch_gemm.
+// windows below 2 GiB).
 bool gemm_conv_ok(const GemmArgs &a);
 hipError_t launch_gemm_conv(const GemmArgs &a, hipStream_t s);
 // Plain scalar-FMA fallback for shapes the MFMA kernel does not take
@@ -134,6 +134,12 @@ struct AttnArgs {
 // Query vectors per work item of the MFMA kernel (0 if hd has no MFMA kernel).
 int attn_block_vectors(int hd);
 hipError_t launch_attention(const AttnArgs &a, hipStream_t s);
+// Attention kernel choice for every later launch in the process (a test
+// hook): by shape (the DMA kernel whenever a row's operand window fits 2 GiB),
+// the fallback that longer windows take (the register-staged MFMA kernel at
+// head_dim 64 / 128 / 256, the generic kernel at 512), or the generic kernel.
+constexpr int ATTN_PATH_AUTO = 0, ATTN_PATH_FALLBACK = 1, ATTN_PATH_GENERIC = 2;
+void set_attention_path(int path);
 
 // Scratch of the allocation-free attention entry point (noalloc.hip), one
 // copy per GPU: work items, then per-token positions and row lengths, then
@@ -215,10 +221,6 @@ static_assert(sizeof(SscpRow) == 3 * sizeof(int32_t), "GemmArgs::conv_rows reads
 hipError_t launch_sscp_conv0(const float *mel, const uint8_t *mask, const SscpRow *rows,
                              int64_t n_rows, const float *w, const float *ln, int C0, float eps,
                              float *out, int *flag, hipStream_t s);
-// Layer-0 taps of every layer-1 output position as rows [pos, 9 C0] in the
-// layer-1 weight's (channel, kernel row, kernel column) order.
-hipError_t launch_sscp_im2col(const float *l0, const uint8_t *mask0, const SscpRow *rows,
-                              int64_t n_rows, int C0, float *col, hipStream_t s);
 // In place: x[p] = relu(layernorm(x[p], ln)) over C channels, n positions.
 hipError_t launch_sscp_ln_relu(float *x, const float *ln, int C, int64_t n, float eps, int *flag,
                                hipStream_t s);

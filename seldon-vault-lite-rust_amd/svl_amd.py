@@ -70,7 +70,8 @@ def _unsupported(msg):
 
 class _TensorView(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int32), ("ndim", ctypes.c_int32),
-                ("shape", ctypes.c_int64 * 8), ("data", ctypes.c_void_p)]
+                ("shape", ctypes.c_int64 * 8), ("data", ctypes.c_void_p),
+                ("nbytes", ctypes.c_size_t)]
 
 
 class _Config(ctypes.Structure):
@@ -114,7 +115,7 @@ EXPORTED = [
     "svl_text_embed_texts", "svl_vector_index_create", "svl_vector_index_destroy",
     "svl_vector_index_size", "svl_vector_index_dimension", "svl_vector_rank",
     "svl_vector_rank_device", "svl_tensor_to_f32", "svl_bidirectional_attention_noalloc",
-    "svl_measure_peaks", "svl_measure_fp64_peak",
+    "svl_measure_peaks", "svl_measure_fp64_peak", "svl_set_attention_path",
 ]
 
 _lib = None
@@ -178,6 +179,7 @@ def lib():
         L.svl_bidirectional_attention.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, f32, vp, vp]
         L.svl_bidirectional_attention_noalloc.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64,
                                                           f32, vp, vp]
+        L.svl_set_attention_path.argtypes = [ctypes.c_int]
         L.svl_gelu_tanh.argtypes = [vp, i64, vp, vp]
         L.svl_geglu.argtypes = [vp, vp, i64, vp, vp]
         L.svl_add.argtypes = [vp, vp, i64, vp, vp]
@@ -460,6 +462,7 @@ class RawTensor:
         for i, d in enumerate(self.shape):
             v.shape[i] = int(d)
         v.data = data.ctypes.data if data.size else None
+        v.nbytes = data.nbytes
         _check(lib().svl_tensor_to_f32(ctypes.byref(v), _ptr(out), out.size))
         return out[:numel].reshape(self.shape)
 
@@ -549,6 +552,7 @@ def tensor_views(weights: dict):
         for i, d in enumerate(shape):
             v.shape[i] = int(d)
         v.data = data.ctypes.data
+        v.nbytes = data.nbytes
         views.append(v)
     return (_TensorView * len(views))(*views), len(views), keep
 
@@ -770,6 +774,16 @@ def bidirectional_attention_noalloc(q, k, v, seq, nh, nkv, hd, window, scale, ou
     _check(lib().svl_bidirectional_attention_noalloc(
         _dp(q), _dp(k), _dp(v), seq, nh, nkv, hd, -1 if window is None else int(window), scale,
         _dp(out), _stream()))
+
+
+ATTENTION_PATHS = {"auto": 0, "fallback": 1, "generic": 2}
+
+
+def set_attention_path(path: str):
+    """Test hook: which attention kernel every later launch of the process
+    uses ("auto" by shape, "fallback" as for rows whose K/V window passes
+    2 GiB, "generic")."""
+    _check(lib().svl_set_attention_path(ATTENTION_PATHS[path]))
 
 
 def gelu_tanh(x, n, out):

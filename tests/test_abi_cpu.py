@@ -47,6 +47,13 @@ def test_library_exports_every_declared_entry_point():
     assert set(syms) == set(svl_amd.EXPORTED)
 
 
+def test_attention_path_hook_rejects_unknown_paths():
+    with pytest.raises(svl_amd.SvlError) as e:
+        svl_amd._check(svl_amd.lib().svl_set_attention_path(3))
+    assert e.value.kind == "Usage"
+    svl_amd.set_attention_path("auto")
+
+
 def test_library_has_a_single_gfx950_code_object():
     data = open(svl_amd.LIB_PATH, "rb").read()
     assert data.count(b"amdgcn-amd-amdhsa--gfx950") >= 1

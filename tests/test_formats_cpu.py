@@ -50,6 +50,26 @@ def test_decode_error_kinds():
     assert e.value.kind == "LimitExceeded"
 
 
+@pytest.mark.parametrize("dtype,itemsize", [("F32", 4), ("BF16", 2)])
+@pytest.mark.parametrize("extra", [-1, +1, -4, +6])
+def test_payload_length_must_match_the_shape(dtype, itemsize, extra):
+    """TensorEntry::to_f32 and bf16::decode_bf16 return Corrupt when the byte
+    slice is not numel * 4 (F32) or numel * 2 (BF16) long
+    (safetensors.rs:79-88, bf16.rs:40-51); nothing past the payload is read."""
+    good = np.arange(6).astype(np.float32 if dtype == "F32" else np.uint16)
+    raw = np.frombuffer(good.tobytes() + b"\x00" * 8, np.uint8)
+    payload = raw[: good.nbytes + extra]
+    with pytest.raises(S.SvlError) as e:
+        S.RawTensor(dtype, (2, 3), payload).to_f32()
+    assert e.value.kind == "Corrupt"
+    want = "bytes, expected" if dtype == "F32" else "BF16 length mismatch"
+    assert want in str(e.value)
+    assert S.RawTensor(dtype, (2, 3), raw[: good.nbytes]).to_f32().shape == (2, 3)
+    with pytest.raises(S.SvlError) as e:   # an empty tensor with a non-empty payload
+        S.RawTensor(dtype, (0, 3), raw[:itemsize]).to_f32()
+    assert e.value.kind == "Corrupt"
+
+
 def _view(t):
     import ctypes
     v = S._TensorView()

@@ -136,6 +136,58 @@ def test_batch_and_device_paths_are_bit_identical(au2):
     assert np.array_equal(d_out.cpu().numpy(), np.concatenate([b.pooled() for b in batch]))
 
 
+def test_subsampling_width_mismatch_fails_the_forward_pass_like_the_reference():
+    """A legal configuration whose first subsampling layer has 36 channels
+    loads, but its input projection takes (36 / 4) * C1 features per row
+    while layer 1 yields 32 * C1, so the forward pass fails with Internal,
+    in the reference (audio.rs:1244-1248) as here, after the subsampling
+    caps and before the no-token check."""
+    c = svl_synth.config_au(1)
+    c["audio_config"]["subsampling_conv_channels"] = [36, 20]
+    w = svl_synth.audio_weights(c, 768, seed=12)
+    gpu = A.AudioModel(A.AudioConfig.from_json_value(c), w, 768)
+    om = O.OracleAudioModel(c, w, 768)
+    mel = _masked_clips()[0]
+    with pytest.raises(S.SvlError) as e:
+        gpu.forward(mel)
+    assert e.value.kind == "Internal"
+    assert "projection input width" in str(e.value)
+    with pytest.raises(O.OracleError) as e:
+        om.forward(mel.features, mel.mask.astype(bool))
+    assert e.value.status == 7
+    empty = svl_synth.mel_clips([9], seed=3, masks=[np.zeros(9, bool)])[0]
+    with pytest.raises(S.SvlError) as e:   # width before the no-token check, as in audio.rs
+        gpu.forward(empty)
+    assert e.value.kind == "Internal"
+    gpu.close()
+
+
+def test_batch_past_one_pass_runs_in_passes():
+    """44 clips of 2999 frames put 66,000 layer-0 rows of 64 x 128 floats in
+    one batch, past the 2 GiB that one pass of the tower takes (43 clips), so
+    the batch runs as two passes. Every clip's soft tokens equal a single
+    call bit for bit, on the host path and on the device path."""
+    import torch
+    c = svl_synth.config_au(1)
+    w = svl_synth.audio_weights(c, 64, seed=13)
+    gpu = A.AudioModel(A.AudioConfig.from_json_value(c), w, 64)
+    mels = svl_synth.mel_clips([2999] * 44, seed=14)
+    batch = gpu.forward_batch(mels)
+    assert [b.audio_tokens() for b in batch] == [750] * 44
+    for i in (0, 42, 43):
+        assert np.array_equal(gpu.forward(mels[i]).pooled(), batch[i].pooled()), f"clip {i}"
+    feats = torch.from_numpy(np.concatenate([m.features for m in mels])).to("cuda:0")
+    d_out = torch.empty((44 * 750, 64), device="cuda:0")
+    torch.cuda.synchronize()
+    gpu.forward_device(feats.data_ptr(), mels, d_out.data_ptr())
+    assert np.array_equal(d_out.cpu().numpy(), np.concatenate([b.pooled() for b in batch]))
+    one = gpu.forward(mels[43], capture_hidden=True)
+    cap = gpu.forward_batch(mels, capture_hidden=True)
+    assert np.array_equal(cap[43].hidden_states()[0], one.hidden_states()[0])
+    assert np.array_equal(cap[43].sscp_output(), one.sscp_output())
+    gpu.close()
+
+
 # Attention shapes beyond config AU: a head_dim of 15 (rows not 16-byte
 # aligned) with 20-row blocks and a 61-entry context (a full wave of lanes
 # per query, two passes over each block's queries, right context), and a

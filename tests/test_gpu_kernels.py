@@ -132,6 +132,41 @@ def test_attention_matches_oracle(seq, nh, nkv, hd, window):
     np.testing.assert_allclose(host(out), ref, atol=1e-4, rtol=1e-4)
 
 
+@pytest.fixture
+def attention_path():
+    """Sets the process-wide attention kernel choice for one test and puts
+    it back to "auto" afterwards, also when the test fails."""
+    yield S.set_attention_path
+    S.set_attention_path("auto")
+
+
+FALLBACK_SHAPES = [
+    (1, 3, 1, 256, None), (37, 3, 1, 256, None), (130, 3, 1, 256, 16), (700, 3, 1, 256, 512),
+    (97, 4, 2, 256, 8), (64, 12, 12, 64, None), (50, 8, 8, 128, 7), (33, 4, 1, 512, None),
+    (300, 4, 4, 64, 40), (131, 6, 2, 128, None), (1000, 3, 1, 256, 100), (300, 8, 2, 512, 40),
+    (129, 2, 2, 512, 3), (900, 4, 4, 128, 64), (200, 3, 1, 64, 33)]
+
+
+@pytest.mark.parametrize("path", ["fallback", "generic"])
+@pytest.mark.parametrize("seq,nh,nkv,hd,window", FALLBACK_SHAPES)
+def test_fallback_attention_kernels_match_oracle(seq, nh, nkv, hd, window, path, attention_path):
+    """The kernels that rows whose K/V operand window passes 2 GiB take (the
+    register-staged 32x32x2 MFMA kernel at head_dim 64 / 128 / 256, the
+    generic kernel at 512), and the generic kernel at every head dim, forced
+    through the test hook on the shapes of the DMA kernel's parity test
+    (kernels.rs:1037-1135)."""
+    rng = np.random.default_rng(seq + hd)
+    q = (rng.standard_normal((seq, nh, hd)) * 0.25).astype(np.float32)
+    k = (rng.standard_normal((seq, nkv, hd)) * 0.25).astype(np.float32)
+    v = rng.standard_normal((seq, nkv, hd)).astype(np.float32)
+    out = empty(seq * nh * hd)
+    attention_path(path)
+    S.bidirectional_attention(dev(q), dev(k), dev(v), seq, nh, nkv, hd, window, 1.0, out)
+    attention_path("auto")
+    ref = O.bidirectional_attention(q, k, v, seq, nh, nkv, hd, window, 1.0)
+    np.testing.assert_allclose(host(out), ref, atol=1e-4, rtol=1e-4)
+
+
 @pytest.mark.parametrize("seq,nh,nkv,hd,window", [
     (37, 3, 1, 256, None), (50, 8, 8, 128, 7), (131, 6, 2, 128, None), (300, 4, 4, 64, 40),
     (33, 4, 1, 512, None), (1000, 3, 1, 256, 100)])

@@ -120,6 +120,21 @@ def test_shape_a_reduced_depth_ragged_rows_match_oracle():
     _shape_parity(cfg, [1, 31, 129, 300, 515, 700])
 
 
+@pytest.mark.parametrize("path", ["fallback", "generic"])
+def test_forward_on_the_fallback_attention_kernels_matches_oracle(path):
+    """The whole forward pass with its attention forced onto the kernels that
+    rows past a 2 GiB K/V window take (the register-staged MFMA kernel at
+    head_dim 256) and onto the generic kernel: shape A at reduced depth with
+    ragged rows across the 512-token window, and shape B (two KV heads, and
+    head_dim 512 on its full layer)."""
+    try:
+        S.set_attention_path(path)
+        _shape_parity(svl_synth.config_a(layers=6, vocab=4096), [1, 31, 129, 300, 515, 700])
+        _shape_parity(svl_synth.config_b(layers=6, vocab=4096), [77, 600])
+    finally:
+        S.set_attention_path("auto")
+
+
 def test_shape_a_full_depth_t1_matches_oracle():
     # 24 layers at the reference-sized config, batch 1 x 128 tokens.
     cfg = svl_synth.config_a(layers=24, vocab=262144)
@@ -322,6 +337,13 @@ def test_weight_inventory_is_validated():  # weights.rs:130-166
     with pytest.raises(S.SvlError) as e:
         S.TextModel(c, w4)
     assert e.value.kind == "Internal"
+    # a payload one element short of its shape (safetensors.rs:79-88)
+    w5 = dict(w)
+    short = np.ascontiguousarray(w["language_model.norm.weight"], np.float32)[:-1]
+    w5["language_model.norm.weight"] = S.RawTensor("F32", (cfg["hidden_size"],), short)
+    with pytest.raises(S.SvlError) as e:
+        S.TextModel(c, w5)
+    assert e.value.kind == "Corrupt"
 
 
 def _to_bf16_bits(a):

@@ -7,9 +7,11 @@ src/model/image.rs:209-253) through the C ABI.
   MFMA attention kernel) against the CPU oracle, image by image, over ragged
   batches with padding rows;
 * config V at full depth on a full 768 x 768 image (48 x 48 patches): every
-  stage checked against a float64 restatement applied to the GPU's own
-  input of that stage (patch embedding, layers 1 / 8 / 16, pooling and
-  projection), since the scalar oracle needs minutes at that size;
+  stage checked from the GPU's own input to it (the patch embedding, pooling
+  and projection in float64; layers 1 / 8 / 16 by the oracle's single-layer
+  path, since the whole oracle tower needs minutes at that size), the
+  260-token image prompt through the 24-layer shape-A text encoder against
+  the text oracle, and a four-image batch bit-identical to single calls;
 * batching and device-resident variants bit-identical to single calls;
 * the image embedder (tower + prompt + text encoder with soft tokens)
   against the oracle chain at Matryoshka dims 768 and 128;
@@ -148,85 +150,97 @@ def test_device_resident_matches_host(tower_v2):
     assert np.array_equal(d_out.cpu().numpy(), host)
 
 
-def test_full_size_image_every_stage(tmp_path):
-    """Config V, 16 layers, one 768 x 768 image (2304 patches, 256 soft
-    tokens). Each checked stage is recomputed in float64 from the GPU's own
-    input to that stage."""
+@pytest.fixture(scope="module")
+def full_v():
+    """Config V at 16 layers and one 768 x 768 noise image (2304 patches, 256
+    soft tokens), run once on the GPU with every hidden state captured."""
     c = svl_synth.config_v(16)
     w = svl_synth.vision_weights(c, 768, seed=13)
     gpu = V.VisionModel(V.VisionConfig.from_json_value(c), w, 768)
     p = svl_synth.image_patches(1, 48, 48, seed=2)[0]
     out = gpu.forward(p, capture_hidden=True)
+    return c, w, gpu, p, out
+
+
+def test_full_size_image_every_stage(full_v):
+    """Config V, 16 layers, one 768 x 768 image (2304 patches, 256 soft
+    tokens). Each checked stage is computed from the GPU's own input to that
+    stage: the patch embedding in float64, layers 1, 8 and 16 by the oracle's
+    single-layer path (the forward pass's own per-layer code; the whole
+    oracle tower needs minutes at this size), and the pool, unscaled norm and
+    projection in float64."""
+    c, w, gpu, p, out = full_v
     hs = out.hidden_states()
     assert len(hs) == 17 and hs[0].shape == (2304, 768)
     assert out.pooled().shape == (256, 768)
     vc = O.resolve_vision_config(c)
     pos = p.positions[:2304]
+    om = O.OracleVisionModel(c, w, 768)
 
     def rel(g, r):
-        return float(np.abs(g - r).max() / np.abs(r).max())
+        return float(np.abs(np.asarray(g, np.float64) - r).max() / np.abs(r).max())
 
-    # patch embedding + position add
-    pe = (2.0 * (p.pixel_values[:2304].astype(np.float64) - 0.5)) @ \
-        w["vision_tower.patch_embedder.input_proj.weight"].astype(np.float64).T
-    table = w["vision_tower.patch_embedder.position_embedding_table"].astype(np.float64)
-    pe += table[0][pos[:, 0]] + table[1][pos[:, 1]]
-    e = rel(hs[0], pe)
-    print(f"patch embedding: relative max error {e:.3g}", flush=True)
-    assert e <= 1e-5
+    with ThreadPoolExecutor(max_workers=3) as ex:
+        layers = {l: ex.submit(om.layer, l - 1, hs[l - 1], pos) for l in (1, 8, 16)}
 
-    # single layers: restate layer l in float64 from the GPU's layer l-1 output
-    one = dict(vc, num_hidden_layers=1)
-    for l in (1, 8, 16):
-        wl = {k: v for k, v in w.items() if not k.startswith("vision_tower.encoder.layers.")}
-        pre = f"vision_tower.encoder.layers.{l - 1}."
-        for k, v in w.items():
-            if k.startswith(pre):
-                wl["vision_tower.encoder.layers.0." + k[len(pre):]] = v
-        ref = _layer64(one, wl, hs[l - 1].astype(np.float64), pos)
-        e = rel(hs[l], ref)
-        print(f"layer {l}: relative max error {e:.3g}", flush=True)
-        assert e <= 1e-4
+        # patch embedding + position add
+        pe = (2.0 * (p.pixel_values[:2304].astype(np.float64) - 0.5)) @ \
+            w["vision_tower.patch_embedder.input_proj.weight"].astype(np.float64).T
+        table = w["vision_tower.patch_embedder.position_embedding_table"].astype(np.float64)
+        pe += table[0][pos[:, 0]] + table[1][pos[:, 1]]
+        e = rel(hs[0], pe)
+        print(f"patch embedding: relative max error {e:.3g}", flush=True)
+        assert e <= 1e-5
 
-    # pool + unscaled norm + projection from the GPU's last hidden state
-    pooled = ref64.pool_patches64(hs[16].astype(np.float64), pos, 48, 48, 256)
-    soft = ref64.rms(pooled, None, vc["rms_norm_eps"]) @ \
-        w["embed_vision.embedding_projection.weight"].astype(np.float64).T
-    d = float(np.abs(out.pooled() - soft).max())
-    c_ = cosine(out.pooled(), soft)
-    print(f"soft tokens: max-abs {d:.3g} cosine {c_:.9f}", flush=True)
-    assert d <= MAX_ABS and c_ >= MIN_COS
-    assert np.isfinite(out.pooled()).all()
+        # pool + unscaled norm + projection from the GPU's last hidden state
+        pooled = ref64.pool_patches64(hs[16].astype(np.float64), pos, 48, 48, 256)
+        soft = ref64.rms(pooled, None, vc["rms_norm_eps"]) @ \
+            w["embed_vision.embedding_projection.weight"].astype(np.float64).T
+        d = float(np.abs(out.pooled() - soft).max())
+        c_ = cosine(out.pooled(), soft)
+        print(f"soft tokens: max-abs {d:.3g} cosine {c_:.9f}", flush=True)
+        assert d <= MAX_ABS and c_ >= MIN_COS
+        assert np.isfinite(out.pooled()).all()
+
+        for l, f in layers.items():
+            e = rel(hs[l], f.result())
+            print(f"layer {l} against the oracle layer: relative max error {e:.3g}", flush=True)
+            assert e <= 1e-4
 
 
-def _layer64(vc, w, h, pos):
-    """One encoder layer of vision.rs:816-935 in float64 (ref64's loop body)."""
-    H, NH, NKV, hd, eps = (vc["hidden_size"], vc["num_attention_heads"],
-                           vc["num_key_value_heads"], vc["head_dim"], vc["rms_norm_eps"])
-    f64 = lambda n: w[n].astype(np.float64)
-    p = "vision_tower.encoder.layers.0."
-    valid = h.shape[0]
-    inv = ref64.axial_inv_freq64(hd, vc["rope_theta"])
-    n = ref64.rms(h, w[p + "input_layernorm.weight"], eps)
-    q = (n @ f64(p + "self_attn.q_proj.linear.weight").T).reshape(valid, NH, hd)
-    k = (n @ f64(p + "self_attn.k_proj.linear.weight").T).reshape(valid, NKV, hd)
-    v = (n @ f64(p + "self_attn.v_proj.linear.weight").T).reshape(valid, NKV, hd)
-    q = ref64.axial_rope64(ref64.rms(q, w[p + "self_attn.q_norm.weight"], eps), pos, inv)
-    k = ref64.axial_rope64(ref64.rms(k, w[p + "self_attn.k_norm.weight"], eps), pos, inv)
-    v = ref64.rms(v, None, eps)
-    out = np.zeros((valid, NH, hd))
-    for hh in range(NH):
-        g = hh // (NH // NKV)
-        s = q[:, hh] @ k[:, g].T
-        pr = np.exp(s - s.max(1, keepdims=True))
-        out[:, hh] = (pr / pr.sum(1, keepdims=True)) @ v[:, g]
-    a = out.reshape(valid, NH * hd) @ f64(p + "self_attn.o_proj.linear.weight").T
-    h = h + ref64.rms(a, w[p + "post_attention_layernorm.weight"], eps)
-    n = ref64.rms(h, w[p + "pre_feedforward_layernorm.weight"], eps)
-    act = ref64.gelu(n @ f64(p + "mlp.gate_proj.linear.weight").T) * \
-        (n @ f64(p + "mlp.up_proj.linear.weight").T)
-    return h + ref64.rms(act @ f64(p + "mlp.down_proj.linear.weight").T,
-                         w[p + "post_feedforward_layernorm.weight"], eps)
+def test_full_size_image_prompt_through_the_text_encoder(full_v):
+    """The 260-token image prompt of one 768 x 768 image through the 24-layer
+    shape-A text encoder (vocab 262144, the reference's special-token ids)
+    against the text oracle run on the GPU tower's own soft tokens
+    (image.rs:209-253), at Matryoshka dims 768 and 128."""
+    c, w, gpu, p, out = full_v
+    tc = svl_synth.config_a()
+    tw = svl_synth.weights(tc, seed=0)
+    tm = S.TextModel(S.TextConfig.from_json_value(tc), tw)
+    tokens = V.ImageSpecialTokens()
+    emb = V.ImageEmbedder(tm, gpu, tokens)
+    got = {d: emb.embed_patches(p, d) for d in (768, 128)}
+    ids = [tokens.bos, tokens.boi] + [tokens.image] * 256 + [tokens.eoi, tokens.eos]
+    ref = O.OracleTextModel(tc, tw).forward(ids, features=out.pooled(), feature_start=2,
+                                            feature_count=256)["normalized"]
+    for d in (768, 128):
+        r = O.truncate_and_normalize(ref, d)
+        diff = float(np.abs(got[d] - r).max())
+        c_ = cosine(got[d], r)
+        print(f"260-token image prompt dim {d}: max-abs {diff:.3g} cosine {c_:.9f}", flush=True)
+        assert diff <= MAX_ABS and c_ >= MIN_COS
+    tm.close()
+
+
+def test_four_full_size_images_equal_single_calls(full_v):
+    """A batch of four 768 x 768 images through the 16-layer tower returns,
+    image by image, the bits of four single calls."""
+    c, w, gpu, p, out = full_v
+    patches = [p] + svl_synth.image_patches(3, 48, 48, seed=5)
+    batch = gpu.forward_batch(patches)
+    assert np.array_equal(batch[0].pooled(), out.pooled())
+    for i in (1, 3):
+        assert np.array_equal(batch[i].pooled(), gpu.forward(patches[i]).pooled()), i
 
 
 # ---- image prompt glue ----------------------------------------------------------------
