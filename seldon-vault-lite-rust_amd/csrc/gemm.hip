@@ -133,9 +133,12 @@ __device__ __forceinline__ void store_pair(const GemmArgs &p, int limit, bool ve
     if (ra + 8 < p.M) store_cols4(p.C + (int64_t)(ra + 8) * p.ldc, col, limit, vec, lo ? t : Y);
 }
 
+// aux_pre (EPI_GELU_MUL, optional): the aux values of every accumulator
+// element, loaded by the caller ahead of the K loop (aux_load below).
 template <int TM, int TN, int EPI>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x4 (&acc)[TM][TN],
-                                              int mw, int nw, int l16, int g, int seg) {
+                                              int mw, int nw, int l16, int g, int seg,
+                                              const f32x4 (*aux_pre)[TN] = nullptr) {
     float olo = 0.f, ohi = 0.f;
     if constexpr (clipped_epi<EPI>()) {
         olo = p.clip[seg][2];
@@ -169,8 +172,14 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x4 (&a
                 for (int u = 0; u < 2; ++u) {
                     const int n0 = nw + (j + u) * 16 + 4 * g;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
+                    for (int r = 0; r < 4; ++r) {
+                        if constexpr (EPI == EPI_GELU_MUL)
+                            if (aux_pre) {
+                                v[u][r] = gelu_tanh(acc[i][j + u][r]) * aux_pre[i][j + u][r];
+                                continue;
+                            }
                         v[u][r] = epi_value<EPI>(p, acc[i][j + u][r], m, n0 + r, olo, ohi);
+                    }
                 }
                 store_pair(p, p.N, vec, mw + i * 16, nw + j * 16, l16, g, v[0], v[1]);
             }
@@ -182,9 +191,46 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &p, const f32x4 (&a
                 const int n0 = nw + j * 16 + 4 * g;
                 f32x4 v;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) v[r] = epi_value<EPI>(p, acc[i][j][r], m, n0 + r, olo, ohi);
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (EPI == EPI_GELU_MUL)
+                        if (aux_pre) {
+                            v[r] = gelu_tanh(acc[i][j][r]) * aux_pre[i][j][r];
+                            continue;
+                        }
+                    v[r] = epi_value<EPI>(p, acc[i][j][r], m, n0 + r, olo, ohi);
+                }
                 store_cols4(crow, n0, p.N, vec, v);
             }
+        }
+    }
+}
+
+// EPI_GELU_MUL: the aux values of a wave's TM x TN accumulator blocks (row
+// mw + 16 i + l16, columns nw + 16 j + 4 g .. + 3), one float4 per block
+// where the row is 16-byte aligned, zero outside the output. Loaded before
+// the K loop, so their latency hides behind it instead of following it.
+template <int TM, int TN>
+__device__ __forceinline__ void aux_load(const GemmArgs &p, int mw, int nw, int l16, int g,
+                                         f32x4 (&out)[TM][TN]) {
+    const bool vec = (p.ldaux & 3) == 0 && ((uintptr_t)p.aux & 15) == 0;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int m = mw + i * 16 + l16;
+        const float *row = p.aux + (int64_t)(m < p.M ? m : 0) * p.ldaux;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = nw + j * 16 + 4 * g;
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (m < p.M) {
+                if (vec && n + 3 < p.N) {
+                    v = *(const f32x4 *)(row + n);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (n + r < p.N) v[r] = row[n + r];
+                }
+            }
+            out[i][j] = v;
         }
     }
 }
@@ -496,6 +542,11 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     using S1 = std::integral_constant<int, 1>;
     using S2 = std::integral_constant<int, 2>;
     using S3 = std::integral_constant<int, 3>;
+    // EPI_GELU_MUL: the per-layer inputs of this wave's outputs, ahead of the
+    // K loop (loaded before the first DMA: the loop's vmcnt waits, which
+    // count only the DMAs issued after them, then also cover these loads)
+    f32x4 auxv[EPI == EPI_GELU_MUL ? TM : 1][EPI == EPI_GELU_MUL ? TN : 1];
+    if constexpr (EPI == EPI_GELU_MUL) aux_load<TM, TN>(p, m0 + wm * WTM, n0 + wn * WTN, l16, g, auxv);
     if (0 < nk) issue(S0{}, 0);
     if constexpr (NS > 2) if (1 < nk) issue(S1{}, BK);
     if constexpr (NS > 3) if (2 < nk) issue(S2{}, 2 * BK);
@@ -598,6 +649,8 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
         }
         __syncthreads();
         if (wn == 0) gemm_epilogue_pair_split<TM, EPI>(p, acc, xch, m0 + wm * WTM, n0, l16, g);
+    } else if constexpr (EPI == EPI_GELU_MUL) {
+        gemm_epilogue<TM, TN, EPI>(p, acc, m0 + wm * WTM, n0 + wn * WTN, l16, g, seg, auxv);
     } else {
         gemm_epilogue<TM, TN, EPI>(p, acc, m0 + wm * WTM, n0 + wn * WTN, l16, g, seg);
     }
@@ -729,7 +782,9 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
             if (a.K % 64 == 0) return launch_dma<32, 64, 64, EPI, 1, 3, 2>(a, s);
             return launch_dma<32, 64, 32, EPI, 1, 4, 2>(a, s);
         }
-        if (a.cus > 0 && a.K % 32 == 0) return launch_dma<64, 128, 32, EPI, 3, 2>(a, s);
+        // concurrent row groups: 128x128 tiles at three per CU (the T2 step
+        // 39.66 against 39.9 ms with 64x128x32 tiles, same box)
+        if (a.cus > 0 && a.K % 16 == 0) return launch_dma<128, 128, 16, EPI, 3, 2>(a, s);
         if (tiles(128, 128) < 2 * 256) {
             // grids of a few thousand rows: tiles small enough to spread over
             // every CU (gate/up at 1040 / 2000 / 3016 rows: 34.7 / 63.8 / 88.0
@@ -749,6 +804,11 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
             if (a.K % 64 == 0) return launch_dma<32, 32, 64, EPI, 1, 3>(a, s);
             return launch_dma<32, 32, 32, EPI, 1, 4>(a, s);
         }
+        // The PLE gate (N = 256, K = 768, GELU x per-layer input): 64x32 tiles
+        // at six per CU, whole batch or row group (T2 whole batch 68 against
+        // 76 us for 64x64 tiles; three row groups together 62 against 66-73 us)
+        if constexpr (EPI == EPI_GELU_MUL)
+            if (a.K % 32 == 0) return launch_dma<64, 32, 32, EPI, 6, 2, 2>(a, s);
         if (a.cus > 0) {
             if (a.K % 32 == 0) return launch_dma<64, 64, 32, EPI, 4, 2>(a, s);
             if (tiles(128, 128) < 4 * 256) return launch_dma_staged<128, 64, 16, EPI, 4, 3>(a, s);
