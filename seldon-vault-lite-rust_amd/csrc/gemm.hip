@@ -32,9 +32,11 @@
 //    128x128 (3 workgroups per CU) for large grids, 128x64 or 64x64 (4 per
 //    CU) when bigger tiles would leave CUs idle or unevenly loaded, 32x32
 //    when even 64x64 tiles would not cover the GPU once.
-//  * Tiles are numbered M-major with N fastest and remapped so consecutive
-//    tiles land on the same XCD: the N tiles that share an A block hit that
-//    XCD's L2 instead of HBM.
+//  * Tiles are remapped so each XCD runs a contiguous range of the tile
+//    list, N fastest (the N tiles that share an A block hit that XCD's L2);
+//    launches of 128 M blocks or more with the whole GPU order the range in
+//    groups of 8 M blocks, M fastest within an N block, so the tiles in
+//    flight on an XCD share a few A blocks and W panels.
 //  * Epilogues fuse the elementwise op that follows each projection in
 //    text.rs (PLE scale, GeGLU, GELU-gate x per-layer input).
 #include <algorithm>
@@ -363,10 +365,17 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
     gemm_epilogue<S::TM, S::TN, EPI>(p, acc, m0 + wm * S::WM, n0 + wn * S::WN, l16, g, seg);
 }
 
+// M blocks per rasterization group of the DMA kernel's tile order, and the
+// fewest M blocks of a whole-GPU launch that takes the grouped order (the
+// 1 x 128-token forward went from 2.00 to 2.04 ms and the audio tower lost
+// 1 % with it; the T2 launches kept their time and fetched 2.6x less).
+constexpr int RASTER_M = 8, RASTER_MIN_TILES_M = 128;
+
 // Direct-to-LDS variant; requires K % BK == 0 and 16-byte aligned rows. NS
 // LDS stages: NS - 1 slices are in flight while one is consumed. WMW waves
 // along M, 4 / WMW along N.
-template <int BM, int BN, int BK, int EPI, int MINB, int NS, int WMW, bool CONV = false>
+template <int BM, int BN, int BK, int EPI, int MINB, int NS, int WMW, bool CONV = false,
+          bool RASTER = false>
 __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m, int tiles_n) {
 #if defined(__HIP_DEVICE_COMPILE__)
     constexpr int WNW = 4 / WMW;                // waves along N
@@ -418,7 +427,20 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
     const int xcd = bid & 7, local = bid >> 3;
     const int q8 = ntiles >> 3, r8 = ntiles & 7;
     const int tile = xcd * q8 + min(xcd, r8) + local;
-    const int tm = uniform(tile / tiles_n), tn = tile - tm * tiles_n;
+    int tm, tn;
+    if constexpr (RASTER) {
+        // Within that range, groups of RASTER_M M blocks run N block by N
+        // block, M fastest: the tiles in flight together on an XCD then share
+        // a few W panels and A blocks in its L2 (the T2 gate/up launch fetched
+        // 188 against 491 MiB with N fastest, at the same speed).
+        const int gsize = RASTER_M * tiles_n, grp = tile / gsize, first = grp * RASTER_M;
+        const int gm = min(RASTER_M, tiles_m - first), in = tile - grp * gsize;
+        tm = uniform(first + in % gm);
+        tn = uniform(in / gm);
+    } else {
+        tm = uniform(tile / tiles_n);
+        tn = tile - tm * tiles_n;
+    }
     const int m0 = tm * BM, n0 = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WNW, wn = wave % WNW;
@@ -711,6 +733,13 @@ __global__ __launch_bounds__(256) void gemm_nt_simple(GemmArgs p) {
 template <int BM, int BN, int BK, int EPI, int MINB, int NS, int WMW = 2, bool CONV = false>
 static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
     const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
+    if constexpr (!CONV) {
+        if (a.cus == 0 && tm >= RASTER_MIN_TILES_M) {
+            hipLaunchKernelGGL((gemm_nt_dma<BM, BN, BK, EPI, MINB, NS, WMW, false, true>),
+                               dim3(tm * tn), dim3(256), 0, s, a, tm, tn);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((gemm_nt_dma<BM, BN, BK, EPI, MINB, NS, WMW, CONV>), dim3(tm * tn),
                        dim3(256), 0, s, a, tm, tn);
     return hipGetLastError();
