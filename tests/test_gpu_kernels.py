@@ -119,7 +119,9 @@ def test_attention_kats():  # kernels.rs:1529-1566
     (97, 4, 2, 256, 8), (64, 12, 12, 64, None), (50, 8, 8, 128, 7), (33, 4, 1, 512, None),
     (21, 2, 1, 8, 2), (9, 2, 1, 16, None), (300, 4, 4, 64, 40), (131, 6, 2, 128, None),
     (1000, 3, 1, 256, 100), (700, 4, 1, 512, None), (300, 8, 2, 512, 40), (1000, 4, 1, 512, 100),
-    (5, 4, 1, 512, None), (129, 2, 2, 512, 3), (2000, 3, 1, 256, 512), (900, 4, 4, 128, 64)])
+    (5, 4, 1, 512, None), (129, 2, 2, 512, 3), (2000, 3, 1, 256, 512), (900, 4, 4, 128, 64),
+    # head_dim 512 with 128 and with 64 work items: the 8-wave and the 4-wave variants
+    (2048, 8, 2, 512, None), (1024, 8, 2, 512, 40)])
 def test_attention_matches_oracle(seq, nh, nkv, hd, window):
     rng = np.random.default_rng(seq + hd)
     # unit-RMS rows scaled like q/k after their norms (weights ~0.25)
