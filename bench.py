@@ -486,7 +486,7 @@ def search_leg(dev, steps, cpu_sample=True):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+        print(f"bench.py: the benchmark runs on one GPU; --gpus {args.gpus} is not supported "
               f"(rows are independent and would shard by data parallelism)",
               file=sys.stderr)
         sys.exit(2)

@@ -1,6 +1,7 @@
 """ctypes binding of the CPU oracle (oracle/svl_oracle.c).
 
-TEST INFRASTRUCTURE ONLY: this module is the checker. Only tests/, the smoke
+TEST INFRASTRUCTURE ONLY: this module is the oracle that the HIP path is
+compared against. Only tests/, the smoke
 check in __graft_entry__.py and the CPU-baseline leg of bench.py import it;
 the product library never does.
 

@@ -1,7 +1,7 @@
 /*
  * CPU oracle: a C restatement of the reference crate's scalar FP32 path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP path, never part of the
+ * TEST INFRASTRUCTURE ONLY: the oracle for the HIP path, never part of the
  * product library. Built with -O2 -ffp-contract=off and no fast-math so that
  * every f32 operation is rounded in the same order as the Rust scalar code.
  *

@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the EmbeddingGemma-2 text encoder forward pass.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker that the HIP path is
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle that the HIP path is
  * compared against; it is never linked into, loaded by, or called from the
  * product library. Only tests, the smoke check and the CPU-baseline leg of
  * bench.py load it.

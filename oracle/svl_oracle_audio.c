@@ -1,7 +1,7 @@
 /*
  * CPU oracle, audio tower: a C restatement of src/model/audio.rs.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP audio path, never part of
+ * TEST INFRASTRUCTURE ONLY: the oracle for the HIP audio path, never part of
  * the product library. Same build rules as svl_oracle.c (-O2,
  * -ffp-contract=off, no fast-math); the reference's f32 operations are
  * evaluated in its order with the platform libm (expf, logf, tanhf, sinf,

@@ -3,7 +3,7 @@
  * src/media/audio_preprocess.rs (log_mel :94-200, hann_window :203-210,
  * mel_filter_bank :212-244, the radix-2 FftPlan :279-333).
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP log-mel kernel, never part
+ * TEST INFRASTRUCTURE ONLY: the oracle for the HIP log-mel kernel, never part
  * of the product library. Built with -ffp-contract=off and no fast-math; the
  * FFT, the magnitudes and the mel projection run in double in the reference's
  * order with the platform libm (cos, sin, pow, log10, log), and each feature

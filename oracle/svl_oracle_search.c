@@ -2,7 +2,7 @@
  * CPU oracle, exact vector search: a C restatement of vector::rank
  * (src/index/vector.rs:17-97).
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP cosine ranking, never part
+ * TEST INFRASTRUCTURE ONLY: the oracle for the HIP cosine ranking, never part
  * of the product library. Built with -ffp-contract=off: the dot product and
  * the squared norms are accumulated in double in dimension order with a
  * separate multiply and add, as the reference does; the ranking is sorted by

@@ -1,7 +1,7 @@
 /*
  * CPU oracle, vision tower: a C restatement of src/model/vision.rs.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP vision path, never part
+ * TEST INFRASTRUCTURE ONLY: the oracle for the HIP vision path, never part
  * of the product library. Same build rules as svl_oracle.c (-O2,
  * -ffp-contract=off, no fast-math) and the same kernels (svlo_linear,
  * svlo_rms_norm_rows, svlo_bidirectional_attention, ...).

@@ -1,6 +1,6 @@
 """CPU oracle, tokenizer: a pure-Python restatement of src/model/tokenizer.rs.
 
-TEST INFRASTRUCTURE ONLY: the checker for the library's C++ tokenizer, never
+TEST INFRASTRUCTURE ONLY: the oracle for the library's C++ tokenizer, never
 part of the product. It follows the reference step by step, including its
 quadratic merge loop (best_merge scans every adjacent pair, then one
 left-to-right pass merges every occurrence; tokenizer.rs:497-552), so it is
