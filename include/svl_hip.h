@@ -176,6 +176,17 @@ svl_status svl_measure_fp64_peak(svl_ctx *ctx, double *fp64_mfma_tflops);
  * as one group on one stream. Results are bit-identical for any setting. */
 svl_status svl_text_model_set_stream_split(svl_text_model *model, int groups);
 
+/* Every forward entry point (svl_text_forward_batch, svl_text_forward_device,
+ * the image and audio prompts) runs a batch as passes of consecutive rows of
+ * at most `tokens` tokens each, one after another (a longer row runs alone),
+ * so the device workspace stays bounded whatever the batch: row r of every
+ * output still equals TextModel::forward(row r), bit for bit, like the
+ * reference's loop over rows (text.rs:150-180). 0 (the default) sizes passes
+ * to about 32 GiB of workspace (677,617 tokens at EmbeddingGemma's shape).
+ * Usage error outside 0..=268435455. No counterpart in the reference, which
+ * holds one row at a time. */
+svl_status svl_text_model_set_pass_tokens(svl_text_model *model, int64_t tokens);
+
 /* Per-kernel GPU time of the last forward call, when enabled: one entry per
  * kernel class (see svl_kernel_class_name). Used by the benchmark to relate
  * a kernel's algorithmic work to its measured duration. */

@@ -104,6 +104,7 @@ struct svl_text_model {
     hipStream_t extra[MAX_GROUPS - 1] = {};  // streams of row groups 1..3
     hipEvent_t ev_fork = nullptr, ev_join[MAX_GROUPS - 1] = {};
     int row_groups = 3;                      // row groups per large batch
+    int64_t pass_tokens = 0;                 // tokens per pass (0: from PASS_BYTES)
     std::mutex mu;
 
     // workspace
@@ -348,6 +349,7 @@ struct Batch {
     std::vector<int64_t> dev_offsets;  // per group: nrows + 1 offsets rebased to the group
     std::vector<AttnTile> tiles;       // all groups, tok0 relative to the group
     std::vector<Group> groups;
+    int64_t hidden_stride = 0;         // tokens per layer block of captured states (0: T)
 };
 
 void build_group(const svl_text_model *m, Batch &b, Group &g) {
@@ -489,7 +491,7 @@ svl_status enqueue_group(svl_text_model *m, const Batch &b, const Group &grp, hi
     float *proj = m->proj.p + t0 * E;
     int32_t *pos = m->pos.p + t0, *rowlen = m->rowlen.p + t0;
     const int64_t *offs = m->offsets.p + grp.off_slot;
-    const int64_t T_all = b.T;
+    const int64_t T_all = b.hidden_stride > 0 ? b.hidden_stride : b.T;
     // CUs each launch can expect while the batch's groups run side by side
     const int cus = b.groups.size() > 1 ? (int)(256 / b.groups.size()) : 0;
 
@@ -699,18 +701,54 @@ svl_status finish(svl_text_model *m, hipStream_t s) {
     return SVL_OK;
 }
 
-svl_status prepare_batch(svl_text_model *m, const int64_t *offsets, int32_t batch, Batch &b) {
+svl_status check_offsets(const int64_t *offsets, int32_t batch) {
     if (batch < 0) return fail(SVL_USAGE, "negative batch");
     if (!offsets) return fail(SVL_USAGE, "offsets are null");
     if (offsets[0] != 0) return fail(SVL_USAGE, "offsets must start at 0");
-    b.B = batch;
-    b.offsets.assign(offsets, offsets + batch + 1);
     for (int r = 0; r < batch; ++r)
         if (offsets[r + 1] < offsets[r]) return fail(SVL_USAGE, "offsets must not decrease");
-    b.T = offsets[batch];
+    return SVL_OK;
+}
+
+// One pass over rows r0 .. r1 - 1 of a checked batch (offsets rebased to the
+// pass's first token).
+svl_status prepare_batch(svl_text_model *m, const int64_t *offsets, int32_t r0, int32_t r1,
+                         Batch &b) {
+    b.B = r1 - r0;
+    b.offsets.resize((size_t)b.B + 1);
+    for (int32_t r = r0; r <= r1; ++r) b.offsets[(size_t)(r - r0)] = offsets[r] - offsets[r0];
+    b.T = b.offsets.back();
     if (b.T > (int64_t)INT32_MAX / 8) return fail(SVL_LIMIT, "batch holds too many tokens");
     build_groups(m, b, m->row_groups);
     return SVL_OK;
+}
+
+// Every workspace buffer grows with the batch's tokens, so a batch runs in
+// passes of consecutive rows whose workspace stays within PASS_BYTES (a row
+// longer than a pass runs alone). Rows are independent and a row's bits do
+// not depend on the rows beside it, so the outputs equal those of one pass.
+constexpr int64_t PASS_BYTES = (int64_t)32 << 30;
+constexpr int64_t MAX_PASS_TOKENS = (int64_t)INT32_MAX / 8;
+
+int64_t pass_token_budget(const svl_text_model *m) {
+    if (m->pass_tokens > 0) return m->pass_tokens;
+    const int64_t per_token =
+        4 * (3 * m->H + m->max_qkv + m->max_q + m->I + m->L * m->P + m->P + m->E + 4);
+    return std::min(MAX_PASS_TOKENS, std::max(MAX_TEXT_TOKENS, PASS_BYTES / per_token));
+}
+
+std::vector<std::pair<int32_t, int32_t>> row_passes(const svl_text_model *m,
+                                                    const int64_t *offsets, int32_t batch) {
+    std::vector<std::pair<int32_t, int32_t>> passes;
+    const int64_t cap = pass_token_budget(m);
+    int32_t r0 = 0;
+    for (int32_t r = 0; r < batch; ++r)
+        if (r > r0 && offsets[r + 1] - offsets[r0] > cap) {
+            passes.emplace_back(r0, r);
+            r0 = r;
+        }
+    if (batch > 0) passes.emplace_back(r0, batch);
+    return passes;
 }
 
 svl_status upload_batch_meta(svl_text_model *m, const Batch &b, hipStream_t s) {
@@ -792,23 +830,30 @@ svl_status text_forward_with_device_features(svl_text_model *m, const uint32_t *
                                              float *out_normalized) {
     std::lock_guard<std::mutex> lock(m->mu);
     HIP_TRY(hipSetDevice(m->device));
-    Batch b;
-    ST_TRY(prepare_batch(m, offsets, batch, b));
+    ST_TRY(check_offsets(offsets, batch));
     if (batch == 0) return SVL_OK;
     for (int r = 0; r < batch; ++r)
         ST_TRY(validate_row(m, r, ids + offsets[r], offsets[r + 1] - offsets[r]));
     if (m->pad < 0)
         return fail(SVL_UNSUPPORTED, "model has no padding token for multimodal inputs");
-    ST_TRY(ensure_workspace(m, b, 0, true, 0));
-    hipStream_t s = m->stream;
-    HIP_TRY(hipMemcpyAsync(m->ids.p, ids, (size_t)b.T * 4, hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(m->featmap.p, featmap, (size_t)b.T * 4, hipMemcpyHostToDevice, s));
-    ST_TRY(upload_batch_meta(m, b, s));
-    ST_TRY(enqueue_forward(m, b, s, m->ids.p, m->featmap.p, d_feats, nullptr, 0, 0, nullptr,
-                           nullptr));
-    HIP_TRY(hipMemcpyAsync(out_normalized, m->normalized.p, (size_t)(batch * m->E) * 4,
-                           hipMemcpyDeviceToHost, s));
-    return finish(m, s);
+    // featmap holds rows of d_feats, so a pass reads its tokens' entries as they are
+    for (const auto &pr : row_passes(m, offsets, batch)) {
+        const int64_t t0 = offsets[pr.first];
+        Batch b;
+        ST_TRY(prepare_batch(m, offsets, pr.first, pr.second, b));
+        ST_TRY(ensure_workspace(m, b, 0, true, 0));
+        hipStream_t s = m->stream;
+        HIP_TRY(hipMemcpyAsync(m->ids.p, ids + t0, (size_t)b.T * 4, hipMemcpyHostToDevice, s));
+        HIP_TRY(hipMemcpyAsync(m->featmap.p, featmap + t0, (size_t)b.T * 4,
+                               hipMemcpyHostToDevice, s));
+        ST_TRY(upload_batch_meta(m, b, s));
+        ST_TRY(enqueue_forward(m, b, s, m->ids.p, m->featmap.p, d_feats, nullptr, 0, 0, nullptr,
+                               nullptr));
+        HIP_TRY(hipMemcpyAsync(out_normalized + (size_t)pr.first * m->E, m->normalized.p,
+                               (size_t)(b.B * m->E) * 4, hipMemcpyDeviceToHost, s));
+        ST_TRY(finish(m, s));
+    }
+    return SVL_OK;
 }
 
 }  // namespace svl
@@ -986,17 +1031,14 @@ svl_status svl_text_forward_batch(svl_text_model *m, const uint32_t *ids, const 
         return fail(SVL_USAGE, "model, ids, offsets and out_normalized are required");
     std::lock_guard<std::mutex> lock(m->mu);
     HIP_TRY(hipSetDevice(m->device));
-    Batch b;
-    ST_TRY(prepare_batch(m, offsets, batch, b));
+    ST_TRY(check_offsets(offsets, batch));
     if (batch == 0) return SVL_OK;
     for (int r = 0; r < batch; ++r)
         ST_TRY(validate_row(m, r, ids + offsets[r], offsets[r + 1] - offsets[r]));
 
-    // Multimodal feature spans (text.rs:226-275).
-    int64_t feat_floats = 0;
-    std::vector<int32_t> featmap;
+    // Multimodal feature spans (text.rs:226-275), every row checked before
+    // any pass runs.
     if (features) {
-        featmap.assign((size_t)b.T, -1);
         for (int r = 0; r < batch; ++r) {
             const svl_feature_span &f = features[r];
             if (!f.data) continue;
@@ -1014,40 +1056,61 @@ svl_status svl_text_forward_batch(svl_text_model *m, const uint32_t *ids, const 
                             r, (long long)f.len, (long long)(f.count * m->H));
             if (m->pad < 0)
                 return fail(SVL_UNSUPPORTED, "model has no padding token for multimodal inputs");
-            for (int64_t i = 0; i < f.count; ++i)
-                featmap[(size_t)(offsets[r] + f.start + i)] = (int32_t)(feat_floats / m->H + i);
-            feat_floats += f.len;
         }
-        if (feat_floats == 0) featmap.clear();
     }
-    ST_TRY(ensure_workspace(m, b, feat_floats, feat_floats > 0, 0));
-    hipStream_t s = m->stream;
-    HIP_TRY(hipMemcpyAsync(m->ids.p, ids, (size_t)b.T * 4, hipMemcpyHostToDevice, s));
-    if (feat_floats > 0) {
-        HIP_TRY(hipMemcpyAsync(m->featmap.p, featmap.data(), featmap.size() * 4,
-                               hipMemcpyHostToDevice, s));
-        int64_t off = 0;
-        for (int r = 0; r < batch; ++r) {
-            const svl_feature_span &f = features[r];
-            if (!f.data) continue;
-            HIP_TRY(hipMemcpyAsync(m->feats.p + off, f.data, (size_t)f.len * 4,
+
+    const int64_t T_all = offsets[batch];
+    for (const auto &pr : row_passes(m, offsets, batch)) {
+        const int32_t r0 = pr.first, r1 = pr.second;
+        const int64_t t0 = offsets[r0];
+        Batch b;
+        ST_TRY(prepare_batch(m, offsets, r0, r1, b));
+        b.hidden_stride = T_all;
+        // per token of the pass: its row of the pass's feature values, or -1
+        int64_t feat_floats = 0;
+        std::vector<int32_t> featmap;
+        if (features) {
+            featmap.assign((size_t)b.T, -1);
+            for (int r = r0; r < r1; ++r) {
+                const svl_feature_span &f = features[r];
+                if (!f.data) continue;
+                for (int64_t i = 0; i < f.count; ++i)
+                    featmap[(size_t)(offsets[r] - t0 + f.start + i)] =
+                        (int32_t)(feat_floats / m->H + i);
+                feat_floats += f.len;
+            }
+            if (feat_floats == 0) featmap.clear();
+        }
+        ST_TRY(ensure_workspace(m, b, feat_floats, feat_floats > 0, 0));
+        hipStream_t s = m->stream;
+        HIP_TRY(hipMemcpyAsync(m->ids.p, ids + t0, (size_t)b.T * 4, hipMemcpyHostToDevice, s));
+        if (feat_floats > 0) {
+            HIP_TRY(hipMemcpyAsync(m->featmap.p, featmap.data(), featmap.size() * 4,
                                    hipMemcpyHostToDevice, s));
-            off += f.len;
+            int64_t off = 0;
+            for (int r = r0; r < r1; ++r) {
+                const svl_feature_span &f = features[r];
+                if (!f.data) continue;
+                HIP_TRY(hipMemcpyAsync(m->feats.p + off, f.data, (size_t)f.len * 4,
+                                       hipMemcpyHostToDevice, s));
+                off += f.len;
+            }
         }
+        ST_TRY(upload_batch_meta(m, b, s));
+        ST_TRY(enqueue_forward(m, b, s, m->ids.p, feat_floats > 0 ? m->featmap.p : nullptr,
+                               feat_floats > 0 ? m->feats.p : nullptr, nullptr, 0, 0, nullptr,
+                               out_hidden ? out_hidden + (size_t)t0 * m->H : nullptr));
+        HIP_TRY(hipMemcpyAsync(out_normalized + (size_t)r0 * m->E, m->normalized.p,
+                               (size_t)(b.B * m->E) * 4, hipMemcpyDeviceToHost, s));
+        if (out_pooled)
+            HIP_TRY(hipMemcpyAsync(out_pooled + (size_t)r0 * m->E, m->pooled.p,
+                                   (size_t)(b.B * m->E) * 4, hipMemcpyDeviceToHost, s));
+        if (out_projected)
+            HIP_TRY(hipMemcpyAsync(out_projected + (size_t)t0 * m->E, m->proj.p,
+                                   (size_t)(b.T * m->E) * 4, hipMemcpyDeviceToHost, s));
+        ST_TRY(finish(m, s));
     }
-    ST_TRY(upload_batch_meta(m, b, s));
-    ST_TRY(enqueue_forward(m, b, s, m->ids.p, feat_floats > 0 ? m->featmap.p : nullptr,
-                           feat_floats > 0 ? m->feats.p : nullptr, nullptr, 0, 0, nullptr,
-                           out_hidden));
-    HIP_TRY(hipMemcpyAsync(out_normalized, m->normalized.p, (size_t)(batch * m->E) * 4,
-                           hipMemcpyDeviceToHost, s));
-    if (out_pooled)
-        HIP_TRY(hipMemcpyAsync(out_pooled, m->pooled.p, (size_t)(batch * m->E) * 4,
-                               hipMemcpyDeviceToHost, s));
-    if (out_projected)
-        HIP_TRY(hipMemcpyAsync(out_projected, m->proj.p, (size_t)(b.T * m->E) * 4,
-                               hipMemcpyDeviceToHost, s));
-    return finish(m, s);
+    return SVL_OK;
 }
 
 svl_status svl_text_forward_device(svl_text_model *m, const uint32_t *d_ids,
@@ -1064,19 +1127,24 @@ svl_status svl_text_forward_device(svl_text_model *m, const uint32_t *d_ids,
                         (long long)m->E);
         dims_total += dims[i];
     }
-    Batch b;
-    ST_TRY(prepare_batch(m, offsets, batch, b));
+    ST_TRY(check_offsets(offsets, batch));
     if (batch == 0) return SVL_OK;
     for (int r = 0; r < batch; ++r)
         ST_TRY(validate_row(m, r, nullptr, offsets[r + 1] - offsets[r]));
-    ST_TRY(ensure_workspace(m, b, 0, false, dims_total));
     HIP_TRY(m->dims.ensure(n_dims));
     hipStream_t s = stream ? (hipStream_t)stream : m->stream;
     HIP_TRY(hipMemcpyAsync(m->dims.p, dims, n_dims * 4, hipMemcpyHostToDevice, s));
-    ST_TRY(upload_batch_meta(m, b, s));
-    ST_TRY(enqueue_forward(m, b, s, d_ids, nullptr, nullptr, m->dims.p, n_dims, dims_total, d_out,
-                           nullptr));
-    return finish(m, s);
+    for (const auto &pr : row_passes(m, offsets, batch)) {
+        Batch b;
+        ST_TRY(prepare_batch(m, offsets, pr.first, pr.second, b));
+        ST_TRY(ensure_workspace(m, b, 0, false, dims_total));
+        ST_TRY(upload_batch_meta(m, b, s));
+        ST_TRY(enqueue_forward(m, b, s, d_ids + offsets[pr.first], nullptr, nullptr, m->dims.p,
+                               n_dims, dims_total, d_out + (size_t)pr.first * dims_total,
+                               nullptr));
+        ST_TRY(finish(m, s));
+    }
+    return SVL_OK;
 }
 
 svl_status svl_truncate_and_normalize(const float *values, size_t n, size_t dimension,
@@ -1154,6 +1222,16 @@ svl_status svl_text_model_set_stream_split(svl_text_model *m, int enable) {
     if (!m) return fail(SVL_USAGE, "model is null");
     std::lock_guard<std::mutex> lock(m->mu);
     m->row_groups = std::max(1, std::min(enable, svl_text_model::MAX_GROUPS));
+    return SVL_OK;
+}
+
+svl_status svl_text_model_set_pass_tokens(svl_text_model *m, int64_t tokens) {
+    if (!m) return fail(SVL_USAGE, "model is null");
+    if (tokens < 0 || tokens > MAX_PASS_TOKENS)
+        return fail(SVL_USAGE, "pass size %lld is outside 0..=%lld tokens", (long long)tokens,
+                    (long long)MAX_PASS_TOKENS);
+    std::lock_guard<std::mutex> lock(m->mu);
+    m->pass_tokens = tokens;
     return SVL_OK;
 }
 

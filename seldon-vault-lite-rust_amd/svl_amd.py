@@ -95,7 +95,7 @@ EXPORTED = [
     "svl_init", "svl_shutdown", "svl_last_error", "svl_text_model_create",
     "svl_text_model_destroy", "svl_text_forward_batch", "svl_text_forward_device",
     "svl_text_embed_ids", "svl_truncate_and_normalize", "svl_text_model_set_stream_split",
-    "svl_text_model_set_kernel_timing",
+    "svl_text_model_set_pass_tokens", "svl_text_model_set_kernel_timing",
     "svl_kernel_class_count", "svl_kernel_class_name", "svl_text_model_kernel_stats",
     "svl_linear", "svl_rms_norm_rows", "svl_rope_with_inv_freq", "svl_rope_inv_freq",
     "svl_bidirectional_attention", "svl_gelu_tanh", "svl_geglu", "svl_add", "svl_mean_pool",
@@ -171,6 +171,7 @@ def lib():
         L.svl_measure_fp64_peak.argtypes = [vp, ctypes.POINTER(ctypes.c_double)]
         L.svl_text_model_set_kernel_timing.argtypes = [vp, ctypes.c_int]
         L.svl_text_model_set_stream_split.argtypes = [vp, ctypes.c_int]
+        L.svl_text_model_set_pass_tokens.argtypes = [vp, i64]
         L.svl_text_model_kernel_stats.argtypes = [vp, vp, vp, vp]
         L.svl_linear.argtypes = [vp, vp, i64, i64, i64, vp, vp]
         L.svl_rms_norm_rows.argtypes = [vp, vp, i64, i64, f32, vp, vp]
@@ -707,6 +708,11 @@ class TextModel:
         g = 3 if groups is True else (1 if groups is False else int(groups))
         _check(lib().svl_text_model_set_stream_split(self.handle, g))
         self.row_groups = max(1, min(g, 4))
+
+    def set_pass_tokens(self, tokens: int):
+        """Largest pass of consecutive rows a batch runs in (0: sized to about
+        32 GiB of device workspace); results do not depend on it."""
+        _check(lib().svl_text_model_set_pass_tokens(self.handle, int(tokens)))
 
     def set_kernel_timing(self, enable: bool):
         _check(lib().svl_text_model_set_kernel_timing(self.handle, 1 if enable else 0))

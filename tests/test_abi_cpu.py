@@ -54,6 +54,13 @@ def test_attention_path_hook_rejects_unknown_paths():
     svl_amd.set_attention_path("auto")
 
 
+def test_pass_size_setter_checks_its_arguments():
+    lib = svl_amd.lib()
+    with pytest.raises(svl_amd.SvlError) as e:
+        svl_amd._check(lib.svl_text_model_set_pass_tokens(None, 5))
+    assert e.value.kind == "Usage"
+
+
 def test_library_has_a_single_gfx950_code_object():
     data = open(svl_amd.LIB_PATH, "rb").read()
     assert data.count(b"amdgcn-amd-amdhsa--gfx950") >= 1

@@ -237,6 +237,44 @@ def test_two_stream_row_groups_are_bit_identical():
         assert m.forward(r).normalized().tobytes() == a.normalized().tobytes()
 
 
+def test_batches_run_in_passes_bit_for_bit():
+    """A batch whose workspace would pass the budget runs as passes of
+    consecutive rows. At a 700-token budget the 13 rows below take ten passes
+    (the 900-token row alone); the host outputs, hidden states included, with
+    feature rows in two of the passes, and the device entry point's Matryoshka
+    outputs equal the one-pass run bit for bit."""
+    import torch
+    cfg = svl_synth.config_a(layers=2, vocab=4096)
+    w = svl_synth.weights(cfg)
+    m = model(cfg, w)
+    lens = [512, 300, 500, 400, 100, 480, 900, 513, 64, 512, 300, 400, 37]
+    rows = svl_synth.token_rows(4096, lens)
+    rng = np.random.default_rng(3)
+    feats = [None] * len(rows)
+    feats[2] = ((rng.standard_normal((10, 768)) * 0.5).astype(np.float32), 5, 10)
+    feats[9] = ((rng.standard_normal((4, 768)) * 0.5).astype(np.float32), 500, 4)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    ids = torch.from_numpy(np.concatenate(rows).astype(np.int32)).to("cuda:0")
+    dims = [768, 256]
+    outs, dev = [], []
+    for budget in (0, 700):
+        m.set_pass_tokens(budget)
+        outs.append(m.forward_batch(rows, capture_hidden=True, features=feats))
+        d = torch.zeros((len(rows), sum(dims)), dtype=torch.float32, device="cuda:0")
+        m.forward_device(ids.data_ptr(), offsets, dims, d.data_ptr(),
+                         torch.cuda.current_stream().cuda_stream)
+        dev.append(d.cpu().numpy())
+    for i, (a, b) in enumerate(zip(*outs)):
+        for part in ("normalized", "pooled", "projected", "hidden_states"):
+            assert getattr(a, part)().tobytes() == getattr(b, part)().tobytes(), (i, part)
+    np.testing.assert_array_equal(outs[1][2].hidden_states()[0][5:15], feats[2][0])
+    assert dev[0].tobytes() == dev[1].tobytes()
+    with pytest.raises(S.SvlError) as e:
+        m.set_pass_tokens(-1)
+    assert e.value.kind == "Usage"
+    m.set_pass_tokens(0)
+
+
 def test_features_replace_rows_like_the_reference():  # text.rs:226-275
     cfg = svl_synth.config_a(layers=3, vocab=4096)
     w = svl_synth.weights(cfg)
