@@ -317,6 +317,17 @@ svl_status svl_vision_model_destroy(svl_vision_model *model);
  * reference encodes one image at a time). */
 svl_status svl_vision_model_set_stream_split(svl_vision_model *model, int groups);
 
+/* Every vision and image entry point runs a batch as passes of consecutive
+ * images of at most `patches` real patches each, one after another (a larger
+ * image runs alone), so the device workspace stays bounded whatever the
+ * batch; every output equals the one-pass run bit for bit (captured hidden
+ * states keep the whole batch's [L + 1, patches, H] layout). 0 (the default)
+ * sizes passes to about 32 GiB of workspace (931,461 patches, 404 images of
+ * 2304 patches, at the EmbeddingGemma tower's shape). Usage error outside
+ * 0..=268435455. No counterpart in the reference, which encodes one image at
+ * a time. */
+svl_status svl_vision_model_set_pass_patches(svl_vision_model *model, int64_t patches);
+
 /* VisionModel::forward (vision.rs:742-959) for `batch` images at once; image
  * i's result equals the reference's forward(image i).
  *  out_soft    [sum soft_tokens, text_hidden]  (VisionOutput::pooled of each

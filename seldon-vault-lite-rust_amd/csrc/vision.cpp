@@ -72,6 +72,7 @@ struct svl_vision_model {
     hipStream_t stream = nullptr;
     // image groups: the encoder layers of the second group run on `extra`
     int groups = 2;
+    int64_t pass_patches = 0;  // patches per pass (0: from VIS_PASS_BYTES)
     hipStream_t extra = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     std::mutex mu;
@@ -196,6 +197,7 @@ struct VisBatch {
     std::vector<AttnTile> tiles;
     int64_t max_coord = 0;
     double attn_flops = 0;
+    int64_t hidden_stride = 0;            // patches per layer block of captured states (0: T)
     // image groups for the encoder layers: patches [t0, t1), attention work
     // items [w0, w1) of `tiles`
     struct Group {
@@ -213,60 +215,71 @@ svl_status checked_len(int i, int64_t rows, int64_t width, const char *label) {
     return SVL_OK;
 }
 
-// Validation in the order VisionModel::forward meets each condition
-// (vision.rs:743-809, then pool_patches :981-1032), and the batch layout.
-svl_status prepare_images(const svl_vision_model *v, const svl_image_patches *im, int32_t batch,
-                          bool need_pixels, VisBatch &b, bool single) {
+// Validation of image i in the order VisionModel::forward meets each
+// condition (vision.rs:743-809, then pool_patches :981-1032).
+svl_status check_image(const svl_vision_model *v, const svl_image_patches &p, int i,
+                       bool need_pixels) {
+    const int64_t valid = p.valid_patches;
+    if (valid <= 0) return fail(SVL_CORRUPT, "image %d: vision tower received zero real patches", i);
+    if (valid > p.max_patches)
+        return fail(SVL_INTERNAL,
+                    "image %d: vision tower received more real patches than the padded tensor", i);
+    ST_TRY(checked_len(i, valid, PATCH_VALUES, "vision patch tensor"));
+    ST_TRY(checked_len(i, valid, v->H, "vision hidden state"));
+    ST_TRY(checked_len(i, valid, v->qd, "vision query rows"));
+    ST_TRY(checked_len(i, valid, v->kd, "vision key rows"));
+    ST_TRY(checked_len(i, valid, v->I, "vision feed-forward buffer"));
+    if (need_pixels && !p.pixel_values)
+        return fail(SVL_USAGE, "image %d: pixel values are null", i);
+    if (!p.positions) return fail(SVL_USAGE, "image %d: positions are null", i);
+    for (int64_t k = 0; k < valid; ++k) {
+        const int32_t x = p.positions[2 * k], y = p.positions[2 * k + 1];
+        if (x < 0) return fail(SVL_INTERNAL, "image %d: vision patch x position is negative", i);
+        if (y < 0) return fail(SVL_INTERNAL, "image %d: vision patch y position is negative", i);
+        if (x >= v->pos_size || y >= v->pos_size)
+            return fail(SVL_CORRUPT,
+                        "image %d: vision patch position (%d, %d) is outside the %lld-entry table",
+                        i, x, y, (long long)v->pos_size);
+    }
+    if (v->hd != 0 && attn_block_vectors((int)v->hd) == 0 && valid > SIMPLE_ATTENTION_MAX_KEYS)
+        return fail(SVL_UNSUPPORTED, "image %d: %lld patches at head dimension %lld", i,
+                    (long long)valid, (long long)v->hd);
+    // pool_patches geometry (vision.rs:981-1032)
+    if (p.grid_width < 0 || p.grid_height < 0 || p.grid_width % POOL || p.grid_height % POOL)
+        return fail(SVL_INTERNAL, "image %d: vision patch grid is not divisible by the pooling kernel", i);
+    const int64_t pw = p.grid_width / POOL, ph = p.grid_height / POOL;
+    if (ph != 0 && pw > INT64_MAX / ph)
+        return fail(SVL_LIMIT, "image %d: vision pooled grid overflow", i);
+    if (pw * ph != p.soft_tokens)
+        return fail(SVL_INTERNAL,
+                    "image %d: vision pooler produces %lld tokens, preprocessing declared %lld",
+                    i, (long long)(pw * ph), (long long)p.soft_tokens);
+    ST_TRY(checked_len(i, p.soft_tokens, v->H, "vision pooled state"));
+    for (int64_t k = 0; k < valid; ++k) {
+        const int64_t x = p.positions[2 * k], y = p.positions[2 * k + 1];
+        if (x / POOL + pw * (y / POOL) >= p.soft_tokens)
+            return fail(SVL_INTERNAL, "image %d: vision pooler computed an out-of-range bin", i);
+    }
+    return SVL_OK;
+}
+
+svl_status check_images(const svl_image_patches *im, int32_t batch) {
     if (batch < 0) return fail(SVL_USAGE, "negative batch");
     if (batch > 0 && !im) return fail(SVL_USAGE, "images are null");
+    return SVL_OK;
+}
+
+// Validation (check_image) and the layout of a batch of images.
+svl_status prepare_images(const svl_vision_model *v, const svl_image_patches *im, int32_t batch,
+                          bool need_pixels, VisBatch &b, bool single) {
+    ST_TRY(check_images(im, batch));
     b.B = batch;
     b.offsets.assign(1, 0);
     b.soft_offsets.assign(1, 0);
     for (int i = 0; i < batch; ++i) {
-        const svl_image_patches &p = im[i];
-        const int64_t valid = p.valid_patches;
-        if (valid <= 0) return fail(SVL_CORRUPT, "image %d: vision tower received zero real patches", i);
-        if (valid > p.max_patches)
-            return fail(SVL_INTERNAL,
-                        "image %d: vision tower received more real patches than the padded tensor", i);
-        ST_TRY(checked_len(i, valid, PATCH_VALUES, "vision patch tensor"));
-        ST_TRY(checked_len(i, valid, v->H, "vision hidden state"));
-        ST_TRY(checked_len(i, valid, v->qd, "vision query rows"));
-        ST_TRY(checked_len(i, valid, v->kd, "vision key rows"));
-        ST_TRY(checked_len(i, valid, v->I, "vision feed-forward buffer"));
-        if (need_pixels && !p.pixel_values)
-            return fail(SVL_USAGE, "image %d: pixel values are null", i);
-        if (!p.positions) return fail(SVL_USAGE, "image %d: positions are null", i);
-        for (int64_t k = 0; k < valid; ++k) {
-            const int32_t x = p.positions[2 * k], y = p.positions[2 * k + 1];
-            if (x < 0) return fail(SVL_INTERNAL, "image %d: vision patch x position is negative", i);
-            if (y < 0) return fail(SVL_INTERNAL, "image %d: vision patch y position is negative", i);
-            if (x >= v->pos_size || y >= v->pos_size)
-                return fail(SVL_CORRUPT,
-                            "image %d: vision patch position (%d, %d) is outside the %lld-entry table",
-                            i, x, y, (long long)v->pos_size);
-        }
-        if (v->hd != 0 && attn_block_vectors((int)v->hd) == 0 && valid > SIMPLE_ATTENTION_MAX_KEYS)
-            return fail(SVL_UNSUPPORTED, "image %d: %lld patches at head dimension %lld", i,
-                        (long long)valid, (long long)v->hd);
-        // pool_patches geometry (vision.rs:981-1032)
-        if (p.grid_width < 0 || p.grid_height < 0 || p.grid_width % POOL || p.grid_height % POOL)
-            return fail(SVL_INTERNAL, "image %d: vision patch grid is not divisible by the pooling kernel", i);
-        const int64_t pw = p.grid_width / POOL, ph = p.grid_height / POOL;
-        if (ph != 0 && pw > INT64_MAX / ph)
-            return fail(SVL_LIMIT, "image %d: vision pooled grid overflow", i);
-        if (pw * ph != p.soft_tokens)
-            return fail(SVL_INTERNAL,
-                        "image %d: vision pooler produces %lld tokens, preprocessing declared %lld",
-                        i, (long long)(pw * ph), (long long)p.soft_tokens);
-        ST_TRY(checked_len(i, p.soft_tokens, v->H, "vision pooled state"));
-        for (int64_t k = 0; k < valid; ++k) {
-            const int64_t x = p.positions[2 * k], y = p.positions[2 * k + 1];
-            if (x / POOL + pw * (y / POOL) >= p.soft_tokens)
-                return fail(SVL_INTERNAL, "image %d: vision pooler computed an out-of-range bin", i);
-        }
-        b.offsets.push_back(b.offsets.back() + valid);
-        b.soft_offsets.push_back(b.soft_offsets.back() + p.soft_tokens);
+        ST_TRY(check_image(v, im[i], i, need_pixels));
+        b.offsets.push_back(b.offsets.back() + im[i].valid_patches);
+        b.soft_offsets.push_back(b.soft_offsets.back() + im[i].soft_tokens);
     }
     b.T = b.offsets.back();
     b.S = b.soft_offsets.back();
@@ -380,10 +393,12 @@ svl_status upload_vis_meta(svl_vision_model *v, const VisBatch &b, hipStream_t s
 // The encoder layers (vision.rs:852-930) over patches [g.t0, g.t1) of the
 // batch on stream s; every kernel works row by row or within the group's
 // images, so the rows get the same arithmetic as one launch over the batch.
-// h_hidden: [L + 1, T, H] host capture (one group only).
+// h_hidden: the batch's first patch in a [L + 1, hidden_stride, H] host
+// capture (one group only).
 svl_status enqueue_vis_layers(svl_vision_model *v, const VisBatch &b, const VisBatch::Group &g,
                               hipStream_t s, float *h_hidden) {
     const int64_t T = b.T, H = v->H, R = g.t1 - g.t0;
+    const int64_t Ts = b.hidden_stride > 0 ? b.hidden_stride : T;
     if (R <= 0) return SVL_OK;
     int *flag = v->flag.p;
     const int64_t ldqkv = v->qd + 2 * v->kd;
@@ -446,7 +461,7 @@ svl_status enqueue_vis_layers(svl_vision_model *v, const VisBatch &b, const VisB
         HIP_TRY(launch_resnorm(tmp, ly.ln_post_ff, h, h, next, next ? n : nullptr, 1.0f, R, (int)H,
                                v->eps, flag, s));
         if (h_hidden)
-            HIP_TRY(hipMemcpyAsync(h_hidden + (size_t)((l + 1) * T * H), v->h.p,
+            HIP_TRY(hipMemcpyAsync(h_hidden + (size_t)((l + 1) * Ts * H), v->h.p,
                                    (size_t)(T * H) * 4, hipMemcpyDeviceToHost, s));
     }
 
@@ -506,16 +521,64 @@ svl_status vis_finish(svl_vision_model *v, hipStream_t s) {
     return SVL_OK;
 }
 
-// Runs the tower for a batch; the soft tokens stay in v->soft (and are
+// Every workspace buffer grows with the batch's patches, so a batch runs in
+// passes of consecutive images whose workspace stays within VIS_PASS_BYTES
+// (an image larger than a pass runs alone). An image's bits do not depend on
+// the images beside it, so the outputs equal those of one pass.
+constexpr int64_t VIS_PASS_BYTES = (int64_t)32 << 30;
+constexpr int64_t MAX_PASS_PATCHES = (int64_t)INT32_MAX / 8;
+
+int64_t vis_pass_budget(const svl_vision_model *v) {
+    if (v->pass_patches > 0) return v->pass_patches;
+    const int64_t per_patch = 4 * (PATCH_VALUES + 3 * v->H + 2 * v->qd + 2 * v->kd + v->I + 6);
+    return std::min(MAX_PASS_PATCHES, std::max<int64_t>(1, VIS_PASS_BYTES / per_patch));
+}
+
+// Images [first, last) of each pass, after check_image has passed for all.
+std::vector<std::pair<int32_t, int32_t>> image_passes(const svl_vision_model *v,
+                                                      const svl_image_patches *im,
+                                                      int32_t batch) {
+    std::vector<std::pair<int32_t, int32_t>> passes;
+    const int64_t cap = vis_pass_budget(v);
+    int32_t i0 = 0;
+    int64_t patches = 0;
+    for (int32_t i = 0; i < batch; ++i) {
+        if (i > i0 && patches + im[i].valid_patches > cap) {
+            passes.emplace_back(i0, i);
+            i0 = i;
+            patches = 0;
+        }
+        patches += im[i].valid_patches;
+    }
+    if (batch > 0) passes.emplace_back(i0, batch);
+    return passes;
+}
+
+// check_image for every image of a batch (image indices of the whole batch
+// in the messages); *patches = their real patches.
+svl_status check_batch(const svl_vision_model *v, const svl_image_patches *im, int32_t batch,
+                       bool need_pixels, int64_t *patches) {
+    ST_TRY(check_images(im, batch));
+    *patches = 0;
+    for (int i = 0; i < batch; ++i) {
+        ST_TRY(check_image(v, im[i], i, need_pixels));
+        *patches += im[i].valid_patches;
+    }
+    return SVL_OK;
+}
+
+// Runs the tower for one pass; the soft tokens stay in v->soft (and are
 // copied to out_soft when given). Pixels come from the host images, or from
 // d_pixels ([sum valid, 768] in HBM, rescaled in place) when it is given.
+// out_hidden: the pass's first patch in a [L + 1, hidden_stride, H] capture.
 // Caller holds v->mu.
 svl_status run_vision(svl_vision_model *v, const svl_image_patches *images, int32_t batch,
                       float *d_pixels, hipStream_t s, VisBatch &b, float *out_soft,
-                      float *out_hidden) {
+                      float *out_hidden, int64_t hidden_stride) {
     HIP_TRY(hipSetDevice(v->device));
     ST_TRY(prepare_images(v, images, batch, d_pixels == nullptr, b, out_hidden != nullptr));
     if (batch == 0) return SVL_OK;
+    b.hidden_stride = hidden_stride;
     ST_TRY(ensure_axial_tables(v, b.max_coord + 1));
     ST_TRY(ensure_vis_workspace(v, b));
     if (!d_pixels) {
@@ -551,37 +614,46 @@ svl_status image_embed(svl_vision_model *v, svl_text_model *text,
         return fail(SVL_USAGE, "the vision projection width %lld is not the text hidden size %lld",
                     (long long)v->text_hidden, (long long)text_hidden_size(text));
     std::lock_guard<std::mutex> lock(v->mu);
-    VisBatch b;
-    ST_TRY(run_vision(v, images, batch, d_pixels, v->stream, b, nullptr, nullptr));
+    int64_t patches = 0;
+    ST_TRY(check_batch(v, images, batch, d_pixels == nullptr, &patches));
     if (batch == 0) return SVL_OK;
     // image.rs:224-244: <bos> <boi> <image> x soft <eoi> <eos>, features at 2.
-    std::vector<int64_t> offsets(1, 0);
     for (int i = 0; i < batch; ++i) {
         const int64_t seq = images[i].soft_tokens + 4;
         if (seq > MAX_TEXT_TOKENS)
             return fail(SVL_LIMIT, "image %d: image prompt has %lld tokens, above the %lld-token context",
                         i, (long long)seq, (long long)MAX_TEXT_TOKENS);
-        offsets.push_back(offsets.back() + seq);
     }
-    std::vector<uint32_t> ids((size_t)offsets.back());
-    std::vector<int32_t> featmap((size_t)offsets.back(), -1);
-    for (int i = 0; i < batch; ++i) {
-        const int64_t o = offsets[i], soft = images[i].soft_tokens;
-        ids[(size_t)o] = tokens->bos;
-        ids[(size_t)o + 1] = tokens->boi;
-        for (int64_t k = 0; k < soft; ++k) {
-            ids[(size_t)(o + 2 + k)] = tokens->image;
-            featmap[(size_t)(o + 2 + k)] = (int32_t)(b.soft_offsets[i] + k);
+    int64_t first_patch = 0;
+    for (const auto &pr : image_passes(v, images, batch)) {
+        const int32_t i0 = pr.first, n = pr.second - pr.first;
+        VisBatch b;
+        ST_TRY(run_vision(v, images + i0, n, d_pixels ? d_pixels + first_patch * PATCH_VALUES : nullptr,
+                          v->stream, b, nullptr, nullptr, 0));
+        first_patch += b.T;
+        std::vector<int64_t> offsets(1, 0);
+        for (int i = 0; i < n; ++i) offsets.push_back(offsets.back() + images[i0 + i].soft_tokens + 4);
+        std::vector<uint32_t> ids((size_t)offsets.back());
+        std::vector<int32_t> featmap((size_t)offsets.back(), -1);
+        for (int i = 0; i < n; ++i) {
+            const int64_t o = offsets[i], soft = images[i0 + i].soft_tokens;
+            ids[(size_t)o] = tokens->bos;
+            ids[(size_t)o + 1] = tokens->boi;
+            for (int64_t k = 0; k < soft; ++k) {
+                ids[(size_t)(o + 2 + k)] = tokens->image;
+                featmap[(size_t)(o + 2 + k)] = (int32_t)(b.soft_offsets[i] + k);
+            }
+            ids[(size_t)(o + 2 + soft)] = tokens->eoi;
+            ids[(size_t)(o + 3 + soft)] = tokens->eos;
         }
-        ids[(size_t)(o + 2 + soft)] = tokens->eoi;
-        ids[(size_t)(o + 3 + soft)] = tokens->eos;
+        std::vector<float> normalized((size_t)(n * E));
+        ST_TRY(text_forward_with_device_features(text, ids.data(), offsets.data(), n,
+                                                 featmap.data(), v->soft.p, normalized.data()));
+        for (int i = 0; i < n; ++i)
+            ST_TRY(svl_truncate_and_normalize(normalized.data() + (size_t)i * E, (size_t)E,
+                                              (size_t)dimension,
+                                              out + (size_t)(i0 + i) * dimension));
     }
-    std::vector<float> normalized((size_t)(batch * E));
-    ST_TRY(text_forward_with_device_features(text, ids.data(), offsets.data(), batch,
-                                             featmap.data(), v->soft.p, normalized.data()));
-    for (int i = 0; i < batch; ++i)
-        ST_TRY(svl_truncate_and_normalize(normalized.data() + (size_t)i * E, (size_t)E,
-                                          (size_t)dimension, out + (size_t)i * dimension));
     return SVL_OK;
 }
 
@@ -681,6 +753,16 @@ svl_status svl_vision_model_set_stream_split(svl_vision_model *model, int groups
     return SVL_OK;
 }
 
+svl_status svl_vision_model_set_pass_patches(svl_vision_model *model, int64_t patches) {
+    if (!model) return fail(SVL_USAGE, "vision model is null");
+    if (patches < 0 || patches > MAX_PASS_PATCHES)
+        return fail(SVL_USAGE, "pass size %lld is outside 0..=%lld patches", (long long)patches,
+                    (long long)MAX_PASS_PATCHES);
+    std::lock_guard<std::mutex> lock(model->mu);
+    model->pass_patches = patches;
+    return SVL_OK;
+}
+
 svl_status svl_vision_model_destroy(svl_vision_model *model) {
     delete model;
     return SVL_OK;
@@ -690,8 +772,18 @@ svl_status svl_vision_forward_batch(svl_vision_model *v, const svl_image_patches
                                     int32_t batch, float *out_soft, float *out_hidden) {
     if (!v || !out_soft) return fail(SVL_USAGE, "model and out_soft are required");
     std::lock_guard<std::mutex> lock(v->mu);
-    VisBatch b;
-    return run_vision(v, images, batch, nullptr, v->stream, b, out_soft, out_hidden);
+    int64_t patches = 0;
+    ST_TRY(check_batch(v, images, batch, true, &patches));
+    int64_t t0 = 0, s0 = 0;
+    for (const auto &pr : image_passes(v, images, batch)) {
+        VisBatch b;
+        ST_TRY(run_vision(v, images + pr.first, pr.second - pr.first, nullptr, v->stream, b,
+                          out_soft + (size_t)(s0 * v->text_hidden),
+                          out_hidden ? out_hidden + (size_t)(t0 * v->H) : nullptr, patches));
+        t0 += b.T;
+        s0 += b.S;
+    }
+    return SVL_OK;
 }
 
 svl_status svl_vision_forward_device(svl_vision_model *v, float *d_pixels,
@@ -700,12 +792,19 @@ svl_status svl_vision_forward_device(svl_vision_model *v, float *d_pixels,
     if (!v || !d_pixels || !d_out) return fail(SVL_USAGE, "model, pixels and output are required");
     std::lock_guard<std::mutex> lock(v->mu);
     hipStream_t s = stream ? (hipStream_t)stream : v->stream;
-    VisBatch b;
-    ST_TRY(run_vision(v, images, batch, d_pixels, s, b, nullptr, nullptr));
-    if (batch == 0) return SVL_OK;
-    HIP_TRY(hipMemcpyAsync(d_out, v->soft.p, (size_t)(b.S * v->text_hidden) * 4,
-                           hipMemcpyDeviceToDevice, s));
-    HIP_TRY(hipStreamSynchronize(s));
+    int64_t patches = 0;
+    ST_TRY(check_batch(v, images, batch, false, &patches));
+    int64_t t0 = 0, s0 = 0;
+    for (const auto &pr : image_passes(v, images, batch)) {
+        VisBatch b;
+        ST_TRY(run_vision(v, images + pr.first, pr.second - pr.first,
+                          d_pixels + (size_t)(t0 * PATCH_VALUES), s, b, nullptr, nullptr, 0));
+        HIP_TRY(hipMemcpyAsync(d_out + (size_t)(s0 * v->text_hidden), v->soft.p,
+                               (size_t)(b.S * v->text_hidden) * 4, hipMemcpyDeviceToDevice, s));
+        HIP_TRY(hipStreamSynchronize(s));
+        t0 += b.T;
+        s0 += b.S;
+    }
     return SVL_OK;
 }
 

@@ -101,7 +101,7 @@ EXPORTED = [
     "svl_bidirectional_attention", "svl_gelu_tanh", "svl_geglu", "svl_add", "svl_mean_pool",
     "svl_l2_normalize", "svl_synth_uniform", "svl_synth_ids", "svl_synth_lengths",
     "svl_vision_model_create", "svl_vision_model_destroy", "svl_vision_model_set_stream_split",
-    "svl_vision_forward_batch",
+    "svl_vision_model_set_pass_patches", "svl_vision_forward_batch",
     "svl_vision_forward_device", "svl_image_embed_batch", "svl_image_embed_device",
     "svl_audio_model_create", "svl_audio_model_destroy", "svl_audio_token_count",
     "svl_audio_forward_batch", "svl_audio_forward_device", "svl_audio_embed_batch",
@@ -196,6 +196,7 @@ def lib():
                                               ctypes.c_size_t, ctypes.POINTER(vp)]
         L.svl_vision_model_destroy.argtypes = [vp]
         L.svl_vision_model_set_stream_split.argtypes = [vp, ctypes.c_int]
+        L.svl_vision_model_set_pass_patches.argtypes = [vp, i64]
         L.svl_vision_forward_batch.argtypes = [vp, vp, i32, vp, vp]
         L.svl_vision_forward_device.argtypes = [vp, vp, vp, i32, vp, vp]
         L.svl_image_embed_batch.argtypes = [vp, vp, vp, vp, i32, i64, vp]

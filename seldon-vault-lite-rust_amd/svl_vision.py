@@ -333,6 +333,12 @@ class VisionModel:
         g = 2 if groups is True else 1 if groups is False else int(groups)
         _check(lib().svl_vision_model_set_stream_split(self.handle, g))
 
+    def set_pass_patches(self, patches: int):
+        """Largest pass of consecutive images a batch runs in, in real
+        patches (0: sized to about 32 GiB of device workspace); results do not
+        depend on it."""
+        _check(lib().svl_vision_model_set_pass_patches(self.handle, int(patches)))
+
     def forward(self, patches: ImagePatches, capture_hidden=False) -> VisionOutput:
         """vision.rs:742-959."""
         return self.forward_batch([patches], capture_hidden)[0]

@@ -150,6 +150,45 @@ def test_device_resident_matches_host(tower_v2):
     assert np.array_equal(d_out.cpu().numpy(), host)
 
 
+def test_batches_run_in_passes_bit_for_bit(tower_v2, embedder):
+    """A batch whose workspace would pass the budget runs as passes of
+    consecutive images. At a 300-patch budget the images below (108, 144, 324,
+    90 and 108 patches) take three passes, the 324-patch image alone. The soft
+    tokens, the captured hidden states, the device entry point and the image
+    embedder equal the one-pass run bit for bit."""
+    import torch
+    w, gpu, om = tower_v2
+    emb, _, _ = embedder
+    grids = [(12, 9), (12, 12), (18, 18), (6, 15), (9, 12)]
+    patches = [svl_synth.image_patches(1, gw, gh, seed=71 + i)[0] for i, (gw, gh) in enumerate(grids)]
+    pix = np.concatenate([p.pixel_values[: p.valid_patches] for p in patches])
+    soft = sum(p.soft_tokens for p in patches)
+    runs = []
+    for budget in (0, 300):
+        gpu.set_pass_patches(budget)
+        emb.vision.set_pass_patches(budget)
+        try:
+            host = gpu.forward_batch(patches, capture_hidden=True)
+            d_pix = torch.from_numpy(pix).to("cuda:0")
+            d_out = torch.empty((soft, 768), device="cuda:0")
+            torch.cuda.synchronize()
+            gpu.forward_device(d_pix.data_ptr(), patches, d_out.data_ptr())
+            runs.append((host, d_out.cpu().numpy(), emb.embed_batch(patches, 768)))
+        finally:
+            gpu.set_pass_patches(0)
+            emb.vision.set_pass_patches(0)
+    (h1, d1, e1), (h2, d2, e2) = runs
+    for i in range(len(patches)):
+        assert h1[i].pooled().tobytes() == h2[i].pooled().tobytes(), f"image {i}"
+        assert (np.stack(h1[i].hidden_states()).tobytes() ==
+                np.stack(h2[i].hidden_states()).tobytes()), f"image {i}"
+    assert d1.tobytes() == d2.tobytes()
+    assert e1.tobytes() == e2.tobytes()
+    with pytest.raises(S.SvlError) as e:
+        gpu.set_pass_patches(-1)
+    assert e.value.kind == "Usage"
+
+
 @pytest.fixture(scope="module")
 def full_v():
     """Config V at 16 layers and one 768 x 768 noise image (2304 patches, 256
