@@ -122,16 +122,24 @@ __global__ __launch_bounds__(256) void resnorm_kernel(
     const int nv = width >> 2;
     const f32x4 *xr = (const f32x4 *)(x + row * width);
     const f32x4 *rr = (const f32x4 *)(res + row * width);
-    f32x4 v[NC];
-    float ss = 0.f;
+    // Every operand of the row is loaded before any arithmetic: one memory
+    // round trip instead of one per chunk and operand, which sets the time of
+    // a launch over a few hundred rows. Chunks past the row's width load its
+    // last chunk and take no part.
+    f32x4 v[NC], rv[NC], w1v[NC], w2v[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const int i = lane + 64 * c;
-        if (i < nv) {
-            v[c] = xr[i];
-            ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
-        }
+        const int i = min(lane + 64 * c, nv - 1);
+        v[c] = xr[i];
+        rv[c] = rr[i];
+        w1v[c] = ((const f32x4 *)w1)[i];
+        if (w2) w2v[c] = ((const f32x4 *)w2)[i];
     }
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+        if (lane + 64 * c < nv)
+            ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
     ss = wave_sum(ss);
     const float inv = rms_inverse(ss, width, eps);
     bool ok = isfinite(ss);
@@ -141,8 +149,8 @@ __global__ __launch_bounds__(256) void resnorm_kernel(
     for (int c = 0; c < NC; ++c) {
         const int i = lane + 64 * c;
         if (i < nv) {
-            const f32x4 y = v[c] * inv * ((const f32x4 *)w1)[i];
-            f32x4 hv = (rr[i] + y) * scale;
+            const f32x4 y = v[c] * inv * w1v[c];
+            f32x4 hv = (rv[c] + y) * scale;
             ok = ok && finite4(hv);
             hrow[i] = hv;
             v[c] = hv;
@@ -157,7 +165,7 @@ __global__ __launch_bounds__(256) void resnorm_kernel(
         for (int c = 0; c < NC; ++c) {
             const int i = lane + 64 * c;
             if (i < nv) {
-                const f32x4 y = v[c] * inv2 * ((const f32x4 *)w2)[i];
+                const f32x4 y = v[c] * inv2 * w2v[c];
                 ok = ok && finite4(y);
                 nrow[i] = y;
             }
@@ -170,7 +178,7 @@ hipError_t launch_resnorm(const float *x, const float *w1, const float *res, flo
                           const float *w2, float *n_out, float scale, int64_t rows, int width,
                           float eps, int *flag, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    if (width % 4 != 0 || width > 256 * ROW_CHUNKS) return hipErrorInvalidValue;
+    if (width <= 0 || width % 4 != 0 || width > 256 * ROW_CHUNKS) return hipErrorInvalidValue;
     SVL_DISPATCH_NC((width + 255) / 256, resnorm_kernel, dim3((unsigned)((rows + 3) / 4)), s, x,
                     w1, res, h_out, w2, n_out, scale, rows, width, eps, flag);
     return hipGetLastError();
@@ -201,7 +209,15 @@ __global__ __launch_bounds__(256) void gather_kernel(
         }
         src = (const f32x4 *)(table + (int64_t)id * width);
     }
-    f32x4 v[NC];
+    // the row's chunks and the norm weights loaded together (chunks past the
+    // width load its last chunk and take no part)
+    f32x4 v[NC], wv[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = min(lane + 64 * c, nv - 1);
+        v[c] = src[i];
+        wv[c] = ((const f32x4 *)w_in)[i];
+    }
     float ss = 0.f;
     bool ok = true;
     f32x4 *hrow = (f32x4 *)(h + t * width);
@@ -209,7 +225,7 @@ __global__ __launch_bounds__(256) void gather_kernel(
     for (int c = 0; c < NC; ++c) {
         const int i = lane + 64 * c;
         if (i < nv) {
-            f32x4 e = src[i];
+            f32x4 e = v[c];
             if (fi < 0) e = e * mul;
             v[c] = e;
             ok = ok && finite4(e);
@@ -224,7 +240,7 @@ __global__ __launch_bounds__(256) void gather_kernel(
     for (int c = 0; c < NC; ++c) {
         const int i = lane + 64 * c;
         if (i < nv) {
-            const f32x4 y = v[c] * inv * ((const f32x4 *)w_in)[i];
+            const f32x4 y = v[c] * inv * wv[c];
             ok = ok && finite4(y);
             nrow[i] = y;
         }
@@ -237,7 +253,7 @@ hipError_t launch_gather(const uint32_t *ids, const float *table, int64_t vocab,
                          const float *w_in, float *h, float *n, int64_t tokens, int width,
                          float eps, int *flag, hipStream_t s) {
     if (tokens <= 0) return hipSuccess;
-    if (width % 4 != 0 || width > 256 * ROW_CHUNKS) return hipErrorInvalidValue;
+    if (width <= 0 || width % 4 != 0 || width > 256 * ROW_CHUNKS) return hipErrorInvalidValue;
     SVL_DISPATCH_NC((width + 255) / 256, gather_kernel, dim3((unsigned)((tokens + 3) / 4)), s, ids,
                     table, vocab, featmap, feats, scale, w_in, h, n, tokens, width, eps, flag);
     return hipGetLastError();
@@ -312,26 +328,32 @@ __global__ __launch_bounds__(256) void qkv_post256_kernel(
     const int per_tok = nh + 2 * nkv;
     const int h = lane >> 5, l32 = lane & 31;
     f32x4 *row = (f32x4 *)(qkv + t * ld) + 64 * h + l32;  // row h of the token
+    // Every operand is loaded before any arithmetic (rows past the token's
+    // last load that row and take no part): two memory round trips, the
+    // position and then its table rows, instead of one per row pair.
+    const int64_t tab = (int64_t)pos[t] * 128 + 4 * l32;
     f32x4 x[PAIRS][2];
+#pragma unroll
+    for (int i = 0; i < PAIRS; ++i) {
+        const f32x4 *src = (const f32x4 *)(qkv + t * ld) + 64 * min(2 * i + h, per_tok - 1) + l32;
+        x[i][0] = src[0];
+        x[i][1] = src[32];
+    }
+    const f32x4 wq0 = ((const f32x4 *)qn)[l32], wq1 = ((const f32x4 *)qn)[l32 + 32];
+    const f32x4 wk0 = ((const f32x4 *)kn)[l32], wk1 = ((const f32x4 *)kn)[l32 + 32];
+    const f32x4 c = *(const f32x4 *)(cos_t + tab);
+    const f32x4 sn = *(const f32x4 *)(sin_t + tab);
     float ss[PAIRS];
 #pragma unroll
     for (int i = 0; i < PAIRS; ++i) {
         ss[i] = 0.f;
-        if (2 * i + h < per_tok) {
-            x[i][0] = row[128 * i];
-            x[i][1] = row[128 * i + 32];
+        if (2 * i + h < per_tok)
             ss[i] = x[i][0].x * x[i][0].x + x[i][0].y * x[i][0].y + x[i][0].z * x[i][0].z +
                     x[i][0].w * x[i][0].w + x[i][1].x * x[i][1].x + x[i][1].y * x[i][1].y +
                     x[i][1].z * x[i][1].z + x[i][1].w * x[i][1].w;
-        }
     }
 #pragma unroll
     for (int i = 0; i < PAIRS; ++i) ss[i] = group_reduce<32, false>(ss[i]);
-    const f32x4 wq0 = ((const f32x4 *)qn)[l32], wq1 = ((const f32x4 *)qn)[l32 + 32];
-    const f32x4 wk0 = ((const f32x4 *)kn)[l32], wk1 = ((const f32x4 *)kn)[l32 + 32];
-    const int64_t tab = (int64_t)pos[t] * 128 + 4 * l32;
-    const f32x4 c = *(const f32x4 *)(cos_t + tab);
-    const f32x4 sn = *(const f32x4 *)(sin_t + tab);
     bool ok = true;
 #pragma unroll
     for (int i = 0; i < PAIRS; ++i) {
@@ -370,26 +392,31 @@ __global__ __launch_bounds__(256) void qkv_post512_kernel(
     if (t >= tokens) return;
     const int per_tok = nh + 2 * nkv;
     f32x4 *row = (f32x4 *)(qkv + t * ld) + lane;
+    // every operand loaded before any arithmetic, as in qkv_post256_kernel
+    const int64_t tab = (int64_t)pos[t] * 256 + 4 * lane;
     f32x4 x[ROWS][2];
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k) {
+        const int kr = min(k, per_tok - 1);
+        x[k][0] = row[128 * kr];
+        x[k][1] = row[128 * kr + 64];
+    }
+    const f32x4 wq0 = ((const f32x4 *)qn)[lane], wq1 = ((const f32x4 *)qn)[lane + 64];
+    const f32x4 wk0 = ((const f32x4 *)kn)[lane], wk1 = ((const f32x4 *)kn)[lane + 64];
+    const f32x4 c = *(const f32x4 *)(cos_t + tab);
+    const f32x4 sn = *(const f32x4 *)(sin_t + tab);
     float ss[ROWS];
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
-        if (k < per_tok) {
-            x[k][0] = row[128 * k];
-            x[k][1] = row[128 * k + 64];
+        ss[k] = 0.f;
+        if (k < per_tok)
             ss[k] = x[k][0].x * x[k][0].x + x[k][0].y * x[k][0].y + x[k][0].z * x[k][0].z +
                     x[k][0].w * x[k][0].w + x[k][1].x * x[k][1].x + x[k][1].y * x[k][1].y +
                     x[k][1].z * x[k][1].z + x[k][1].w * x[k][1].w;
-        }
     }
 #pragma unroll
     for (int k = 0; k < ROWS; ++k)
         if (k < per_tok) ss[k] = wave_sum(ss[k]);
-    const f32x4 wq0 = ((const f32x4 *)qn)[lane], wq1 = ((const f32x4 *)qn)[lane + 64];
-    const f32x4 wk0 = ((const f32x4 *)kn)[lane], wk1 = ((const f32x4 *)kn)[lane + 64];
-    const int64_t tab = (int64_t)pos[t] * 256 + 4 * lane;
-    const f32x4 c = *(const f32x4 *)(cos_t + tab);
-    const f32x4 sn = *(const f32x4 *)(sin_t + tab);
     bool ok = true;
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
