@@ -39,16 +39,20 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(const float *__restrict__
     if (row >= rows) return;
     const int nv = width >> 2;
     const f32x4 *xr = (const f32x4 *)(x + row * width);
-    f32x4 v[NC];
-    float ss = 0.f;
+    // the row and the weights loaded together (chunks past the width load
+    // its last chunk and take no part)
+    f32x4 v[NC], wv[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const int i = lane + 64 * c;
-        if (i < nv) {
-            v[c] = xr[i];
-            ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
-        }
+        const int i = min(lane + 64 * c, nv - 1);
+        v[c] = xr[i];
+        if (w) wv[c] = ((const f32x4 *)w)[i];
     }
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+        if (lane + 64 * c < nv)
+            ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
     ss = wave_sum(ss);
     const float inv = rms_inverse(ss, width, eps);
     bool ok = isfinite(ss);
@@ -58,7 +62,7 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(const float *__restrict__
         const int i = lane + 64 * c;
         if (i < nv) {
             f32x4 y = v[c] * inv;
-            if (w) y = y * ((const f32x4 *)w)[i];
+            if (w) y = y * wv[c];
             ok = ok && finite4(y);
             orow[i] = y;
         }
@@ -94,7 +98,8 @@ hipError_t launch_rms_rows(const float *x, const float *w, float *out, int64_t r
                            float eps, int *flag, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     const dim3 grid((unsigned)((rows + 3) / 4));
-    const bool vec = width % 4 == 0 && width <= 256 * ROW_CHUNKS && (uintptr_t)x % 16 == 0 &&
+    const bool vec = width > 0 && width % 4 == 0 && width <= 256 * ROW_CHUNKS &&
+                     (uintptr_t)x % 16 == 0 &&
                      (uintptr_t)out % 16 == 0 && (!w || (uintptr_t)w % 16 == 0);
     if (vec) {
         SVL_DISPATCH_NC((width + 255) / 256, rms_rows_kernel, grid, s, x, w, out, rows, width, eps,
@@ -526,7 +531,8 @@ hipError_t launch_positions(const int64_t *offsets, int batch, int32_t *pos, int
 // sums its column over the row's tokens in token order and multiplies by
 // 1/len: the same operations in the same order as mean_pool_scalar, so
 // pooled is bit-identical for identical projected inputs. Loads are issued
-// eight tokens ahead of the additions to keep HBM busy.
+// 32 (then 8) tokens ahead of the additions, so a row costs a few memory
+// round trips rather than one per eight tokens.
 // pool_norm_kernel: one workgroup per row: L2 normalisation and the
 // Matryoshka truncations, each renormalised.
 constexpr int POOL_MAX_WIDTH = 4096;
@@ -551,6 +557,14 @@ __global__ __launch_bounds__(64) void pool_sum_kernel(const float *__restrict__ 
     const int64_t n = b - a;
     float acc = 0.f;
     int64_t t = 0;
+    // 32 loads in flight per round trip: a 128-token row takes four
+    for (; t + 32 <= n; t += 32) {
+        float v[32];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) v[u] = src[(t + u) * width];
+#pragma unroll
+        for (int u = 0; u < 32; ++u) acc += v[u];
+    }
     for (; t + 8 <= n; t += 8) {
         float v[8];
 #pragma unroll
