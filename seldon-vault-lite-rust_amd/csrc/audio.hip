@@ -171,18 +171,25 @@ __global__ __launch_bounds__(256) void audio_rows_kernel(
     if (row >= rows) return;
     const int nv = width >> 2;
     const f32x4 *xr = (const f32x4 *)(x + row * width);
-    f32x4 v[NC];
+    // Every operand of the row is loaded before any arithmetic or store (one
+    // memory round trip); chunks past the width load its last chunk and take
+    // no part.
+    f32x4 v[NC], w1v[NC], rv[NC], w2v[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int i = min(lane + 64 * c, nv - 1);
+        v[c] = xr[i];
+        if (w1) w1v[c] = ((const f32x4 *)w1)[i];
+        if (res) rv[c] = ((const f32x4 *)(res + row * width))[i];
+        if (w2) w2v[c] = ((const f32x4 *)w2)[i];
+    }
     bool ok = true;
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const int i = lane + 64 * c;
-        if (i < nv) {
-            v[c] = xr[i];
-            if (w1) {
-                v[c] = clamp4(v[c], -c1, c1);
-                ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
-            }
+        if (lane + 64 * c < nv && w1) {
+            v[c] = clamp4(v[c], -c1, c1);
+            ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
         }
     }
     if (w1) {
@@ -192,7 +199,7 @@ __global__ __launch_bounds__(256) void audio_rows_kernel(
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const int i = lane + 64 * c;
-            if (i < nv) v[c] = v[c] * inv * ((const f32x4 *)w1)[i];
+            if (i < nv) v[c] = v[c] * inv * w1v[c];
         }
     }
     float ss2 = 0.f;
@@ -200,7 +207,7 @@ __global__ __launch_bounds__(256) void audio_rows_kernel(
     for (int c = 0; c < NC; ++c) {
         const int i = lane + 64 * c;
         if (i < nv) {
-            if (res) v[c] = ((const f32x4 *)(res + row * width))[i] + v[c] * rw;
+            if (res) v[c] = rv[c] + v[c] * rw;
             ok = ok && finite4(v[c]);
             if (h_out) {
                 if (w2) {
@@ -226,7 +233,7 @@ __global__ __launch_bounds__(256) void audio_rows_kernel(
         for (int c = 0; c < NC; ++c) {
             const int i = lane + 64 * c;
             if (i < nv) {
-                const f32x4 y = v[c] * inv * ((const f32x4 *)w2)[i];
+                const f32x4 y = v[c] * inv * w2v[c];
                 ok = ok && finite4(y);
                 for (int k = 0; k < oc.copies; ++k)
                     ((f32x4 *)(n_out + k * oc.stride + row * width))[i] = clamp4(y, oc.lo[k], oc.hi[k]);
@@ -240,9 +247,10 @@ hipError_t launch_audio_rows(const float *x, float c1, const float *w1, const fl
                              float *h_out, float c2, const float *w2, float *n_out, int64_t rows,
                              int width, float eps, int *flag, hipStream_t s, const OutClamp &oc) {
     if (rows <= 0) return hipSuccess;
-    if (width % 4 || width > 2048 || oc.copies < 1 || oc.copies > 3) return hipErrorInvalidValue;
+    if (width <= 0 || width % 4 || width > 2048 || oc.copies < 1 || oc.copies > 3)
+        return hipErrorInvalidValue;
     const dim3 grid((unsigned)((rows + 3) / 4));
-#define AR_LAUNCH(NC)                                                                          \
+#define AR_LAUNCH(NC)                                                                        \
     hipLaunchKernelGGL(audio_rows_kernel<NC>, grid, dim3(256), 0, s, x, c1, w1, res, rw, h_out, \
                        c2, w2, n_out, rows, width, eps, flag, oc)
     switch ((width + 255) / 256) {
