@@ -827,8 +827,12 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
         return launch_dma<64, 128, 16, EPI, 4, 2>(a, s);
     } else {
         if (tiny) {
-            // 128-wide K slices: fewer DMA round trips on a chain that is
-            // mostly memory latency (O at 128 tokens: 7.0 us against 7.6)
+            // Wide K slices: fewer DMA round trips and barriers on a chain
+            // that is mostly memory latency. 256-wide slices (two 64 KB
+            // stages) took the 1 x 128-token forward from 1.837 to 1.811 ms
+            // against 128-wide ones; 128-wide took O at 128 tokens from 7.6
+            // to 7.0 us against 64-wide.
+            if (a.K % 256 == 0) return launch_dma<32, 32, 256, EPI, 1, 2>(a, s);
             if (a.K % 128 == 0) return launch_dma<32, 32, 128, EPI, 1, 2>(a, s);
             if (a.K % 64 == 0) return launch_dma<32, 32, 64, EPI, 1, 3>(a, s);
             return launch_dma<32, 32, 32, EPI, 1, 4>(a, s);
