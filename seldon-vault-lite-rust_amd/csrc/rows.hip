@@ -26,6 +26,24 @@ constexpr int ROW_CHUNKS = 8;  // register-resident rows up to 8 * 256 floats
         default: hipLaunchKernelGGL(KERNEL<8>, grid, dim3(256), 0, __VA_ARGS__); break;       \
     }
 
+// The same with a second, boolean template argument B.
+#define SVL_DISPATCH_NC_B(nc, KERNEL, B, grid, ...)                                             \
+    switch (nc) {                                                                             \
+        case 1: hipLaunchKernelGGL((KERNEL<1, B>), grid, dim3(256), 0, __VA_ARGS__); break;   \
+        case 2: hipLaunchKernelGGL((KERNEL<2, B>), grid, dim3(256), 0, __VA_ARGS__); break;   \
+        case 3: hipLaunchKernelGGL((KERNEL<3, B>), grid, dim3(256), 0, __VA_ARGS__); break;   \
+        case 4: hipLaunchKernelGGL((KERNEL<4, B>), grid, dim3(256), 0, __VA_ARGS__); break;   \
+        case 5: hipLaunchKernelGGL((KERNEL<5, B>), grid, dim3(256), 0, __VA_ARGS__); break;   \
+        case 6: hipLaunchKernelGGL((KERNEL<6, B>), grid, dim3(256), 0, __VA_ARGS__); break;   \
+        case 7: hipLaunchKernelGGL((KERNEL<7, B>), grid, dim3(256), 0, __VA_ARGS__); break;   \
+        default: hipLaunchKernelGGL((KERNEL<8, B>), grid, dim3(256), 0, __VA_ARGS__); break;  \
+    }
+
+// Row kernels whose launch covers fewer rows than this load every operand of
+// a row before its arithmetic (LOAD_FIRST below); larger launches keep the
+// load order that holds fewer registers per wave.
+constexpr int64_t LOAD_FIRST_MAX_ROWS = 4096;
+
 // ---- RMSNorm rows (kernels.rs:727-857) ------------------------------------
 
 // Register-resident variant: width % 4 == 0 and width <= 2048.
@@ -116,7 +134,16 @@ hipError_t launch_rms_rows(const float *x, const float *w, float *out, int64_t r
 // (res + y) * scale rounds exactly like add() then the scalar multiply.
 // h_out may alias res (in-place residual update): each lane reads its
 // elements of res before writing the same elements of h_out.
-template <int NC>
+//
+// Two load orders, one arithmetic. LOAD_FIRST loads every operand of the
+// row before any arithmetic (chunks past the width load its last chunk and
+// take no part): one memory round trip where the other order takes one per
+// chunk and operand, which sets the time of a launch over a few hundred rows
+// (the 1 x 128-token forward's 72 launches: 5.1 against 3.6 us). Launches
+// of many rows take the other order, whose waves hold fewer registers: with
+// the other row groups' GEMMs on the same CUs the three-group T2 step took
+// 39.50 against 39.36 ms with every launch loading first.
+template <int NC, bool LOAD_FIRST>
 __global__ __launch_bounds__(256) void resnorm_kernel(
     const float *__restrict__ x, const float *__restrict__ w1, const float *res, float *h_out,
     const float *__restrict__ w2, float *__restrict__ n_out,
@@ -127,24 +154,31 @@ __global__ __launch_bounds__(256) void resnorm_kernel(
     const int nv = width >> 2;
     const f32x4 *xr = (const f32x4 *)(x + row * width);
     const f32x4 *rr = (const f32x4 *)(res + row * width);
-    // Every operand of the row is loaded before any arithmetic: one memory
-    // round trip instead of one per chunk and operand, which sets the time of
-    // a launch over a few hundred rows. Chunks past the row's width load its
-    // last chunk and take no part.
     f32x4 v[NC], rv[NC], w1v[NC], w2v[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const int i = min(lane + 64 * c, nv - 1);
-        v[c] = xr[i];
-        rv[c] = rr[i];
-        w1v[c] = ((const f32x4 *)w1)[i];
-        if (w2) w2v[c] = ((const f32x4 *)w2)[i];
-    }
     float ss = 0.f;
+    if constexpr (LOAD_FIRST) {
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
-        if (lane + 64 * c < nv)
-            ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+        for (int c = 0; c < NC; ++c) {
+            const int i = min(lane + 64 * c, nv - 1);
+            v[c] = xr[i];
+            rv[c] = rr[i];
+            w1v[c] = ((const f32x4 *)w1)[i];
+            if (w2) w2v[c] = ((const f32x4 *)w2)[i];
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if (lane + 64 * c < nv)
+                ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+    } else {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int i = lane + 64 * c;
+            if (i < nv) {
+                v[c] = xr[i];
+                ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+            }
+        }
+    }
     ss = wave_sum(ss);
     const float inv = rms_inverse(ss, width, eps);
     bool ok = isfinite(ss);
@@ -154,6 +188,10 @@ __global__ __launch_bounds__(256) void resnorm_kernel(
     for (int c = 0; c < NC; ++c) {
         const int i = lane + 64 * c;
         if (i < nv) {
+            if constexpr (!LOAD_FIRST) {
+                w1v[c] = ((const f32x4 *)w1)[i];
+                rv[c] = rr[i];
+            }
             const f32x4 y = v[c] * inv * w1v[c];
             f32x4 hv = (rv[c] + y) * scale;
             ok = ok && finite4(hv);
@@ -170,6 +208,7 @@ __global__ __launch_bounds__(256) void resnorm_kernel(
         for (int c = 0; c < NC; ++c) {
             const int i = lane + 64 * c;
             if (i < nv) {
+                if constexpr (!LOAD_FIRST) w2v[c] = ((const f32x4 *)w2)[i];
                 const f32x4 y = v[c] * inv2 * w2v[c];
                 ok = ok && finite4(y);
                 nrow[i] = y;
@@ -184,8 +223,14 @@ hipError_t launch_resnorm(const float *x, const float *w1, const float *res, flo
                           float eps, int *flag, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
     if (width <= 0 || width % 4 != 0 || width > 256 * ROW_CHUNKS) return hipErrorInvalidValue;
-    SVL_DISPATCH_NC((width + 255) / 256, resnorm_kernel, dim3((unsigned)((rows + 3) / 4)), s, x,
-                    w1, res, h_out, w2, n_out, scale, rows, width, eps, flag);
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (rows < LOAD_FIRST_MAX_ROWS) {
+        SVL_DISPATCH_NC_B((width + 255) / 256, resnorm_kernel, true, grid, s, x, w1, res, h_out,
+                          w2, n_out, scale, rows, width, eps, flag);
+    } else {
+        SVL_DISPATCH_NC_B((width + 255) / 256, resnorm_kernel, false, grid, s, x, w1, res, h_out,
+                          w2, n_out, scale, rows, width, eps, flag);
+    }
     return hipGetLastError();
 }
 
@@ -322,7 +367,7 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(
 // [4 (l % 32), +4) and [128 + 4 (l % 32), +4): the rotate-half partner of
 // each element (j and j + 128) sits in the same lane, and each row's norm is
 // a 32-lane reduction.
-template <int PAIRS>
+template <int PAIRS, bool LOAD_FIRST>
 __global__ __launch_bounds__(256) void qkv_post256_kernel(
     float *__restrict__ qkv, int64_t ld, int64_t tokens, int nh, int nkv,
     const float *__restrict__ qn, const float *__restrict__ kn, const float *__restrict__ cos_t,
@@ -333,32 +378,59 @@ __global__ __launch_bounds__(256) void qkv_post256_kernel(
     const int per_tok = nh + 2 * nkv;
     const int h = lane >> 5, l32 = lane & 31;
     f32x4 *row = (f32x4 *)(qkv + t * ld) + 64 * h + l32;  // row h of the token
-    // Every operand is loaded before any arithmetic (rows past the token's
-    // last load that row and take no part): two memory round trips, the
-    // position and then its table rows, instead of one per row pair.
-    const int64_t tab = (int64_t)pos[t] * 128 + 4 * l32;
-    f32x4 x[PAIRS][2];
-#pragma unroll
-    for (int i = 0; i < PAIRS; ++i) {
-        const f32x4 *src = (const f32x4 *)(qkv + t * ld) + 64 * min(2 * i + h, per_tok - 1) + l32;
-        x[i][0] = src[0];
-        x[i][1] = src[32];
-    }
-    const f32x4 wq0 = ((const f32x4 *)qn)[l32], wq1 = ((const f32x4 *)qn)[l32 + 32];
-    const f32x4 wk0 = ((const f32x4 *)kn)[l32], wk1 = ((const f32x4 *)kn)[l32 + 32];
-    const f32x4 c = *(const f32x4 *)(cos_t + tab);
-    const f32x4 sn = *(const f32x4 *)(sin_t + tab);
+    f32x4 x[PAIRS][2], wq0, wq1, wk0, wk1, c, sn;
     float ss[PAIRS];
+    if constexpr (LOAD_FIRST) {
+        // Every operand is loaded before any arithmetic (rows past the
+        // token's last load that row and take no part): two memory round
+        // trips, the position and then its table rows, instead of one per
+        // row pair (the load orders of resnorm_kernel).
+        const int64_t tab = (int64_t)pos[t] * 128 + 4 * l32;
 #pragma unroll
-    for (int i = 0; i < PAIRS; ++i) {
-        ss[i] = 0.f;
-        if (2 * i + h < per_tok)
-            ss[i] = x[i][0].x * x[i][0].x + x[i][0].y * x[i][0].y + x[i][0].z * x[i][0].z +
-                    x[i][0].w * x[i][0].w + x[i][1].x * x[i][1].x + x[i][1].y * x[i][1].y +
-                    x[i][1].z * x[i][1].z + x[i][1].w * x[i][1].w;
+        for (int i = 0; i < PAIRS; ++i) {
+            const f32x4 *src =
+                (const f32x4 *)(qkv + t * ld) + 64 * min(2 * i + h, per_tok - 1) + l32;
+            x[i][0] = src[0];
+            x[i][1] = src[32];
+        }
+        wq0 = ((const f32x4 *)qn)[l32];
+        wq1 = ((const f32x4 *)qn)[l32 + 32];
+        wk0 = ((const f32x4 *)kn)[l32];
+        wk1 = ((const f32x4 *)kn)[l32 + 32];
+        c = *(const f32x4 *)(cos_t + tab);
+        sn = *(const f32x4 *)(sin_t + tab);
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            ss[i] = 0.f;
+            if (2 * i + h < per_tok)
+                ss[i] = x[i][0].x * x[i][0].x + x[i][0].y * x[i][0].y + x[i][0].z * x[i][0].z +
+                        x[i][0].w * x[i][0].w + x[i][1].x * x[i][1].x + x[i][1].y * x[i][1].y +
+                        x[i][1].z * x[i][1].z + x[i][1].w * x[i][1].w;
+        }
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) ss[i] = group_reduce<32, false>(ss[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+            ss[i] = 0.f;
+            if (2 * i + h < per_tok) {
+                x[i][0] = row[128 * i];
+                x[i][1] = row[128 * i + 32];
+                ss[i] = x[i][0].x * x[i][0].x + x[i][0].y * x[i][0].y + x[i][0].z * x[i][0].z +
+                        x[i][0].w * x[i][0].w + x[i][1].x * x[i][1].x + x[i][1].y * x[i][1].y +
+                        x[i][1].z * x[i][1].z + x[i][1].w * x[i][1].w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) ss[i] = group_reduce<32, false>(ss[i]);
+        wq0 = ((const f32x4 *)qn)[l32];
+        wq1 = ((const f32x4 *)qn)[l32 + 32];
+        wk0 = ((const f32x4 *)kn)[l32];
+        wk1 = ((const f32x4 *)kn)[l32 + 32];
+        const int64_t tab = (int64_t)pos[t] * 128 + 4 * l32;
+        c = *(const f32x4 *)(cos_t + tab);
+        sn = *(const f32x4 *)(sin_t + tab);
     }
-#pragma unroll
-    for (int i = 0; i < PAIRS; ++i) ss[i] = group_reduce<32, false>(ss[i]);
     bool ok = true;
 #pragma unroll
     for (int i = 0; i < PAIRS; ++i) {
@@ -387,7 +459,7 @@ __global__ __launch_bounds__(256) void qkv_post256_kernel(
 // head_dim 512 fast path: one wave per token. Lane l holds elements
 // [4l, 4l+4) and [256+4l, 256+4l+4) of every head row, so the rotate-half
 // partner of each element (j and j + 256) sits in the same lane.
-template <int ROWS>
+template <int ROWS, bool LOAD_FIRST>
 __global__ __launch_bounds__(256) void qkv_post512_kernel(
     float *__restrict__ qkv, int64_t ld, int64_t tokens, int nh, int nkv,
     const float *__restrict__ qn, const float *__restrict__ kn, const float *__restrict__ cos_t,
@@ -397,31 +469,56 @@ __global__ __launch_bounds__(256) void qkv_post512_kernel(
     if (t >= tokens) return;
     const int per_tok = nh + 2 * nkv;
     f32x4 *row = (f32x4 *)(qkv + t * ld) + lane;
-    // every operand loaded before any arithmetic, as in qkv_post256_kernel
-    const int64_t tab = (int64_t)pos[t] * 256 + 4 * lane;
-    f32x4 x[ROWS][2];
-#pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-        const int kr = min(k, per_tok - 1);
-        x[k][0] = row[128 * kr];
-        x[k][1] = row[128 * kr + 64];
-    }
-    const f32x4 wq0 = ((const f32x4 *)qn)[lane], wq1 = ((const f32x4 *)qn)[lane + 64];
-    const f32x4 wk0 = ((const f32x4 *)kn)[lane], wk1 = ((const f32x4 *)kn)[lane + 64];
-    const f32x4 c = *(const f32x4 *)(cos_t + tab);
-    const f32x4 sn = *(const f32x4 *)(sin_t + tab);
+    f32x4 x[ROWS][2], wq0, wq1, wk0, wk1, c, sn;
     float ss[ROWS];
+    if constexpr (LOAD_FIRST) {
+        // every operand loaded before any arithmetic, as in qkv_post256_kernel
+        const int64_t tab = (int64_t)pos[t] * 256 + 4 * lane;
 #pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-        ss[k] = 0.f;
-        if (k < per_tok)
-            ss[k] = x[k][0].x * x[k][0].x + x[k][0].y * x[k][0].y + x[k][0].z * x[k][0].z +
-                    x[k][0].w * x[k][0].w + x[k][1].x * x[k][1].x + x[k][1].y * x[k][1].y +
-                    x[k][1].z * x[k][1].z + x[k][1].w * x[k][1].w;
+        for (int k = 0; k < ROWS; ++k) {
+            const int kr = min(k, per_tok - 1);
+            x[k][0] = row[128 * kr];
+            x[k][1] = row[128 * kr + 64];
+        }
+        wq0 = ((const f32x4 *)qn)[lane];
+        wq1 = ((const f32x4 *)qn)[lane + 64];
+        wk0 = ((const f32x4 *)kn)[lane];
+        wk1 = ((const f32x4 *)kn)[lane + 64];
+        c = *(const f32x4 *)(cos_t + tab);
+        sn = *(const f32x4 *)(sin_t + tab);
+#pragma unroll
+        for (int k = 0; k < ROWS; ++k) {
+            ss[k] = 0.f;
+            if (k < per_tok)
+                ss[k] = x[k][0].x * x[k][0].x + x[k][0].y * x[k][0].y + x[k][0].z * x[k][0].z +
+                        x[k][0].w * x[k][0].w + x[k][1].x * x[k][1].x + x[k][1].y * x[k][1].y +
+                        x[k][1].z * x[k][1].z + x[k][1].w * x[k][1].w;
+        }
+#pragma unroll
+        for (int k = 0; k < ROWS; ++k)
+            if (k < per_tok) ss[k] = wave_sum(ss[k]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < ROWS; ++k) {
+            if (k < per_tok) {
+                x[k][0] = row[128 * k];
+                x[k][1] = row[128 * k + 64];
+                ss[k] = x[k][0].x * x[k][0].x + x[k][0].y * x[k][0].y + x[k][0].z * x[k][0].z +
+                        x[k][0].w * x[k][0].w + x[k][1].x * x[k][1].x + x[k][1].y * x[k][1].y +
+                        x[k][1].z * x[k][1].z + x[k][1].w * x[k][1].w;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < ROWS; ++k)
+            if (k < per_tok) ss[k] = wave_sum(ss[k]);
+        wq0 = ((const f32x4 *)qn)[lane];
+        wq1 = ((const f32x4 *)qn)[lane + 64];
+        wk0 = ((const f32x4 *)kn)[lane];
+        wk1 = ((const f32x4 *)kn)[lane + 64];
+        const int64_t tab = (int64_t)pos[t] * 256 + 4 * lane;
+        c = *(const f32x4 *)(cos_t + tab);
+        sn = *(const f32x4 *)(sin_t + tab);
     }
-#pragma unroll
-    for (int k = 0; k < ROWS; ++k)
-        if (k < per_tok) ss[k] = wave_sum(ss[k]);
     bool ok = true;
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
@@ -456,17 +553,32 @@ hipError_t launch_qkv_post(float *qkv, int64_t ld, int64_t tokens, int nh, int n
     const bool aligned = ld % 4 == 0 && (uintptr_t)qkv % 16 == 0;
     if (hd == 256 && aligned && nh + 2 * nkv <= 8) {
         const dim3 grid((unsigned)((tokens + 3) / 4));
-        if (nh + 2 * nkv <= 6)
-            hipLaunchKernelGGL(qkv_post256_kernel<3>, grid, dim3(256), 0, s, qkv, ld, tokens, nh,
-                               nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
-        else
-            hipLaunchKernelGGL(qkv_post256_kernel<4>, grid, dim3(256), 0, s, qkv, ld, tokens, nh,
-                               nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
+        const bool first = tokens < LOAD_FIRST_MAX_ROWS;
+        if (nh + 2 * nkv <= 6) {
+            if (first)
+                hipLaunchKernelGGL((qkv_post256_kernel<3, true>), grid, dim3(256), 0, s, qkv, ld,
+                                   tokens, nh, nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
+            else
+                hipLaunchKernelGGL((qkv_post256_kernel<3, false>), grid, dim3(256), 0, s, qkv, ld,
+                                   tokens, nh, nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
+        } else {
+            if (first)
+                hipLaunchKernelGGL((qkv_post256_kernel<4, true>), grid, dim3(256), 0, s, qkv, ld,
+                                   tokens, nh, nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
+            else
+                hipLaunchKernelGGL((qkv_post256_kernel<4, false>), grid, dim3(256), 0, s, qkv, ld,
+                                   tokens, nh, nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
+        }
         return hipGetLastError();
     }
     if (hd == 512 && aligned && nh + 2 * nkv <= 6) {
-        hipLaunchKernelGGL(qkv_post512_kernel<6>, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0,
-                           s, qkv, ld, tokens, nh, nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
+        const dim3 grid((unsigned)((tokens + 3) / 4));
+        if (tokens < LOAD_FIRST_MAX_ROWS)
+            hipLaunchKernelGGL((qkv_post512_kernel<6, true>), grid, dim3(256), 0, s, qkv, ld,
+                               tokens, nh, nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
+        else
+            hipLaunchKernelGGL((qkv_post512_kernel<6, false>), grid, dim3(256), 0, s, qkv, ld,
+                               tokens, nh, nkv, qn, kn, cos_t, sin_t, pos, eps, flag);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(qkv_post_kernel, dim3((unsigned)((head_rows + 3) / 4)), dim3(256), 0, s,
