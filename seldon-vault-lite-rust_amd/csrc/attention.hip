@@ -673,10 +673,11 @@ int attn_block_vectors(int hd) {
 // 16-key tiles). Grids of fewer than 128 work items split every item over 4 or
 // 8 workgroups of fewer waves; below 64 items each 16-vector group also takes
 // OS waves that split the output dims (4 at head_dim 256, 2 at 128), up to
-// one wave per SIMD (32 items at OS 4), with three LDS stages. Per layer, the
-// 1 x 128-token row's attention (3 items) went from 24.0 to 17.6 us, a
-// 754-token row's from 124 to 83 us (two stages: 17.8 and 85 us; four: 18.0
-// and 85 us).
+// one wave per SIMD (32 items at OS 4). Per layer, the 1 x 128-token row's
+// attention (3 items) went from 24.0 to 17.6 us, a 754-token row's from 124
+// to 83 us. Two LDS stages: with the partial sums interleaved, a timing
+// harness put the 128-token row at 11.1 us against 11.5 us for three stages,
+// and the one-row forward went from 1.822 to 1.811 ms (two A/B pairs).
 // Workgroups go to XCDs in contiguous chunks of the work list when a sliding
 // window is narrower than every row (the 8 x 2048-token batch's sliding
 // layers: 0.42 against 0.54 ms per launch). Every work item then spans about
@@ -700,7 +701,7 @@ static hipError_t launch_attn16(const AttnArgs &a, hipStream_t s) {
     else if constexpr (DS == 1 && HD >= 128) {
         constexpr int OS = HD / 64 >= 4 ? 4 : HD / 64;
         if (OS * 8 * t <= 1024)
-            hipLaunchKernelGGL((attn16_kernel<HD, OS, KT, OS, 3>), dim3((unsigned)(8 * t)),
+            hipLaunchKernelGGL((attn16_kernel<HD, OS, KT, OS, 2>), dim3((unsigned)(8 * t)),
                                dim3(64 * OS), 0, s, a, chunks);
         else
             hipLaunchKernelGGL((attn16_kernel<HD, 2, KT, 2>), dim3((unsigned)(8 * t)), dim3(128),
