@@ -253,6 +253,12 @@ def test_audio_embedder_matches_oracle():
     one = emb.embed_mel(mels[1], 768)
     batch = emb.embed_batch(mels, 768)
     assert np.array_equal(one, batch[1])
+    # the prompts through the text encoder in one pass each (a 20-token pass budget)
+    tm.set_pass_tokens(20)
+    try:
+        assert emb.embed_batch(mels, 768).tobytes() == batch.tobytes()
+    finally:
+        tm.set_pass_tokens(0)
     feats = torch.from_numpy(np.concatenate([m.features for m in mels])).to("cuda:0")
     torch.cuda.synchronize()
     assert np.array_equal(emb.embed_device(feats.data_ptr(), mels, 768), batch)

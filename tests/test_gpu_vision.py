@@ -153,9 +153,11 @@ def test_device_resident_matches_host(tower_v2):
 def test_batches_run_in_passes_bit_for_bit(tower_v2, embedder):
     """A batch whose workspace would pass the budget runs as passes of
     consecutive images. At a 300-patch budget the images below (108, 144, 324,
-    90 and 108 patches) take three passes, the 324-patch image alone. The soft
-    tokens, the captured hidden states, the device entry point and the image
-    embedder equal the one-pass run bit for bit."""
+    90 and 108 patches) take three passes, the 324-patch image alone, and with
+    a 30-token text budget their prompts (16, 20, 40, 14 and 16 tokens) take
+    the text encoder in four passes. The soft tokens, the captured hidden
+    states, the device entry point and the image embedder equal the one-pass
+    run bit for bit."""
     import torch
     w, gpu, om = tower_v2
     emb, _, _ = embedder
@@ -167,6 +169,7 @@ def test_batches_run_in_passes_bit_for_bit(tower_v2, embedder):
     for budget in (0, 300):
         gpu.set_pass_patches(budget)
         emb.vision.set_pass_patches(budget)
+        emb.model.set_pass_tokens(30 if budget else 0)
         try:
             host = gpu.forward_batch(patches, capture_hidden=True)
             d_pix = torch.from_numpy(pix).to("cuda:0")
@@ -177,6 +180,7 @@ def test_batches_run_in_passes_bit_for_bit(tower_v2, embedder):
         finally:
             gpu.set_pass_patches(0)
             emb.vision.set_pass_patches(0)
+            emb.model.set_pass_tokens(0)
     (h1, d1, e1), (h2, d2, e2) = runs
     for i in range(len(patches)):
         assert h1[i].pooled().tobytes() == h2[i].pooled().tobytes(), f"image {i}"
