@@ -322,7 +322,9 @@ __global__ __launch_bounds__(64 * WAVES, (attn_min_blocks<HD, WAVES, NS>())) voi
     const int wg = xcd_chunks ? xcd_chunk((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
     const AttnTile tile = p.tiles[wg / SPLIT];
     const int G = p.nh / p.nkv;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // a scalar wave index: the DMA's LDS destinations (M0) then need no
+    // v_readfirstlane per instruction
+    const int lane = threadIdx.x & 63, wave = uniform((int)threadIdx.x >> 6);
     const int l16 = lane & 15, g = lane >> 4;
     const int dpart = DS > 1 ? wave % DS : 0;  // this wave's block of head dims
     const int opart = OS > 1 ? wave % OS : 0;  // this wave's block of output dims

@@ -442,7 +442,16 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
         tn = tile - tm * tiles_n;
     }
     const int m0 = tm * BM, n0 = tn * BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // The wave index through v_readfirstlane: the LDS destinations of the
+    // DMA instructions (M0) then come from scalar registers, set by one
+    // s_mov each, instead of a v_readfirstlane before every instruction of
+    // every slice (T2 gate/up 479 -> 466 us, the 64x64 projections 5 %).
+    // The one- or two-chain tiles that spread their DMA over the steps keep
+    // it in a vector register: the audio tower's K = 4096 FFN down took 198
+    // against 206 us that way, and its tower 15.17 against 15.40 ms.
+    constexpr bool CHAIN_SPREAD = TM * TN <= 2 && MINB >= 2;
+    const int tid = threadIdx.x, lane = tid & 63,
+              wave = CHAIN_SPREAD ? tid >> 6 : uniform(tid >> 6);
     const int wm = wave / WNW, wn = wave % WNW;
     const int l16 = lane & 15, g = lane >> 4;
     const int M = p.M, N = p.N;
@@ -583,8 +592,8 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
         __syncthreads();   // ... and every wave's; slice kt-1 is no longer read
         constexpr bool CHAIN = TM * TN <= 2;  // one or two accumulator chains per wave
         // several workgroups per CU: spread the next slice's DMA issue over
-        // the steps (below)
-        constexpr bool SPREAD = CHAIN && MINB >= 2;
+        // the MFMAs (below)
+        constexpr bool SPREAD = MINB >= 2;
         using NEXT = std::integral_constant<int, (cur + NS - 1) % NS>;
         const bool refill = kt + NS - 1 < nk;
         if constexpr (!SPREAD)
@@ -598,7 +607,8 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
 #pragma unroll
             for (int j = 0; j < TN; ++j) b[j] = *(const f32x4 *)(ws + j * 16 * BK + 4 * pos);
         };
-        auto mfmas = [&](const f32x4 (&a)[TM], const f32x4 (&b)[TN], auto &&mid) {
+        // the four MFMA rounds of a 16-k step; after(s) runs behind round s
+        auto mfmas = [&](const f32x4 (&a)[TM], const f32x4 (&b)[TN], auto &&after) {
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
 #pragma unroll
@@ -607,7 +617,7 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
                     for (int j = 0; j < TN; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b[j][s], a[i][s],
                                                                          acc[i][j], 0, 0, 0);
-                if (s == 0) mid();
+                after(s);
             }
         };
         if constexpr (CHAIN) {
@@ -630,7 +640,8 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
                 if (kk + 16 < BK) frags(kk + 16, na, nb);
                 __builtin_amdgcn_sched_barrier(0);
                 const int t = kk / 16;
-                mfmas(a, b, [&] {
+                mfmas(a, b, [&](int s) {
+                    if (s != 0) return;
                     if (SPREAD && refill) {
 #pragma unroll
                         for (int q = 0; q < NDMA; ++q)
@@ -646,11 +657,29 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
                 }
             }
         } else {
+            // Larger wave tiles: with several workgroups per CU, DMA
+            // instruction q of the next slice goes behind MFMA round
+            // q * NR / NDMA of the first half of this slice's rounds rather
+            // than all of them before its first MFMA (the T2 gate/up 467 ->
+            // 462 us, the 128x128 projections of 18688 rows 495 -> 486 us;
+            // over all the rounds, the last DMA issued at the slice's end,
+            // 464 and 488 us, and the audio tower's FFN up 187 against 182 us).
+            constexpr int NDMA = A_CH + W_CH, NR = BK / 16 * 2;  // MFMA rounds per half slice
 #pragma unroll
             for (int kk = 0; kk < BK; kk += 16) {
                 f32x4 a[TM], b[TN];
                 frags(kk, a, b);
-                mfmas(a, b, [] {});
+                const int r0 = kk / 16 * 4;
+                mfmas(a, b, [&](int s) {
+                    if constexpr (SPREAD) {
+                        if (refill) {
+#pragma unroll
+                            for (int q = 0; q < NDMA; ++q)
+                                if (q * NR / NDMA == r0 + s) issue_one(NEXT{}, (kt + NS - 1) * BK, q);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                });
             }
         }
     };
