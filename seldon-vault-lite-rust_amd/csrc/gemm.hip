@@ -840,9 +840,11 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
             if (a.K % 64 == 0) return launch_dma<32, 64, 64, EPI, 1, 3, 2>(a, s);
             return launch_dma<32, 64, 32, EPI, 1, 4, 2>(a, s);
         }
-        // concurrent row groups: 128x128 tiles at three per CU (the T2 step
-        // 39.66 against 39.9 ms with 64x128x32 tiles, same box)
-        if (a.cus > 0 && a.K % 16 == 0) return launch_dma<128, 128, 16, EPI, 3, 2>(a, s);
+        // concurrent row groups: 64x128x16 tiles at four per CU, as for the
+        // whole batch (the T2 step 37.57-37.64 against 37.98-38.04 ms with
+        // 128x128x16 tiles at three per CU, which had led before the DMA
+        // issue moved behind the MFMAs; same box)
+        if (a.cus > 0 && a.K % 16 == 0) return launch_dma<64, 128, 16, EPI, 4, 2>(a, s);
         if (tiles(128, 128) < 2 * 256) {
             // grids of a few thousand rows: tiles small enough to spread over
             // every CU (gate/up at 1040 / 2000 / 3016 rows: 34.7 / 63.8 / 88.0
