@@ -779,9 +779,9 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 //    256 CUs, so it takes about ceil(tiles / 256) tile-times on its busiest
 //    CU; the cost of a tile shape is that count times the tile's MAC count
 //    over the shape's measured efficiency (128x128 at 3 per CU and 64x64 at
-//    4 per CU: 1.0; 128x64 at 4 per CU: 0.95), ties going to the larger
-//    tile (the audio tower's M = 3000 x 4096 projection: 250 us at 128x128,
-//    275 us at 64x64). With 16x16 fragments 64x64 tiles keep up with larger
+//    4 per CU: 1.0; 128x64 at 4 per CU: 0.95; 64x32 at 4 per CU: 0.93),
+//    ties going to the larger tile (the audio tower's M = 3000 x 4096
+//    projection: 250 us at 128x128, 275 us at 64x64). With 16x16 fragments 64x64 tiles keep up with larger
 //    ones (the 18688-token O projection: 168 us against 202 us for 128x64
 //    tiles), and their finer grid wastes less of the last round.
 //  * A launch that shares the GPU with other streams (a.cus > 0, the text
@@ -879,14 +879,19 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
             return launch_dma_staged<128, 128, 16, EPI, 3, 3>(a, s);
         }
         if (a.N <= 32 && a.K % 32 == 0) return launch_dma<128, 32, 32, EPI, 4, 2, 4>(a, s);
-        // less than one round of 64x64 tiles at four per CU: 64x32 tiles
-        // spread the work over every CU (N = 768 at 2000 / 3016 / 4500 rows:
-        // 22.1 / 33.2 / 49.5 us against 28.4 / 39.6 / 55.0 us)
-        if (tiles(64, 64) < 4 * 256 && a.K % 32 == 0) return launch_dma<64, 32, 32, EPI, 4, 2, 2>(a, s);
+        // The least work on the busiest CU, over the shape's efficiency. 64x32
+        // tiles (one or two accumulator blocks per wave) run at 0.93 of 64x64
+        // ones, and their finer grid evens out grids of a few thousand rows: at
+        // 3000 rows N = 768 (K = 1536) took 63.7 against 70.9 us for 64x64
+        // tiles (564 of them leave CUs with two or three) and N = 1536 74.6
+        // against 79.4 us, while N = 1024 (752 64x64 tiles, three per CU)
+        // took 190.6 against 205.8 us at K = 4096 on 64x64 tiles.
         auto per_cu = [&](int bm, int bn) { return (double)((tiles(bm, bn) + 255) / 256); };
         const double c128 = per_cu(128, 128) * (128.0 * 128.0);
         const double c12864 = per_cu(128, 64) * (128.0 * 64.0) / 0.95;
         const double c64 = per_cu(64, 64) * (64.0 * 64.0);
+        const double c6432 = a.K % 32 == 0 ? per_cu(64, 32) * (64.0 * 32.0) / 0.93 : 1e300;
+        if (c6432 < c64 && c6432 < c128 && c6432 < c12864) return launch_dma<64, 32, 32, EPI, 4, 2, 2>(a, s);
         if (c64 < c128 && c64 < c12864) {
             if (a.K % 32 == 0) return launch_dma_staged<64, 64, 32, EPI, 4, 3>(a, s);
             return launch_dma_staged<64, 64, 16, EPI, 4, 4>(a, s);
