@@ -781,9 +781,10 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 //    over the shape's measured efficiency (128x128 at 3 per CU and 64x64 at
 //    4 per CU: 1.0; 128x64 at 4 per CU: 0.95; 64x32 at 4 per CU: 0.93),
 //    ties going to the larger tile (the audio tower's M = 3000 x 4096
-//    projection: 250 us at 128x128, 275 us at 64x64). With 16x16 fragments 64x64 tiles keep up with larger
-//    ones (the 18688-token O projection: 168 us against 202 us for 128x64
-//    tiles), and their finer grid wastes less of the last round.
+//    projection: 250 us at 128x128, 275 us at 64x64). With 16x16 fragments
+//    64x64 tiles keep up with larger ones (the 18688-token O projection:
+//    168 us against 202 us for 128x64 tiles), and their finer grid wastes
+//    less of the last round.
 //  * A launch that shares the GPU with other streams (a.cus > 0, the text
 //    path's row groups): 64x64 (O and down per group: 65 and 93 us against
 //    75 and 110 us for 128x64); the other streams' work fills the partial
@@ -795,8 +796,8 @@ static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
 //    joined through LDS for the epilogue.
 //  * Otherwise paired epilogues keep the 32 + 32 columns of a pair in one
 //    wave: 64x128 tiles (4 per CU; the 18688-token gate/up: 481 us against
-//    502 us for 128x128; per row group, with 32-wide K slices: 168 us against
-//    185 us), with deeper pipelines below two rounds of 128x128 tiles.
+//    502 us for 128x128), for the row groups too, with deeper pipelines below
+//    two rounds of 128x128 tiles.
 //  * Outputs of at most 32 columns (the audio subsampling's 32 channels):
 //    128x32 tiles, the four waves stacked along M, instead of 64x64 tiles
 //    that would spend half their MFMAs on zero columns.
