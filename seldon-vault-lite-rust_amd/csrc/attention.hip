@@ -672,12 +672,13 @@ int attn_block_vectors(int hd) {
 // arithmetic never depends on the launch): 16 keys at head_dim 256 (64 KB
 // double buffered, two 4-wave workgroups per CU), 32 at 128 and at 64 (the
 // vision tower: 31.4 ms per 4 images against 31.8 with 64-key and 32.5 with
-// 16-key tiles). Grids of fewer than 128 work items split every item over 4 or
-// 8 workgroups of fewer waves; below 64 items each 16-vector group also takes
-// OS waves that split the output dims (4 at head_dim 256, 2 at 128), up to
-// one wave per SIMD (32 items at OS 4). Per layer, the 1 x 128-token row's
-// attention (3 items) went from 24.0 to 17.6 us, a 754-token row's from 124
-// to 83 us. Two LDS stages: with the partial sums interleaved, a timing
+// 16-key tiles). At head_dim 128 and 256, grids of up to 64 work items split
+// every item over 8 workgroups whose 16-vector group takes OS waves that
+// split the output dims (4 at head_dim 256, 2 at 128); larger grids run two
+// 4-wave workgroups per item. Other head dims split grids of fewer than 128
+// items over 4 or 8 workgroups of fewer waves. Per layer, the 1 x 128-token
+// row's attention (3 items) went from 24.0 to 17.6 us, a 754-token row's
+// from 124 to 83 us. Two LDS stages: with the partial sums interleaved, a timing
 // harness put the 128-token row at 11.1 us against 11.5 us for three stages,
 // and the one-row forward went from 1.822 to 1.811 ms (two A/B pairs).
 // Workgroups go to XCDs in contiguous chunks of the work list when a sliding
@@ -694,21 +695,26 @@ static hipError_t launch_attn16(const AttnArgs &a, hipStream_t s) {
     constexpr int DS = attn_dim_split<HD>();
     const int64_t t = a.n_tiles;
     const int chunks = a.window >= 0 && a.shortest > a.window + 1;
-    if (2 * t >= 256)
+    if constexpr (DS == 1 && HD >= 128) {
+        // Up to 64 items, 8 workgroups of OS waves per item fill at most the
+        // 512 two-per-CU slots once; above that, two 4-wave workgroups per item
+        // (the 4 x 754-token audio prompts, 72 items: 116 against 122 us for
+        // four 2-wave workgroups per item; 36 items: 71 against 77 us for
+        // 8 workgroups of OS = 2 waves).
+        constexpr int OS = HD / 64 >= 4 ? 4 : HD / 64;
+        if (8 * t <= 512)
+            hipLaunchKernelGGL((attn16_kernel<HD, OS, KT, OS, 2>), dim3((unsigned)(8 * t)),
+                               dim3(64 * OS), 0, s, a, chunks);
+        else
+            hipLaunchKernelGGL((attn16_kernel<HD, 4, KT>), dim3((unsigned)(2 * t)), dim3(256), 0,
+                               s, a, chunks);
+    } else if (2 * t >= 256)
         hipLaunchKernelGGL((attn16_kernel<HD, 4 * DS, KT>), dim3((unsigned)(2 * t)),
                            dim3(256 * DS), 0, s, a, chunks);
     else if (4 * t >= 256)
         hipLaunchKernelGGL((attn16_kernel<HD, 2 * DS, KT>), dim3((unsigned)(4 * t)),
                            dim3(128 * DS), 0, s, a, chunks);
-    else if constexpr (DS == 1 && HD >= 128) {
-        constexpr int OS = HD / 64 >= 4 ? 4 : HD / 64;
-        if (OS * 8 * t <= 1024)
-            hipLaunchKernelGGL((attn16_kernel<HD, OS, KT, OS, 2>), dim3((unsigned)(8 * t)),
-                               dim3(64 * OS), 0, s, a, chunks);
-        else
-            hipLaunchKernelGGL((attn16_kernel<HD, 2, KT, 2>), dim3((unsigned)(8 * t)), dim3(128),
-                               0, s, a, chunks);
-    } else
+    else
         hipLaunchKernelGGL((attn16_kernel<HD, DS, KT>), dim3((unsigned)(8 * t)), dim3(64 * DS),
                            0, s, a, chunks);
     return hipGetLastError();

@@ -832,11 +832,13 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
     // instructions long.
     const bool tiny = tiles(64, 64) < 256 && a.K % 32 == 0;
     if constexpr (paired_epi<EPI>()) {
-        if (tiny) {
+        if (tiny && tiles(32, 64) <= 256) {
             // 32x64 tiles: the x and y halves of each pair on two waves, so a
             // wave's chain is 2 x K / 4 MFMAs (gate/up at 128 tokens: 12.1 us
             // against 17.6 us for 64x64 tiles with one 16x64 block per wave;
-            // three or four stages measured no faster)
+            // three or four stages measured no faster). They fill the GPU
+            // once at one workgroup per CU; larger grids take the rules below
+            // (gate/up at 256 tokens 17.2 against 20.0 us).
             if (a.K % 128 == 0) return launch_dma<32, 64, 128, EPI, 1, 2, 2>(a, s);
             if (a.K % 64 == 0) return launch_dma<32, 64, 64, EPI, 1, 3, 2>(a, s);
             return launch_dma<32, 64, 32, EPI, 1, 4, 2>(a, s);
@@ -863,9 +865,15 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
             // that is mostly memory latency. 256-wide slices (two 64 KB
             // stages) took the 1 x 128-token forward from 1.837 to 1.811 ms
             // against 128-wide ones; 128-wide took O at 128 tokens from 7.6
-            // to 7.0 us against 64-wide.
-            if (a.K % 256 == 0) return launch_dma<32, 32, 256, EPI, 1, 2>(a, s);
-            if (a.K % 128 == 0) return launch_dma<32, 32, 128, EPI, 1, 2>(a, s);
+            // to 7.0 us against 64-wide. Those hold one workgroup per CU, so
+            // they serve grids of one round; larger ones take 64-wide slices
+            // in three stages, three workgroups per CU (at 1040 tokens the
+            // N = 768 projections 15.7 against 20.8 us, the PLE gate 9.1
+            // against 11.3 us; at 520 tokens QKV 12.8 against 16.7 us).
+            if (tiles(32, 32) <= 256) {
+                if (a.K % 256 == 0) return launch_dma<32, 32, 256, EPI, 1, 2>(a, s);
+                if (a.K % 128 == 0) return launch_dma<32, 32, 128, EPI, 1, 2>(a, s);
+            }
             if (a.K % 64 == 0) return launch_dma<32, 32, 64, EPI, 1, 3>(a, s);
             return launch_dma<32, 32, 32, EPI, 1, 4>(a, s);
         }
