@@ -40,6 +40,7 @@
 //  * Epilogues fuse the elementwise op that follows each projection in
 //    text.rs (PLE scale, GeGLU, GELU-gate x per-layer input).
 #include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "dev_common.hpp"
@@ -896,7 +897,11 @@ static hipError_t launch_dma_auto(const GemmArgs &a, hipStream_t s) {
         // against 79.4 us, while N = 1024 (752 64x64 tiles, three per CU)
         // took 190.6 against 205.8 us at K = 4096 on 64x64 tiles.
         auto per_cu = [&](int bm, int bn) { return (double)((tiles(bm, bn) + 255) / 256); };
-        const double c128 = per_cu(128, 128) * (128.0 * 128.0);
+        // 128x128 tiles run three at a time per CU, and a CU's last round
+        // holds its remainder: their count is rounded up to whole rounds (the
+        // 16384-row QKV, five per CU: 268 us against 230 us for 64x64 tiles;
+        // the 3016-row QKV, one per CU: 52.6 against 49.0 us)
+        const double c128 = std::ceil(per_cu(128, 128) / 3.0) * 3.0 * (128.0 * 128.0);
         const double c12864 = per_cu(128, 64) * (128.0 * 64.0) / 0.95;
         const double c64 = per_cu(64, 64) * (64.0 * 64.0);
         const double c6432 = a.K % 32 == 0 ? per_cu(64, 32) * (64.0 * 32.0) / 0.93 : 1e300;
