@@ -121,7 +121,9 @@ def test_attention_kats():  # kernels.rs:1529-1566
     (1000, 3, 1, 256, 100), (700, 4, 1, 512, None), (300, 8, 2, 512, 40), (1000, 4, 1, 512, 100),
     (5, 4, 1, 512, None), (129, 2, 2, 512, 3), (2000, 3, 1, 256, 512), (900, 4, 4, 128, 64),
     # head_dim 512 with 128 and with 64 work items: the 8-wave and the 4-wave variants
-    (2048, 8, 2, 512, None), (1024, 8, 2, 512, 40)])
+    (2048, 8, 2, 512, None), (1024, 8, 2, 512, 40),
+    # 65 to 127 work items at head_dim 256 and 128: two 4-wave workgroups per item
+    (3000, 3, 1, 256, 512), (2500, 4, 1, 128, None)])
 def test_attention_matches_oracle(seq, nh, nkv, hd, window):
     rng = np.random.default_rng(seq + hd)
     # unit-RMS rows scaled like q/k after their norms (weights ~0.25)
