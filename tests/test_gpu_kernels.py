@@ -33,14 +33,17 @@ def test_linear_kat():  # kernels.rs:1401-1410
 
 
 # Shapes chosen to reach every tile path of the GEMM dispatcher: one-row
-# grids with 128-, 64- and 32-wide K slices (32x32 tiles), K not a multiple
-# of 32 (64x64x16) or of 16 (the register-staged kernel's K tail) or of 4
-# (the scalar kernel), grids large enough for the cost model's 64x64 and
-# 128x128 choices, and narrow outputs (128x32 tiles, ragged N included).
+# grids with 256-, 128-, 64- and 32-wide K slices (32x32 tiles), grids too
+# large for one round of those (64-wide slices, three stages), K not a
+# multiple of 32 (64x64x16) or of 16 (the register-staged kernel's K tail) or
+# of 4 (the scalar kernel), grids large enough for the cost model's 64x32,
+# 64x64 and 128x128 choices (128x128 counts rounded to whole rounds), and
+# narrow outputs (128x32 tiles, ragged N included).
 @pytest.mark.parametrize("rows,inf,outf", [
     (1, 768, 768), (37, 768, 1280), (130, 1152, 768), (257, 256, 768), (5, 12, 20), (3, 10, 7),
     (64, 16, 8), (300, 1120, 96), (129, 784, 40), (2000, 100, 300), (9000, 256, 64),
-    (2048, 768, 768), (4096, 768, 2304), (20000, 128, 32), (16500, 64, 20)])
+    (2048, 768, 768), (4096, 768, 2304), (20000, 128, 32), (16500, 64, 20),
+    (520, 768, 1280), (3000, 1024, 1024), (16384, 768, 1280)])
 def test_linear_matches_oracle(rows, inf, outf):
     rng = np.random.default_rng(rows * 7 + inf)
     x = rng.standard_normal((rows, inf)).astype(np.float32)
