@@ -35,8 +35,9 @@
 //  * Tiles are remapped so each XCD runs a contiguous range of the tile
 //    list, N fastest (the N tiles that share an A block hit that XCD's L2);
 //    launches of 128 M blocks or more with the whole GPU order the range in
-//    groups of 8 M blocks, M fastest within an N block, so the tiles in
-//    flight on an XCD share a few A blocks and W panels.
+//    groups of 8 M blocks, M fastest within an N block and the N blocks of
+//    every second group in reverse, so the tiles in flight on an XCD share a
+//    few A blocks and W panels.
 //  * Epilogues fuse the elementwise op that follows each projection in
 //    text.rs (PLE scale, GeGLU, GELU-gate x per-layer input).
 #include <algorithm>
@@ -433,11 +434,14 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_dma(GemmArgs p, int tiles_m
         // Within that range, groups of RASTER_M M blocks run N block by N
         // block, M fastest: the tiles in flight together on an XCD then share
         // a few W panels and A blocks in its L2 (the T2 gate/up launch fetched
-        // 188 against 491 MiB with N fastest, at the same speed).
+        // 188 against 491 MiB with N fastest, at the same speed). Odd groups
+        // run the N blocks in reverse, so a group starts on the W panels the
+        // one before it ended on (the same launch fetched 187 against 217 MiB,
+        // at the same speed).
         const int gsize = RASTER_M * tiles_n, grp = tile / gsize, first = grp * RASTER_M;
         const int gm = min(RASTER_M, tiles_m - first), in = tile - grp * gsize;
         tm = uniform(first + in % gm);
-        tn = uniform(in / gm);
+        tn = uniform(grp & 1 ? tiles_n - 1 - in / gm : in / gm);
     } else {
         tm = uniform(tile / tiles_n);
         tn = tile - tm * tiles_n;
