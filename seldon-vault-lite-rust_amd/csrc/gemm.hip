@@ -34,7 +34,8 @@
 //    when even 64x64 tiles would not cover the GPU once.
 //  * Tiles are remapped so each XCD runs a contiguous range of the tile
 //    list, N fastest (the N tiles that share an A block hit that XCD's L2);
-//    launches of 128 M blocks or more with the whole GPU order the range in
+//    launches of 128 M blocks or more with the whole GPU (32 or more when
+//    the launch shares the GPU with other streams) order the range in
 //    groups of 8 M blocks, M fastest within an N block and the N blocks of
 //    every second group in reverse, so the tiles in flight on an XCD share a
 //    few A blocks and W panels.
@@ -368,10 +369,14 @@ __global__ __launch_bounds__(256, MINB) void gemm_nt_mfma(GemmArgs p, int tiles_
 }
 
 // M blocks per rasterization group of the DMA kernel's tile order, and the
-// fewest M blocks of a whole-GPU launch that takes the grouped order (the
-// 1 x 128-token forward went from 2.00 to 2.04 ms and the audio tower lost
-// 1 % with it; the T2 launches kept their time and fetched 2.6x less).
-constexpr int RASTER_M = 8, RASTER_MIN_TILES_M = 128;
+// fewest M blocks of a launch that takes the grouped order: 128 for a launch
+// with the whole GPU (below that the 1 x 128-token forward went from 2.00 to
+// 2.04 ms and the audio tower lost 1 % with it; the T2 launches kept their
+// time and fetched 2.6x less), 32 for one that shares the GPU with other
+// streams (the T2 row groups, about 98 M blocks each: 1695-1696 against
+// 1680-1690 embeddings/s, and the image tower 29.31-29.37 against
+// 29.48-29.64 ms; 16 and 64 measured the same as 32).
+constexpr int RASTER_M = 8, RASTER_MIN_TILES_M = 128, RASTER_MIN_TILES_M_SHARED = 32;
 
 // Direct-to-LDS variant; requires K % BK == 0 and 16-byte aligned rows. NS
 // LDS stages: NS - 1 slices are in flight while one is consumed. WMW waves
@@ -768,7 +773,7 @@ template <int BM, int BN, int BK, int EPI, int MINB, int NS, int WMW = 2, bool C
 static hipError_t launch_dma(const GemmArgs &a, hipStream_t s) {
     const int tm = (a.M + BM - 1) / BM, tn = (a.N + BN - 1) / BN;
     if constexpr (!CONV) {
-        if (a.cus == 0 && tm >= RASTER_MIN_TILES_M) {
+        if (tm >= (a.cus > 0 ? RASTER_MIN_TILES_M_SHARED : RASTER_MIN_TILES_M)) {
             hipLaunchKernelGGL((gemm_nt_dma<BM, BN, BK, EPI, MINB, NS, WMW, false, true>),
                                dim3(tm * tn), dim3(256), 0, s, a, tm, tn);
             return hipGetLastError();
