@@ -58,6 +58,27 @@ def test_linear_matches_oracle(rows, inf, outf):
         np.testing.assert_allclose(got, ref, atol=2e-4 * np.abs(exact).max(), rtol=0)
 
 
+# A row's output bits do not depend on the launch around it: every tile shape
+# and tile order runs the same MFMA sequence over k. The whole launches here
+# take the grouped tile order (128 M blocks or more; a partial last group, the
+# odd groups' N blocks in reverse) on 128x32, 64x64 and 64x32 tiles; 100-row
+# slices take 32x32 tiles in the plain order.
+@pytest.mark.parametrize("rows,inf,outf", [
+    (16500, 64, 20), (9000, 768, 2304), (18688, 768, 256), (8229, 1152, 768)])
+def test_linear_rows_do_not_depend_on_the_launch(rows, inf, outf):
+    rng = np.random.default_rng(rows + outf)
+    x = rng.standard_normal((rows, inf)).astype(np.float32)
+    w = (rng.standard_normal((outf, inf)) / np.sqrt(inf)).astype(np.float32)
+    xd, wd = dev(x), dev(w)
+    out = empty(rows * outf)
+    S.linear(xd, wd, rows, inf, outf, out)
+    full = host(out).reshape(rows, outf)
+    part = empty(100 * outf)
+    for r0 in (0, rows // 2 + 3, rows - 100):
+        S.linear(xd[r0:r0 + 100], wd, 100, inf, outf, part)
+        np.testing.assert_array_equal(host(part).reshape(100, outf), full[r0:r0 + 100])
+
+
 def test_linear_rejects_nonfinite_output():
     out = empty(1)
     with pytest.raises(S.SvlError) as e:

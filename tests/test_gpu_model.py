@@ -237,6 +237,28 @@ def test_two_stream_row_groups_are_bit_identical():
         assert m.forward(r).normalized().tobytes() == a.normalized().tobytes()
 
 
+def test_row_groups_in_grouped_tile_order_are_bit_identical():
+    # About 16,000 tokens: each of the three row groups' GEMMs has 80 or more
+    # 64-row M blocks, so the shared launches take the grouped tile order
+    # (odd groups of 8 M blocks run their N blocks in reverse, the last group
+    # is partial); the single-stream launches of the whole batch take it too,
+    # and one row alone runs small tiles in the plain order.
+    cfg = svl_synth.config_a(layers=2, vocab=4096)
+    w = svl_synth.weights(cfg)
+    m = model(cfg, w)
+    lengths = [300 + (97 * i) % 213 for i in range(40)]
+    rows = svl_synth.token_rows(4096, lengths, seed=5)
+    split = m.forward_batch(rows, capture_hidden=True)
+    m.set_stream_split(False)
+    single = m.forward_batch(rows, capture_hidden=True)
+    m.set_stream_split(True)
+    for a, b in zip(split, single):
+        assert a.normalized().tobytes() == b.normalized().tobytes()
+        assert a.hidden_states().tobytes() == b.hidden_states().tobytes()
+    for i in (0, 13, 39):
+        assert m.forward(rows[i]).normalized().tobytes() == split[i].normalized().tobytes()
+
+
 def test_batches_run_in_passes_bit_for_bit():
     """A batch whose workspace would pass the budget runs as passes of
     consecutive rows. At a 700-token budget the 13 rows below take ten passes
