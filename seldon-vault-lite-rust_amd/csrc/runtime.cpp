@@ -80,6 +80,12 @@ struct TimedLaunch {
     hipEvent_t a, b;
 };
 
+// Typed view into the model's metadata block (set by upload_batch_meta).
+template <typename T>
+struct MetaView {
+    T *p = nullptr;
+};
+
 }  // namespace
 
 struct svl_text_model {
@@ -109,11 +115,19 @@ struct svl_text_model {
 
     // workspace
     DevBuf<float> h, n, tmp, qkv, attn, act, ple, pg, proj, feats, pooled, normalized, trunc;
-    DevBuf<int32_t> pos, rowlen, featmap, dims;
+    DevBuf<int32_t> pos, rowlen, featmap;
     DevBuf<uint32_t> ids;
-    DevBuf<int64_t> offsets;
-    DevBuf<AttnTile> tiles;
-    DevBuf<int> flag;
+    // A pass's metadata in one device block, filled by one copy from pinned
+    // host memory: the error flag (cleared), the Matryoshka dims, the row
+    // offsets and the attention work items (the views below).
+    DevBuf<unsigned char> meta;
+    unsigned char *h_meta = nullptr;  // pinned staging of `meta`
+    size_t h_meta_n = 0;
+    hipEvent_t ev_meta = nullptr;     // after the last copy out of h_meta
+    MetaView<int> flag;
+    MetaView<int32_t> dims;
+    MetaView<int64_t> offsets;
+    MetaView<AttnTile> tiles;
     int *h_flag = nullptr;  // pinned
 
     // kernel timing
@@ -134,8 +148,12 @@ struct svl_text_model {
         h.release(); n.release(); tmp.release(); qkv.release(); attn.release(); act.release();
         ple.release(); pg.release(); proj.release(); feats.release(); pooled.release();
         normalized.release(); trunc.release(); pos.release(); rowlen.release();
-        featmap.release(); dims.release(); ids.release(); offsets.release(); tiles.release();
-        flag.release();
+        featmap.release(); ids.release(); meta.release();
+        if (ev_meta) {
+            (void)hipEventSynchronize(ev_meta);
+            (void)hipEventDestroy(ev_meta);
+        }
+        if (h_meta) (void)hipHostFree(h_meta);
         if (h_flag) (void)hipHostFree(h_flag);
         for (auto &e : event_pool) (void)hipEventDestroy(e);
         for (auto &t : pending) {
@@ -459,11 +477,8 @@ svl_status ensure_workspace(svl_text_model *m, const Batch &b, int64_t feat_floa
     HIP_TRY(m->pos.ensure(T));
     HIP_TRY(m->rowlen.ensure(T));
     HIP_TRY(m->ids.ensure(T));
-    HIP_TRY(m->offsets.ensure(std::max<size_t>(b.dev_offsets.size(), 1)));
-    HIP_TRY(m->tiles.ensure(std::max<size_t>(b.tiles.size(), 1)));
     HIP_TRY(m->pooled.ensure((size_t)b.B * m->E));
     HIP_TRY(m->normalized.ensure((size_t)b.B * m->E));
-    HIP_TRY(m->flag.ensure(1));
     if (feat_floats > 0) HIP_TRY(m->feats.ensure(feat_floats));
     if (need_featmap) HIP_TRY(m->featmap.ensure(T));
     if (dims_total > 0) HIP_TRY(m->trunc.ensure((size_t)b.B * dims_total));
@@ -751,13 +766,40 @@ std::vector<std::pair<int32_t, int32_t>> row_passes(const svl_text_model *m,
     return passes;
 }
 
-svl_status upload_batch_meta(svl_text_model *m, const Batch &b, hipStream_t s) {
-    HIP_TRY(hipMemcpyAsync(m->offsets.p, b.dev_offsets.data(),
-                           b.dev_offsets.size() * sizeof(int64_t), hipMemcpyHostToDevice, s));
+// The pass's metadata as one block: the error flag (zero), `n_dims`
+// Matryoshka dims, the row offsets and the attention work items, staged in
+// pinned host memory and sent by one copy on `s` (a copy or fill per array
+// costs a transfer each on the stream, about 10 us apiece at one row). The
+// staging is rewritten only once the copy before has left it.
+svl_status upload_batch_meta(svl_text_model *m, const Batch &b, hipStream_t s,
+                             const int32_t *dims = nullptr, int n_dims = 0) {
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t off_dims = 256;
+    const size_t off_offs = off_dims + up((size_t)n_dims * sizeof(int32_t));
+    const size_t off_tiles = off_offs + up(b.dev_offsets.size() * sizeof(int64_t));
+    const size_t used = off_tiles + b.tiles.size() * sizeof(AttnTile);
+    HIP_TRY(m->meta.ensure(up(used)));
+    if (m->ev_meta) HIP_TRY(hipEventSynchronize(m->ev_meta));
+    else HIP_TRY(hipEventCreateWithFlags(&m->ev_meta, hipEventDisableTiming));
+    if (m->h_meta_n < used) {
+        if (m->h_meta) HIP_TRY(hipHostFree(m->h_meta));
+        m->h_meta = nullptr;
+        m->h_meta_n = 0;
+        HIP_TRY(hipHostMalloc((void **)&m->h_meta, up(used), hipHostMallocDefault));
+        m->h_meta_n = up(used);
+    }
+    unsigned char *h = m->h_meta, *d = m->meta.p;
+    std::memset(h, 0, off_offs);
+    if (n_dims > 0) std::memcpy(h + off_dims, dims, (size_t)n_dims * sizeof(int32_t));
+    std::memcpy(h + off_offs, b.dev_offsets.data(), b.dev_offsets.size() * sizeof(int64_t));
     if (!b.tiles.empty())
-        HIP_TRY(hipMemcpyAsync(m->tiles.p, b.tiles.data(), b.tiles.size() * sizeof(AttnTile),
-                               hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemsetAsync(m->flag.p, 0, sizeof(int), s));
+        std::memcpy(h + off_tiles, b.tiles.data(), b.tiles.size() * sizeof(AttnTile));
+    m->flag.p = (int *)d;
+    m->dims.p = n_dims > 0 ? (int32_t *)(d + off_dims) : nullptr;
+    m->offsets.p = (int64_t *)(d + off_offs);
+    m->tiles.p = (AttnTile *)(d + off_tiles);
+    HIP_TRY(hipMemcpyAsync(d, h, used, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipEventRecord(m->ev_meta, s));
     return SVL_OK;
 }
 
@@ -1131,14 +1173,12 @@ svl_status svl_text_forward_device(svl_text_model *m, const uint32_t *d_ids,
     if (batch == 0) return SVL_OK;
     for (int r = 0; r < batch; ++r)
         ST_TRY(validate_row(m, r, nullptr, offsets[r + 1] - offsets[r]));
-    HIP_TRY(m->dims.ensure(n_dims));
     hipStream_t s = stream ? (hipStream_t)stream : m->stream;
-    HIP_TRY(hipMemcpyAsync(m->dims.p, dims, n_dims * 4, hipMemcpyHostToDevice, s));
     for (const auto &pr : row_passes(m, offsets, batch)) {
         Batch b;
         ST_TRY(prepare_batch(m, offsets, pr.first, pr.second, b));
         ST_TRY(ensure_workspace(m, b, 0, false, dims_total));
-        ST_TRY(upload_batch_meta(m, b, s));
+        ST_TRY(upload_batch_meta(m, b, s, dims, n_dims));
         ST_TRY(enqueue_forward(m, b, s, d_ids + offsets[pr.first], nullptr, nullptr, m->dims.p,
                                n_dims, dims_total, d_out + (size_t)pr.first * dims_total,
                                nullptr));
