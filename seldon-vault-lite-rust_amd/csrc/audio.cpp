@@ -63,6 +63,12 @@ struct AuLayer {
     float *norm_pre_attn = nullptr, *norm_post_attn = nullptr, *norm_out = nullptr;
 };
 
+// Typed view into the model's metadata block (set by upload_au_meta).
+template <typename T>
+struct AuView {
+    T *p = nullptr;
+};
+
 }  // namespace
 
 struct svl_audio_model {
@@ -76,11 +82,20 @@ struct svl_audio_model {
     std::vector<AuLayer> layers;
     // workspace
     DevBuf<float> mel, l0, l1, h, n, tmp, act, qkv, att, gated, proj, projn, soft;
-    DevBuf<uint8_t> mask, mask0, mask1;
-    DevBuf<SscpRow> rows0, rows1;
-    DevBuf<int32_t> pos, rowlen, valid_idx, att_blocks;
-    DevBuf<int64_t> offsets;
-    DevBuf<int> flag;
+    DevBuf<int32_t> pos, rowlen;
+    // A pass's metadata in one device block, filled by one copy from pinned
+    // host memory: the error flag, the frame mask, the subsampling masks and
+    // rows, the valid-token index, the attention blocks and the row offsets
+    // (the views below). Every pass of a call has its own staging region.
+    DevBuf<unsigned char> meta;
+    unsigned char *h_meta = nullptr;  // pinned staging
+    size_t h_meta_n = 0;
+    hipEvent_t ev_meta = nullptr;     // after the last copy out of h_meta
+    AuView<int> flag;
+    AuView<uint8_t> mask, mask0, mask1;
+    AuView<SscpRow> rows0, rows1;
+    AuView<int32_t> valid_idx, att_blocks;
+    AuView<int64_t> offsets;
     int *h_flag = nullptr;
     hipStream_t stream = nullptr;
     svl_log_mel *lm = nullptr;  // log-mel tables, created by the first sample call
@@ -92,9 +107,12 @@ struct svl_audio_model {
         for (float *p : allocations) (void)hipFree(p);
         mel.release(); l0.release(); l1.release(); h.release(); n.release(); tmp.release();
         act.release(); qkv.release(); att.release(); gated.release(); proj.release();
-        projn.release(); soft.release(); mask.release(); mask0.release(); mask1.release();
-        rows0.release(); rows1.release(); pos.release(); rowlen.release(); valid_idx.release();
-        att_blocks.release(); offsets.release(); flag.release();
+        projn.release(); soft.release(); pos.release(); rowlen.release(); meta.release();
+        if (ev_meta) {
+            (void)hipEventSynchronize(ev_meta);
+            (void)hipEventDestroy(ev_meta);
+        }
+        if (h_meta) (void)hipHostFree(h_meta);
         if (h_flag) (void)hipHostFree(h_flag);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -344,11 +362,12 @@ bool au_pass_fits(const svl_audio_model *m, int64_t t0) {
     return t0 * FREQ0 * m->C0 * 4 < 0x7FFFFFF0;
 }
 
+size_t au_meta_layout(const AuBatch &b, size_t off[9]);
+
 svl_status ensure_au_workspace(svl_audio_model *m, const AuBatch &b) {
     const int64_t F = std::max<int64_t>(b.F, 1), T0 = std::max<int64_t>(b.T0, 1),
                   T = std::max<int64_t>(b.T, 1), N = std::max<int64_t>(b.tokens, 1);
     HIP_TRY(m->mel.ensure(F * FEATURE_SIZE));
-    HIP_TRY(m->mask.ensure(F));
     HIP_TRY(m->l0.ensure(T0 * FREQ0 * m->C0));
     HIP_TRY(m->l1.ensure(T * FREQ1 * m->C1));
     HIP_TRY(m->h.ensure(T * m->H));
@@ -361,33 +380,75 @@ svl_status ensure_au_workspace(svl_audio_model *m, const AuBatch &b) {
     HIP_TRY(m->proj.ensure(T * m->P));
     HIP_TRY(m->projn.ensure(N * m->P));
     HIP_TRY(m->soft.ensure(N * m->text_hidden));
-    HIP_TRY(m->mask0.ensure(T0));
-    HIP_TRY(m->mask1.ensure(T));
-    HIP_TRY(m->rows0.ensure(T0));
-    HIP_TRY(m->rows1.ensure(T));
     HIP_TRY(m->pos.ensure(T));
     HIP_TRY(m->rowlen.ensure(T));
-    HIP_TRY(m->valid_idx.ensure(N));
-    HIP_TRY(m->att_blocks.ensure(std::max<size_t>(b.att_blocks.size(), 1)));
-    HIP_TRY(m->offsets.ensure((size_t)b.B + 1));
-    HIP_TRY(m->flag.ensure(1));
+    size_t off[9];
+    HIP_TRY(m->meta.ensure(au_meta_layout(b, off)));
     return SVL_OK;
 }
 
-svl_status upload_au_meta(svl_audio_model *m, const AuBatch &b, hipStream_t s, bool reset_flag) {
-    HIP_TRY(hipMemcpyAsync(m->rows0.p, b.rows0.data(), b.rows0.size() * sizeof(SscpRow),
-                           hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(m->rows1.p, b.rows1.data(), b.rows1.size() * sizeof(SscpRow),
-                           hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(m->mask0.p, b.mask0.data(), b.mask0.size(), hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(m->mask1.p, b.mask1.data(), b.mask1.size(), hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(m->valid_idx.p, b.valid_idx.data(), b.valid_idx.size() * 4,
-                           hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(m->att_blocks.p, b.att_blocks.data(), b.att_blocks.size() * 4,
-                           hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(m->offsets.p, b.row_off.data(), b.row_off.size() * 8,
-                           hipMemcpyHostToDevice, s));
-    if (reset_flag) HIP_TRY(hipMemsetAsync(m->flag.p, 0, sizeof(int), s));
+// Byte offsets in a pass's metadata block (each array 256-byte aligned):
+// flag, frame mask, mask0, mask1, rows0, rows1, valid_idx, att_blocks,
+// offsets; returns the block's size.
+size_t au_meta_layout(const AuBatch &b, size_t off[9]) {
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t bytes[9] = {sizeof(int), (size_t)b.F, b.mask0.size(), b.mask1.size(),
+                             b.rows0.size() * sizeof(SscpRow), b.rows1.size() * sizeof(SscpRow),
+                             b.valid_idx.size() * 4, b.att_blocks.size() * 4,
+                             b.row_off.size() * 8};
+    size_t at = 0;
+    for (int i = 0; i < 9; ++i) {
+        off[i] = at;
+        at += up(std::max<size_t>(bytes[i], 1));
+    }
+    return at;
+}
+
+// Pinned staging for the passes of one call, `bytes` in all; waits for the
+// copies of the call before out of it.
+svl_status au_staging(svl_audio_model *m, size_t bytes) {
+    if (m->ev_meta) HIP_TRY(hipEventSynchronize(m->ev_meta));
+    else HIP_TRY(hipEventCreateWithFlags(&m->ev_meta, hipEventDisableTiming));
+    if (m->h_meta_n >= bytes) return SVL_OK;
+    if (m->h_meta) HIP_TRY(hipHostFree(m->h_meta));
+    m->h_meta = nullptr;
+    m->h_meta_n = 0;
+    HIP_TRY(hipHostMalloc((void **)&m->h_meta, bytes, hipHostMallocDefault));
+    m->h_meta_n = bytes;
+    return SVL_OK;
+}
+
+// One pass's metadata (the frame masks of its clips `mels`, the batch
+// layout, the flag cleared on the first pass only, so a later pass keeps an
+// earlier one's error) through its staging region at `stage` by one copy.
+svl_status upload_au_meta(svl_audio_model *m, const AuBatch &b, const svl_mel *mels, hipStream_t s,
+                          bool reset_flag, size_t stage) {
+    size_t off[9];
+    const size_t total = au_meta_layout(b, off);
+    unsigned char *h = m->h_meta + stage, *d = m->meta.p;
+    std::memset(h, 0, total);
+    for (int32_t i = 0; i < b.B; ++i)
+        if (mels[i].frames > 0)
+            std::memcpy(h + off[1] + b.frame_off[(size_t)i], mels[i].mask, (size_t)mels[i].frames);
+    std::memcpy(h + off[2], b.mask0.data(), b.mask0.size());
+    std::memcpy(h + off[3], b.mask1.data(), b.mask1.size());
+    std::memcpy(h + off[4], b.rows0.data(), b.rows0.size() * sizeof(SscpRow));
+    std::memcpy(h + off[5], b.rows1.data(), b.rows1.size() * sizeof(SscpRow));
+    std::memcpy(h + off[6], b.valid_idx.data(), b.valid_idx.size() * 4);
+    std::memcpy(h + off[7], b.att_blocks.data(), b.att_blocks.size() * 4);
+    std::memcpy(h + off[8], b.row_off.data(), b.row_off.size() * 8);
+    m->flag.p = (int *)d;
+    m->mask.p = d + off[1];
+    m->mask0.p = d + off[2];
+    m->mask1.p = d + off[3];
+    m->rows0.p = (SscpRow *)(d + off[4]);
+    m->rows1.p = (SscpRow *)(d + off[5]);
+    m->valid_idx.p = (int32_t *)(d + off[6]);
+    m->att_blocks.p = (int32_t *)(d + off[7]);
+    m->offsets.p = (int64_t *)(d + off[8]);
+    const size_t from = reset_flag ? 0 : off[1];
+    HIP_TRY(hipMemcpyAsync(d + from, h + from, total - from, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipEventRecord(m->ev_meta, s));
     return SVL_OK;
 }
 
@@ -596,6 +657,14 @@ svl_status run_audio(svl_audio_model *m, const svl_mel *mels, int32_t batch,
     // while an earlier pass still reads it
     for (size_t g = 0; g < passes; ++g) ST_TRY(ensure_au_workspace(m, passes > 1 ? parts[g] : b));
     HIP_TRY(m->soft.ensure((size_t)std::max<int64_t>(b.tokens, 1) * m->text_hidden));
+    // each pass's metadata has its own staging region: the passes are
+    // enqueued back to back, so no region is rewritten before its copy ran
+    std::vector<size_t> stage(passes + 1, 0);
+    for (size_t g = 0; g < passes; ++g) {
+        size_t off[9];
+        stage[g + 1] = stage[g] + au_meta_layout(passes > 1 ? parts[g] : b, off);
+    }
+    ST_TRY(au_staging(m, stage[passes]));
     std::vector<std::vector<float>> cap_sscp(passes), cap_hidden(passes);
     int64_t tok_off = 0;
     for (size_t g = 0; g < passes; ++g) {
@@ -605,15 +674,12 @@ svl_status run_audio(svl_audio_model *m, const svl_mel *mels, int32_t batch,
                                         : m->mel.p;
         for (int32_t i = 0; i < nc; ++i) {
             const svl_mel &mel = mels[c0 + i];
-            if (mel.frames <= 0) continue;
-            if (!d_features)
-                HIP_TRY(hipMemcpyAsync(m->mel.p + pb.frame_off[(size_t)i] * FEATURE_SIZE,
-                                       mel.features, (size_t)(mel.frames * FEATURE_SIZE) * 4,
-                                       hipMemcpyHostToDevice, s));
-            HIP_TRY(hipMemcpyAsync(m->mask.p + pb.frame_off[(size_t)i], mel.mask,
-                                   (size_t)mel.frames, hipMemcpyHostToDevice, s));
+            if (mel.frames <= 0 || d_features) continue;
+            HIP_TRY(hipMemcpyAsync(m->mel.p + pb.frame_off[(size_t)i] * FEATURE_SIZE,
+                                   mel.features, (size_t)(mel.frames * FEATURE_SIZE) * 4,
+                                   hipMemcpyHostToDevice, s));
         }
-        ST_TRY(upload_au_meta(m, pb, s, g == 0));
+        ST_TRY(upload_au_meta(m, pb, mels + c0, s, g == 0, stage[g]));
         if (out_sscp) cap_sscp[g].resize((size_t)(pb.T * m->H));
         if (out_hidden) cap_hidden[g].resize((size_t)(m->L * pb.T * m->H));
         ST_TRY(enqueue_audio(m, pb, feats, s, m->soft.p + tok_off * m->text_hidden,
