@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -64,10 +65,26 @@ struct svl_vision_model {
     int64_t n_coord = 0;
     // workspace
     DevBuf<float> pix, h, n, tmp, qkv, attn, act, pooled, soft;
-    DevBuf<int32_t> coord, apos, rowlen, bin_start, bin_patch;
-    DevBuf<int64_t> offsets;
-    DevBuf<AttnTile> tiles;
-    DevBuf<int> flag;
+    DevBuf<int32_t> apos, rowlen;
+    // A call's metadata in one device block, filled by one copy from pinned
+    // host memory: the error flag (cleared), the patch coordinates, the
+    // pooling bins, the image offsets and the attention work items.
+    DevBuf<unsigned char> meta;
+    unsigned char *h_meta = nullptr;  // pinned staging of `meta`
+    size_t h_meta_n = 0;
+    hipEvent_t ev_meta = nullptr;     // after the last copy out of h_meta
+    struct {
+        int *p = nullptr;
+    } flag;
+    struct {
+        int32_t *p = nullptr;
+    } coord, bin_start, bin_patch;
+    struct {
+        int64_t *p = nullptr;
+    } offsets;
+    struct {
+        AttnTile *p = nullptr;
+    } tiles;
     int *h_flag = nullptr;
     hipStream_t stream = nullptr;
     // image groups: the encoder layers of the second group run on `extra`
@@ -83,8 +100,12 @@ struct svl_vision_model {
         cos_t.release(); sin_t.release();
         pix.release(); h.release(); n.release(); tmp.release(); qkv.release(); attn.release();
         act.release(); pooled.release(); soft.release();
-        coord.release(); apos.release(); rowlen.release(); bin_start.release();
-        bin_patch.release(); offsets.release(); tiles.release(); flag.release();
+        apos.release(); rowlen.release(); meta.release();
+        if (ev_meta) {
+            (void)hipEventSynchronize(ev_meta);
+            (void)hipEventDestroy(ev_meta);
+        }
+        if (h_meta) (void)hipHostFree(h_meta);
         if (h_flag) (void)hipHostFree(h_flag);
         if (stream) (void)hipStreamDestroy(stream);
         if (extra) (void)hipStreamDestroy(extra);
@@ -364,29 +385,50 @@ svl_status ensure_vis_workspace(svl_vision_model *v, const VisBatch &b) {
     HIP_TRY(v->act.ensure(T * v->I));
     HIP_TRY(v->pooled.ensure(S * v->H));
     HIP_TRY(v->soft.ensure(S * v->text_hidden));
-    HIP_TRY(v->coord.ensure(2 * T));
     HIP_TRY(v->apos.ensure(T));
     HIP_TRY(v->rowlen.ensure(T));
-    HIP_TRY(v->bin_start.ensure(S + 1));
-    HIP_TRY(v->bin_patch.ensure(T));
-    HIP_TRY(v->offsets.ensure((size_t)b.B + 1));
-    HIP_TRY(v->tiles.ensure(std::max<size_t>(b.tiles.size(), 1)));
-    HIP_TRY(v->flag.ensure(1));
     return SVL_OK;
 }
 
+// The call's metadata (flag cleared, patch coordinates, pooling bins, image
+// offsets, attention work items) staged in pinned host memory and sent by
+// one copy on `s` instead of a copy or fill per array. The staging is
+// rewritten only once the copy before has left it.
 svl_status upload_vis_meta(svl_vision_model *v, const VisBatch &b, hipStream_t s) {
-    HIP_TRY(hipMemcpyAsync(v->coord.p, b.coord.data(), b.coord.size() * 4, hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(v->bin_start.p, b.bin_start.data(), b.bin_start.size() * 4,
-                           hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(v->bin_patch.p, b.bin_patch.data(), b.bin_patch.size() * 4,
-                           hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemcpyAsync(v->offsets.p, b.offsets.data(), b.offsets.size() * 8,
-                           hipMemcpyHostToDevice, s));
-    if (!b.tiles.empty())
-        HIP_TRY(hipMemcpyAsync(v->tiles.p, b.tiles.data(), b.tiles.size() * sizeof(AttnTile),
-                               hipMemcpyHostToDevice, s));
-    HIP_TRY(hipMemsetAsync(v->flag.p, 0, sizeof(int), s));
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t bytes[6] = {sizeof(int), b.coord.size() * 4, b.bin_start.size() * 4,
+                             b.bin_patch.size() * 4, b.offsets.size() * 8,
+                             b.tiles.size() * sizeof(AttnTile)};
+    size_t off[6], total = 0;
+    for (int i = 0; i < 6; ++i) {
+        off[i] = total;
+        total += up(std::max<size_t>(bytes[i], 1));
+    }
+    HIP_TRY(v->meta.ensure(total));
+    if (v->ev_meta) HIP_TRY(hipEventSynchronize(v->ev_meta));
+    else HIP_TRY(hipEventCreateWithFlags(&v->ev_meta, hipEventDisableTiming));
+    if (v->h_meta_n < total) {
+        if (v->h_meta) HIP_TRY(hipHostFree(v->h_meta));
+        v->h_meta = nullptr;
+        v->h_meta_n = 0;
+        HIP_TRY(hipHostMalloc((void **)&v->h_meta, total, hipHostMallocDefault));
+        v->h_meta_n = total;
+    }
+    unsigned char *h = v->h_meta, *d = v->meta.p;
+    std::memset(h, 0, total);
+    std::memcpy(h + off[1], b.coord.data(), bytes[1]);
+    std::memcpy(h + off[2], b.bin_start.data(), bytes[2]);
+    std::memcpy(h + off[3], b.bin_patch.data(), bytes[3]);
+    std::memcpy(h + off[4], b.offsets.data(), bytes[4]);
+    if (bytes[5]) std::memcpy(h + off[5], b.tiles.data(), bytes[5]);
+    v->flag.p = (int *)d;
+    v->coord.p = (int32_t *)(d + off[1]);
+    v->bin_start.p = (int32_t *)(d + off[2]);
+    v->bin_patch.p = (int32_t *)(d + off[3]);
+    v->offsets.p = (int64_t *)(d + off[4]);
+    v->tiles.p = (AttnTile *)(d + off[5]);
+    HIP_TRY(hipMemcpyAsync(d, h, total, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipEventRecord(v->ev_meta, s));
     return SVL_OK;
 }
 
