@@ -125,7 +125,10 @@ svl_status select_top(svl_vector_index *ix, int32_t nq, int64_t offset, int64_t 
     HIP_TRY(ix->cand_idx_alt.ensure((size_t)(nq * cap)));
     HIP_TRY(ix->cnt.ensure((size_t)nq));
     HIP_TRY(ix->blk_count.ensure((size_t)nq * (size_t)candidate_blocks(n)));
-    HIP_TRY(sort_samples(ix->keys.p, nq, n, ix->samples.p, s));
+    if (nq <= SELECT_SAMPLE_MAX_QUERIES)
+        HIP_TRY(select_sample(ix->keys.p, nq, n, rank, ix->samples.p, s));
+    else
+        HIP_TRY(sort_samples(ix->keys.p, nq, n, ix->samples.p, s));
     HIP_TRY(launch_compact_keys(ix->keys.p, nq, n, ix->samples.p, S, rank, cap, ix->blk_count.p,
                                 ix->cnt.p, ix->cand_key.p, ix->cand_idx.p, s));
     std::vector<unsigned int> cnt((size_t)nq);

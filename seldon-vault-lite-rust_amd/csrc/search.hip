@@ -639,11 +639,69 @@ __global__ __launch_bounds__(256) void segment_bounds_kernel(const unsigned int 
     end[q] = (unsigned int)(q * cap + min((int64_t)cnt[q], cap));
 }
 
+// For a few queries, the one sample the candidate passes read (rank `rank`
+// of the ascending order, written to sorted[q * SAMPLE_COUNT + rank]) by
+// counting instead of sorting: block (c, q) takes samples 64 c .. 64 c + 63
+// of query q, one per lane; wave w of its eight counts the samples j of its
+// eighth [512 w, 512 w + 512) below the lane's sample (ties by position),
+// and the sample whose eight counts sum to `rank` is the one sorted order
+// puts there. 64 blocks per query spread over the CUs, where the sort is one
+// block's chain of compare-exchange stages. Every thread loads its eight
+// samples before storing any, and the count reads two samples per LDS read,
+// eight reads in flight.
+constexpr int SELECT_WAVES = 8;
+__global__ __launch_bounds__(64 * SELECT_WAVES) void select_sample_kernel(const uint64_t *keys,
+                                                                          int64_t n, int64_t stride,
+                                                                          int rank,
+                                                                          uint64_t *sorted) {
+    constexpr int THREADS = 64 * SELECT_WAVES, PER_THREAD = SAMPLE_COUNT / THREADS;
+    constexpr int SPAN = SAMPLE_COUNT / SELECT_WAVES;
+    __shared__ __align__(16) uint64_t ls[SAMPLE_COUNT];
+    __shared__ int part[SELECT_WAVES][64];
+    const int q = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const uint64_t *kq = keys + (int64_t)q * n;
+    uint64_t r[PER_THREAD];
+#pragma unroll
+    for (int e = 0; e < PER_THREAD; ++e) r[e] = kq[(int64_t)(t + e * THREADS) * stride];
+#pragma unroll
+    for (int e = 0; e < PER_THREAD; ++e) ls[t + e * THREADS] = r[e];
+    __syncthreads();
+    const int me = (int)blockIdx.x * 64 + lane;
+    const uint64_t v = ls[me];
+    const int j0 = w * SPAN;
+    const ulonglong2 *l2 = reinterpret_cast<const ulonglong2 *>(ls + j0);
+    int below = 0;
+#pragma unroll 8
+    for (int i = 0; i < SPAN / 2; ++i) {
+        const ulonglong2 u = l2[i];
+        const int j = j0 + 2 * i;
+        below += (int)((u.x < v) | ((u.x == v) & (j < me)));
+        below += (int)((u.y < v) | ((u.y == v) & (j + 1 < me)));
+    }
+    part[w][lane] = below;
+    __syncthreads();
+    if (w == 0) {
+        int total = 0;
+#pragma unroll
+        for (int k = 0; k < SELECT_WAVES; ++k) total += part[k][lane];
+        if (total == rank) sorted[(int64_t)q * SAMPLE_COUNT + rank] = v;
+    }
+}
+
 hipError_t sort_samples(const uint64_t *keys, int nq, int64_t n, uint64_t *sorted,
                         hipStream_t s) {
     if (nq <= 0) return hipSuccess;
     hipLaunchKernelGGL(sort_samples_kernel, dim3((unsigned)nq), dim3(1024), 0, s, keys, n,
                        n / SAMPLE_COUNT, sorted);
+    return hipGetLastError();
+}
+
+hipError_t select_sample(const uint64_t *keys, int nq, int64_t n, int rank, uint64_t *sorted,
+                         hipStream_t s) {
+    if (nq <= 0) return hipSuccess;
+    if (rank < 0 || rank >= SAMPLE_COUNT) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(select_sample_kernel, dim3(SAMPLE_COUNT / 64, (unsigned)nq),
+                       dim3(64 * SELECT_WAVES), 0, s, keys, n, n / SAMPLE_COUNT, rank, sorted);
     return hipGetLastError();
 }
 

@@ -321,6 +321,11 @@ hipError_t rank_sort(const uint64_t *keys, uint64_t *keys_alt, uint32_t *idx, ui
 constexpr int SAMPLE_COUNT = 4096;
 hipError_t sort_samples(const uint64_t *keys, int nq, int64_t n, uint64_t *sorted,
                         hipStream_t s);
+// Only the sample of rank `rank` (into sorted[q * SAMPLE_COUNT + rank]), by
+// counting; the faster choice up to SELECT_SAMPLE_MAX_QUERIES queries.
+constexpr int SELECT_SAMPLE_MAX_QUERIES = 4;
+hipError_t select_sample(const uint64_t *keys, int nq, int64_t n, int rank, uint64_t *sorted,
+                         hipStream_t s);
 // blk_count: candidate_blocks(n) * nq counters.
 int candidate_blocks(int64_t n);
 hipError_t launch_compact_keys(const uint64_t *keys, int nq, int64_t n,

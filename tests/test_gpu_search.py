@@ -189,3 +189,8 @@ def test_top_k_selection_path():
         for q in range(6):
             check_query(ix, emb, ids, qs[q], got[q], mask=masks[q], offset=offset, limit=limit,
                         label=f"query {q} page ({offset}, {limit})")
+            # one query alone takes the threshold by counting instead of the
+            # sample sort of the 6-query call: the same page, bit for bit
+            one = ix.rank(qs[q:q + 1], masks=masks[q:q + 1], offset=offset, limit=limit)[0]
+            assert np.array_equal(one[0], got[q][0]), f"query {q} alone ({offset}, {limit})"
+            assert np.array_equal(one[1].view(np.uint64), got[q][1].view(np.uint64))
