@@ -194,3 +194,9 @@ def test_top_k_selection_path():
             one = ix.rank(qs[q:q + 1], masks=masks[q:q + 1], offset=offset, limit=limit)[0]
             assert np.array_equal(one[0], got[q][0]), f"query {q} alone ({offset}, {limit})"
             assert np.array_equal(one[1].view(np.uint64), got[q][1].view(np.uint64))
+        # three and four queries count too, one block row per query
+        for k in (3, 4):
+            few = ix.rank(qs[:k], masks=masks[:k], offset=offset, limit=limit)
+            for q in range(k):
+                assert np.array_equal(few[q][0], got[q][0]), f"{k} queries, query {q}"
+                assert np.array_equal(few[q][1].view(np.uint64), got[q][1].view(np.uint64))
